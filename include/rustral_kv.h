@@ -1,0 +1,156 @@
+/*
+ * rustral_kv.h -- C ABI of the MI355X (gfx950) paged-KV library
+ * librustral_kv.so.
+ *
+ * This is the drop-in boundary under rustral's KV-cache and attention
+ * interfaces.  rustral's own CPU path for these operations is a stub
+ * (crates/nn/src/kv_cache.rs:172-243, :381-432); each entry point below
+ * names the reference interface it stands in for.
+ *
+ * Conventions shared by every entry point
+ *  - All pointers are DEVICE pointers unless marked "host".  Nothing is
+ *    freed or kept: the caller owns every buffer.
+ *  - stream: an opaque hipStream_t (NULL = the default stream).  Work is
+ *    enqueued asynchronously; nothing synchronizes.
+ *  - Return value: RKV_OK (0) or a negative RKV_ERR_* code.  The message of
+ *    the last failure on the calling thread is rkv_last_error().  Argument
+ *    errors are detected on the host before any launch.  Entries the host
+ *    cannot see (block ids, slots, context lengths) are range-checked on the
+ *    device and out-of-range entries are skipped, never dereferenced.
+ *  - KV pool layout, one pool per layer and per K/V:
+ *        pool[num_blocks][num_kv_heads][block_size][head_dim]
+ *    dtype RKV_F32 (float) or RKV_BF16 (bf16 bits; fp32 -> bf16 rounds to
+ *    nearest even, NaN stays NaN).  Token position p of a sequence is row
+ *    p % block_size of block block_table[p / block_size].
+ *  - GQA: query head h reads KV head h / (num_q_heads / num_kv_heads).
+ *  - Supported shapes: head_dim in {32, 64, 128}, block_size 16,
+ *    num_q_heads / num_kv_heads in {1, 2, 4, 8} (append/gather/copy accept
+ *    any head_dim that is a multiple of 8).
+ */
+#ifndef RUSTRAL_KV_H
+#define RUSTRAL_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RKV_F32 0
+#define RKV_BF16 1
+
+#define RKV_OK 0
+#define RKV_ERR_INVALID_ARG (-1) /* maps to CoreError::InvalidArgument / Shape */
+#define RKV_ERR_UNSUPPORTED (-2) /* shape/dtype combination not built     */
+#define RKV_ERR_WORKSPACE (-3)   /* workspace missing or too small         */
+#define RKV_ERR_HIP (-4)         /* HIP launch/runtime error -> Backend(msg) */
+
+/* Thread-local message of the last failed call ("" if none).  Stands in for
+ * the String payload of CoreError (crates/core/src/error.rs:8-46). */
+const char* rkv_last_error(void);
+
+/* ABI version, major*10000 + minor*100 + patch. */
+int rkv_version(void);
+
+/* Append new K/V rows into paged pools.
+ * Replaces KVCache::append (crates/nn/src/kv_cache.rs:172-216), which
+ * intends to write new_k/new_v [batch, Hkv, T, D] at positions
+ * current_len..current_len+T but writes nothing.
+ *
+ * For layer l < n_layers, token t < n_tokens, head h, dim d:
+ *   src = k_new + l*src_layer_stride + t*src_tok_stride + h*src_head_stride + d
+ *   dst = k_pool + l*pool_layer_stride + ((blk*Hkv + h)*block_size + row)*head_dim + d
+ * with slot_mapping[t] = blk*block_size + row (int64, shared by all layers).
+ * Strides are in elements; src strides must be multiples of 4 and src
+ * pointers 16-byte aligned.  Slots < 0 (padding) or >= num_blocks*block_size
+ * are skipped.  One launch covers every layer. */
+int rkv_append(void* k_pool, void* v_pool, int64_t pool_layer_stride, const float* k_new,
+               const float* v_new, int64_t src_layer_stride, int64_t src_tok_stride,
+               int64_t src_head_stride, const int64_t* slot_mapping, int64_t n_tokens,
+               int n_layers, int num_kv_heads, int head_dim, int block_size,
+               int64_t num_blocks, int dtype, void* stream);
+
+/* Gather each sequence's K/V into the contiguous KVCache layout.
+ * Replaces KVCache::get_range / k_cache / v_cache
+ * (crates/nn/src/kv_cache.rs:219-243), whose layout is
+ * [batch, Hkv, seq, D] (kv_cache.rs:139-142).
+ * Sequence b (L_b = ctx_lens[b], clamped to max_blocks_per_seq*block_size)
+ * is written to
+ *   out_offsets == NULL: out[b][h][p][d] with shape [num_seqs, Hkv, max_ctx, D]
+ *                        (rejected on the device side if L_b > max_ctx: rows
+ *                        p >= max_ctx are not written)
+ *   out_offsets != NULL: out + out_offsets[b] + (h*L_b + p)*D + d  (packed)
+ * Only tokens p < L_b are written.  out_dtype is dtype (bit copy) or RKV_F32
+ * (exact bf16 -> fp32 upcast).  Blocks with an id outside [0, num_blocks)
+ * are skipped. */
+int rkv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+               const int32_t* block_tables, int max_blocks_per_seq, const int32_t* ctx_lens,
+               const int64_t* out_offsets, int num_seqs, int num_kv_heads, int head_dim,
+               int block_size, int64_t num_blocks, int max_ctx, int dtype, int out_dtype,
+               void* stream);
+
+/* Copy whole blocks (all heads, all rows) inside every layer's K and V pool:
+ * for l < n_layers, i < n_pairs: block pairs[2i+1] := block pairs[2i].
+ * No reference counterpart: PagedCache only allocates and frees block ids
+ * (crates/nn/src/kv_cache.rs:413-431) and eviction is a free
+ * (crates/nn/src/continuous_batching.rs:380-386).  This is the compaction
+ * step of continuous batching.  block_bytes = Hkv*block_size*head_dim*elem
+ * (multiple of 16); layer l's pool starts at pool + l*layer_stride_bytes.
+ * The set of destinations must not intersect the set of sources within one
+ * call (results are then independent of execution order). */
+int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int n_layers,
+                    const int32_t* pairs, int n_pairs, int64_t block_bytes, int64_t num_blocks,
+                    void* stream);
+
+/* Workspace (bytes) rkv_decode_attention needs for split-K partials.
+ * max_context: host-side upper bound on every ctx_lens[b] (for example
+ * max_blocks_per_seq*block_size).  partition_size <= 0 picks the default. */
+size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_context,
+                                  int partition_size);
+
+/* Partition size (tokens) rkv_decode_attention uses for a request of
+ * partition_size (<= 0: the library default). */
+int rkv_decode_partition_size(int partition_size, int head_dim, int dtype);
+
+/* Single-token paged decode attention with GQA (two passes: partitions of
+ * partition_size tokens, then a merge; one partition skips the merge).
+ * Replaces the per-head recipe of TapeMultiHeadAttention
+ * (crates/nn/src/tape_transformer.rs:87-139), for one query token per
+ * sequence attending to its whole cache, and AttentionOps
+ * (crates/core/src/backend.rs:551-602), which has no block tables.
+ *   out[b][h][:] = softmax_j((q[b][h] . K[b][kv(h)][j]) * scale) @ V[b][kv(h)][j]
+ * q, out: [num_seqs, num_q_heads, head_dim] fp32.  Accumulation is fp32.
+ * block_tables: [num_seqs, max_blocks_per_seq] int32; ctx_lens: [num_seqs].
+ * L_b <= 0 gives a zero row.  max_context is the host-side upper bound used
+ * to size the grid (<= max_blocks_per_seq*block_size).
+ * workspace: >= rkv_decode_workspace_bytes(...) bytes, may be NULL when
+ * max_context <= partition size. */
+int rkv_decode_attention(float* out, const float* q, const void* k_pool, const void* v_pool,
+                         const int32_t* block_tables, int max_blocks_per_seq,
+                         const int32_t* ctx_lens, int num_seqs, int num_q_heads,
+                         int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                         int max_context, float scale, int dtype, int partition_size,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two passes of rkv_decode_attention as separate launches, for callers
+ * that schedule them apart (and for per-kernel timing).  Same arguments;
+ * pass 1 writes finished rows for single-partition sequences and partials
+ * for the rest, pass 2 merges the partials. */
+int rkv_decode_attention_partitions(float* out, const float* q, const void* k_pool,
+                                    const void* v_pool, const int32_t* block_tables,
+                                    int max_blocks_per_seq, const int32_t* ctx_lens,
+                                    int num_seqs, int num_q_heads, int num_kv_heads,
+                                    int head_dim, int block_size, int64_t num_blocks,
+                                    int max_context, float scale, int dtype,
+                                    int partition_size, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens, int max_blocks_per_seq,
+                               int num_seqs, int num_q_heads, int head_dim, int block_size,
+                               int max_context, int dtype, int partition_size,
+                               const void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RUSTRAL_KV_H */

@@ -1,0 +1,472 @@
+/*
+ * rkv_oracle.c -- CPU restatement of rustral's paged-KV hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see rkv_oracle.h): the checker for the HIP
+ * library, never part of the product path.
+ *
+ * Built with -O2 -ffp-contract=off so every float operation is rounded in
+ * program order, like the reference's scalar Rust loops.
+ */
+#include "rkv_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- bf16 -------------------------------------------------------------- */
+
+uint16_t orc_bf16_from_f32(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) /* NaN: keep sign/payload, set quiet bit */
+    return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u); /* round to nearest, ties to even */
+  return (uint16_t)(u >> 16);
+}
+
+float orc_f32_from_bf16(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16; /* as bf16_to_f32, compression.rs:263-267 */
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void orc_bf16_from_f32_array(const float* x, uint16_t* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_bf16_from_f32(x[i]);
+}
+
+void orc_f32_from_bf16_array(const uint16_t* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_from_bf16(x[i]);
+}
+
+static inline float load_elem(const void* pool, int dtype, int64_t idx) {
+  if (dtype == ORC_F32) return ((const float*)pool)[idx];
+  return orc_f32_from_bf16(((const uint16_t*)pool)[idx]);
+}
+
+static inline size_t dtype_size(int dtype) { return dtype == ORC_F32 ? 4 : 2; }
+
+/* ---- append ------------------------------------------------------------ */
+
+int orc_append(void* k_pool, void* v_pool, const float* k_new, const float* v_new,
+               const int64_t* slot_mapping, int64_t n_tokens, int num_kv_heads, int head_dim,
+               int block_size, int64_t num_blocks, int64_t src_tok_stride,
+               int64_t src_head_stride, int pool_dtype) {
+  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping) return -1;
+  if (n_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0) return -1;
+  if (pool_dtype != ORC_F32 && pool_dtype != ORC_BF16) return -1;
+  const int64_t n_slots = num_blocks * block_size;
+  for (int64_t t = 0; t < n_tokens; ++t) {
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0 || slot >= n_slots) continue;
+    const int64_t blk = slot / block_size, row = slot % block_size;
+    for (int h = 0; h < num_kv_heads; ++h) {
+      const int64_t dst = ((blk * num_kv_heads + h) * block_size + row) * head_dim;
+      const int64_t src = t * src_tok_stride + (int64_t)h * src_head_stride;
+      for (int d = 0; d < head_dim; ++d) {
+        if (pool_dtype == ORC_F32) {
+          ((float*)k_pool)[dst + d] = k_new[src + d];
+          ((float*)v_pool)[dst + d] = v_new[src + d];
+        } else {
+          ((uint16_t*)k_pool)[dst + d] = orc_bf16_from_f32(k_new[src + d]);
+          ((uint16_t*)v_pool)[dst + d] = orc_bf16_from_f32(v_new[src + d]);
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* ---- gather ------------------------------------------------------------ */
+
+static inline int clamp_ctx(int L, int max_blocks_per_seq, int block_size) {
+  const int cap = max_blocks_per_seq * block_size;
+  if (L < 0) return 0;
+  return L > cap ? cap : L;
+}
+
+int orc_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+               const int32_t* block_tables, int max_blocks_per_seq, const int32_t* ctx_lens,
+               const int64_t* out_offsets, int num_seqs, int num_kv_heads, int head_dim,
+               int block_size, int64_t num_blocks, int max_ctx, int pool_dtype, int out_dtype) {
+  if (!k_out || !v_out || !k_pool || !v_pool || !block_tables || !ctx_lens) return -1;
+  if (out_dtype != ORC_F32 && out_dtype != pool_dtype) return -1;
+  for (int b = 0; b < num_seqs; ++b) {
+    const int L = clamp_ctx(ctx_lens[b], max_blocks_per_seq, block_size);
+    if (!out_offsets && L > max_ctx) return -1;
+    for (int p = 0; p < L; ++p) {
+      const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + p / block_size];
+      if (blk < 0 || blk >= num_blocks) continue;
+      const int row = p % block_size;
+      for (int h = 0; h < num_kv_heads; ++h) {
+        const int64_t src = (((int64_t)blk * num_kv_heads + h) * block_size + row) * head_dim;
+        int64_t dst;
+        if (out_offsets)
+          dst = out_offsets[b] + ((int64_t)h * L + p) * head_dim;
+        else
+          dst = (((int64_t)b * num_kv_heads + h) * max_ctx + p) * head_dim;
+        if (out_dtype == pool_dtype) {
+          const size_t es = dtype_size(pool_dtype);
+          memcpy((char*)k_out + dst * es, (const char*)k_pool + src * es, head_dim * es);
+          memcpy((char*)v_out + dst * es, (const char*)v_pool + src * es, head_dim * es);
+        } else {
+          for (int d = 0; d < head_dim; ++d) {
+            ((float*)k_out)[dst + d] = load_elem(k_pool, pool_dtype, src + d);
+            ((float*)v_out)[dst + d] = load_elem(v_pool, pool_dtype, src + d);
+          }
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+/* ---- copy_blocks ------------------------------------------------------- */
+
+int orc_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int n_layers,
+                    const int32_t* pairs, int n_pairs, int64_t block_bytes, int64_t num_blocks) {
+  if (!k_pool || !v_pool || (n_pairs > 0 && !pairs) || block_bytes <= 0) return -1;
+  for (int l = 0; l < n_layers; ++l) {
+    char* kp = (char*)k_pool + (int64_t)l * layer_stride_bytes;
+    char* vp = (char*)v_pool + (int64_t)l * layer_stride_bytes;
+    for (int i = 0; i < n_pairs; ++i) {
+      const int32_t src = pairs[2 * i], dst = pairs[2 * i + 1];
+      if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) continue;
+      memmove(kp + (int64_t)dst * block_bytes, kp + (int64_t)src * block_bytes, block_bytes);
+      memmove(vp + (int64_t)dst * block_bytes, vp + (int64_t)src * block_bytes, block_bytes);
+    }
+  }
+  return 0;
+}
+
+/* ---- softmax / argmax -------------------------------------------------- */
+
+void orc_softmax_rows(const float* x, float* y, int rows, int cols) {
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (int64_t)r * cols;
+    float* yr = y + (int64_t)r * cols;
+    float mx = -INFINITY;
+    for (int c = 0; c < cols; ++c) mx = fmaxf(mx, xr[c]);
+    float sum = 0.0f;
+    for (int c = 0; c < cols; ++c) {
+      const float e = expf(xr[c] - mx);
+      yr[c] = e;
+      sum += e;
+    }
+    const float inv = 1.0f / sum;
+    for (int c = 0; c < cols; ++c) yr[c] *= inv;
+  }
+}
+
+int64_t orc_argmax(const float* x, int64_t n) {
+  if (n <= 0) return -1;
+  /* max_by keeps the later element when the comparison says Equal; NaN
+   * compares Equal through unwrap_or(Equal) (ndarray-backend/src/lib.rs:434). */
+  int64_t best = 0;
+  for (int64_t i = 1; i < n; ++i) {
+    const float a = x[best], b = x[i];
+    const int less = a < b, greater = a > b;
+    if (less || (!less && !greater)) best = i; /* b >= a, or unordered */
+  }
+  return best;
+}
+
+/* ---- decode attention -------------------------------------------------- */
+
+typedef struct {
+  const float* q;
+  const void* k_pool;
+  const void* v_pool;
+  const int32_t* block_tables;
+  const int32_t* ctx_lens;
+  int max_blocks_per_seq, num_q_heads, num_kv_heads, head_dim, block_size, pool_dtype;
+  int64_t num_blocks;
+  float scale;
+} dec_args;
+
+static int check_dec(const float* q, const void* k, const void* v, const int32_t* bt,
+                     const int32_t* cl, int nq, int nkv, int d, int bs) {
+  if (!q || !k || !v || !bt || !cl) return -1;
+  if (nq <= 0 || nkv <= 0 || d <= 0 || bs <= 0 || nq % nkv) return -1;
+  return 0;
+}
+
+/* Row index of token j in the pool for KV head kh, or -1 if its block id is
+ * invalid. */
+static inline int64_t token_row(const dec_args* a, int b, int kh, int j) {
+  const int32_t blk = a->block_tables[(int64_t)b * a->max_blocks_per_seq + j / a->block_size];
+  if (blk < 0 || blk >= a->num_blocks) return -1;
+  return (((int64_t)blk * a->num_kv_heads + kh) * a->block_size + j % a->block_size) *
+         a->head_dim;
+}
+
+/* One (b, h) row in fp32, ndarray op order.  scratch holds L floats. */
+static void decode_one_f32(const dec_args* a, int b, int h, float* out, float* s) {
+  const int D = a->head_dim;
+  const int kh = h / (a->num_q_heads / a->num_kv_heads);
+  const int L = clamp_ctx(a->ctx_lens[b], a->max_blocks_per_seq, a->block_size);
+  const float* qv = a->q + ((int64_t)b * a->num_q_heads + h) * D;
+  for (int d = 0; d < D; ++d) out[d] = 0.0f;
+  if (L == 0) return;
+  float mx = -INFINITY;
+  for (int j = 0; j < L; ++j) {
+    const int64_t r = token_row(a, b, kh, j);
+    if (r < 0) {
+      s[j] = -INFINITY;
+      continue;
+    }
+    float dot = 0.0f; /* matmul: sum += a*b over kk (lib.rs:211-214) */
+    for (int d = 0; d < D; ++d) dot += qv[d] * load_elem(a->k_pool, a->pool_dtype, r + d);
+    s[j] = dot * a->scale; /* mul_scalar (lib.rs:747-756) */
+    mx = fmaxf(mx, s[j]);
+  }
+  if (mx == -INFINITY) return; /* every block id invalid */
+  float sum = 0.0f;
+  for (int j = 0; j < L; ++j) {
+    const float e = (s[j] == -INFINITY) ? 0.0f : expf(s[j] - mx);
+    s[j] = e;
+    sum += e;
+  }
+  const float inv = 1.0f / sum;
+  for (int j = 0; j < L; ++j) s[j] *= inv;
+  /* weights[1,L] @ vh[L,D]: out[d] = sum over j in order (lib.rs:211-214) */
+  for (int j = 0; j < L; ++j) {
+    const int64_t r = token_row(a, b, kh, j);
+    if (r < 0) continue;
+    for (int d = 0; d < D; ++d) out[d] += s[j] * load_elem(a->v_pool, a->pool_dtype, r + d);
+  }
+}
+
+static int max_ctx_of(const int32_t* cl, int B, int mbs, int bs) {
+  int m = 1;
+  for (int b = 0; b < B; ++b) {
+    const int L = clamp_ctx(cl[b], mbs, bs);
+    if (L > m) m = L;
+  }
+  return m;
+}
+
+int orc_decode_attention(float* out, const float* q, const void* k_pool, const void* v_pool,
+                         const int32_t* block_tables, int max_blocks_per_seq,
+                         const int32_t* ctx_lens, int num_seqs, int num_q_heads, int num_kv_heads,
+                         int head_dim, int block_size, int64_t num_blocks, float scale,
+                         int pool_dtype) {
+  if (!out || check_dec(q, k_pool, v_pool, block_tables, ctx_lens, num_q_heads, num_kv_heads,
+                        head_dim, block_size))
+    return -1;
+  dec_args a = {q, k_pool, v_pool, block_tables, ctx_lens, max_blocks_per_seq, num_q_heads,
+                num_kv_heads, head_dim, block_size, pool_dtype, num_blocks, scale};
+  float* s = (float*)malloc(sizeof(float) * max_ctx_of(ctx_lens, num_seqs, max_blocks_per_seq,
+                                                       block_size));
+  if (!s) return -1;
+  for (int b = 0; b < num_seqs; ++b)
+    for (int h = 0; h < num_q_heads; ++h)
+      decode_one_f32(&a, b, h, out + ((int64_t)b * num_q_heads + h) * head_dim, s);
+  free(s);
+  return 0;
+}
+
+int orc_decode_attention_f64(double* out, const float* q, const void* k_pool,
+                             const void* v_pool, const int32_t* block_tables,
+                             int max_blocks_per_seq, const int32_t* ctx_lens, int num_seqs,
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                             int64_t num_blocks, float scale, int pool_dtype) {
+  if (!out || check_dec(q, k_pool, v_pool, block_tables, ctx_lens, num_q_heads, num_kv_heads,
+                        head_dim, block_size))
+    return -1;
+  dec_args a = {q, k_pool, v_pool, block_tables, ctx_lens, max_blocks_per_seq, num_q_heads,
+                num_kv_heads, head_dim, block_size, pool_dtype, num_blocks, scale};
+  double* s = (double*)malloc(sizeof(double) * max_ctx_of(ctx_lens, num_seqs,
+                                                          max_blocks_per_seq, block_size));
+  if (!s) return -1;
+  const int G = num_q_heads / num_kv_heads, D = head_dim;
+  for (int b = 0; b < num_seqs; ++b) {
+    const int L = clamp_ctx(ctx_lens[b], max_blocks_per_seq, block_size);
+    for (int h = 0; h < num_q_heads; ++h) {
+      double* o = out + ((int64_t)b * num_q_heads + h) * D;
+      const float* qv = q + ((int64_t)b * num_q_heads + h) * D;
+      for (int d = 0; d < D; ++d) o[d] = 0.0;
+      double mx = -INFINITY;
+      for (int j = 0; j < L; ++j) {
+        const int64_t r = token_row(&a, b, h / G, j);
+        if (r < 0) {
+          s[j] = -INFINITY;
+          continue;
+        }
+        double dot = 0.0;
+        for (int d = 0; d < D; ++d)
+          dot += (double)qv[d] * (double)load_elem(k_pool, pool_dtype, r + d);
+        s[j] = dot * (double)scale;
+        if (s[j] > mx) mx = s[j];
+      }
+      if (L == 0 || mx == -INFINITY) continue;
+      double sum = 0.0;
+      for (int j = 0; j < L; ++j) {
+        s[j] = (s[j] == -INFINITY) ? 0.0 : exp(s[j] - mx);
+        sum += s[j];
+      }
+      for (int j = 0; j < L; ++j) {
+        const int64_t r = token_row(&a, b, h / G, j);
+        if (r < 0) continue;
+        const double p = s[j] / sum;
+        for (int d = 0; d < D; ++d) o[d] += p * (double)load_elem(v_pool, pool_dtype, r + d);
+      }
+    }
+  }
+  free(s);
+  return 0;
+}
+
+/* ---- split-K ----------------------------------------------------------- */
+
+int orc_decode_partials(float* m, float* l, float* acc, const float* q, const void* k_pool,
+                        const void* v_pool, const int32_t* block_tables, int max_blocks_per_seq,
+                        const int32_t* ctx_lens, int num_seqs, int num_q_heads, int num_kv_heads,
+                        int head_dim, int block_size, int64_t num_blocks, float scale,
+                        int pool_dtype, int partition_size, int max_parts) {
+  if (!m || !l || !acc || partition_size <= 0 ||
+      check_dec(q, k_pool, v_pool, block_tables, ctx_lens, num_q_heads, num_kv_heads, head_dim,
+                block_size))
+    return -1;
+  dec_args a = {q, k_pool, v_pool, block_tables, ctx_lens, max_blocks_per_seq, num_q_heads,
+                num_kv_heads, head_dim, block_size, pool_dtype, num_blocks, scale};
+  const int G = num_q_heads / num_kv_heads, D = head_dim;
+  float* s = (float*)malloc(sizeof(float) * partition_size);
+  if (!s) return -1;
+  for (int b = 0; b < num_seqs; ++b) {
+    const int L = clamp_ctx(ctx_lens[b], max_blocks_per_seq, block_size);
+    const int np = (L + partition_size - 1) / partition_size;
+    if (np > max_parts) {
+      free(s);
+      return -1;
+    }
+    for (int h = 0; h < num_q_heads; ++h) {
+      const float* qv = q + ((int64_t)b * num_q_heads + h) * D;
+      for (int p = 0; p < np; ++p) {
+        const int64_t o = ((int64_t)b * num_q_heads + h) * max_parts + p;
+        const int j0 = p * partition_size;
+        const int j1 = (j0 + partition_size < L) ? j0 + partition_size : L;
+        float mx = -INFINITY;
+        for (int j = j0; j < j1; ++j) {
+          const int64_t r = token_row(&a, b, h / G, j);
+          float v = -INFINITY;
+          if (r >= 0) {
+            float dot = 0.0f;
+            for (int d = 0; d < D; ++d) dot += qv[d] * load_elem(k_pool, pool_dtype, r + d);
+            v = dot * scale;
+          }
+          s[j - j0] = v;
+          mx = fmaxf(mx, v);
+        }
+        float sum = 0.0f;
+        float* ac = acc + o * D;
+        for (int d = 0; d < D; ++d) ac[d] = 0.0f;
+        for (int j = j0; j < j1; ++j) {
+          const float e = (s[j - j0] == -INFINITY) ? 0.0f : expf(s[j - j0] - mx);
+          sum += e;
+          const int64_t r = token_row(&a, b, h / G, j);
+          if (r < 0) continue;
+          for (int d = 0; d < D; ++d) ac[d] += e * load_elem(v_pool, pool_dtype, r + d);
+        }
+        m[o] = mx;
+        l[o] = sum;
+      }
+    }
+  }
+  free(s);
+  return 0;
+}
+
+int orc_splitk_merge(float* out, const float* m, const float* l, const float* acc,
+                     const int32_t* ctx_lens, int max_blocks_per_seq, int block_size,
+                     int num_seqs, int num_q_heads, int head_dim, int partition_size,
+                     int max_parts) {
+  if (!out || !m || !l || !acc || !ctx_lens || partition_size <= 0) return -1;
+  const int D = head_dim;
+  for (int b = 0; b < num_seqs; ++b) {
+    const int L = clamp_ctx(ctx_lens[b], max_blocks_per_seq, block_size);
+    const int np = (L + partition_size - 1) / partition_size;
+    for (int h = 0; h < num_q_heads; ++h) {
+      const int64_t base = ((int64_t)b * num_q_heads + h) * max_parts;
+      float* o = out + ((int64_t)b * num_q_heads + h) * D;
+      float M = -INFINITY;
+      for (int p = 0; p < np; ++p) M = fmaxf(M, m[base + p]);
+      for (int d = 0; d < D; ++d) o[d] = 0.0f;
+      if (np == 0 || M == -INFINITY) continue;
+      float den = 0.0f;
+      for (int p = 0; p < np; ++p) {
+        const float w = (m[base + p] == -INFINITY) ? 0.0f : expf(m[base + p] - M);
+        den += w * l[base + p];
+        for (int d = 0; d < D; ++d) o[d] += w * acc[(base + p) * D + d];
+      }
+      for (int d = 0; d < D; ++d) o[d] /= den;
+    }
+  }
+  return 0;
+}
+
+/* ---- threaded baseline ------------------------------------------------- */
+
+typedef struct {
+  dec_args a;
+  float* out;
+  int num_seqs, next_unit_stride, first_unit, max_ctx;
+} mt_job;
+
+static void* mt_worker(void* p) {
+  mt_job* j = (mt_job*)p;
+  const dec_args* a = &j->a;
+  const int G = a->num_q_heads / a->num_kv_heads;
+  const int units = j->num_seqs * a->num_kv_heads;
+  float* s = (float*)malloc(sizeof(float) * j->max_ctx);
+  if (!s) return (void*)1;
+  for (int u = j->first_unit; u < units; u += j->next_unit_stride) {
+    const int b = u / a->num_kv_heads, kh = u % a->num_kv_heads;
+    for (int g = 0; g < G; ++g) {
+      const int h = kh * G + g;
+      decode_one_f32(a, b, h, j->out + ((int64_t)b * a->num_q_heads + h) * a->head_dim, s);
+    }
+  }
+  free(s);
+  return NULL;
+}
+
+int orc_decode_attention_mt(float* out, const float* q, const void* k_pool, const void* v_pool,
+                            const int32_t* block_tables, int max_blocks_per_seq,
+                            const int32_t* ctx_lens, int num_seqs, int num_q_heads,
+                            int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                            float scale, int pool_dtype, int n_threads) {
+  if (!out || n_threads <= 0 ||
+      check_dec(q, k_pool, v_pool, block_tables, ctx_lens, num_q_heads, num_kv_heads, head_dim,
+                block_size))
+    return -1;
+  if (n_threads > 1024) n_threads = 1024;
+  dec_args a = {q, k_pool, v_pool, block_tables, ctx_lens, max_blocks_per_seq, num_q_heads,
+                num_kv_heads, head_dim, block_size, pool_dtype, num_blocks, scale};
+  const int mc = max_ctx_of(ctx_lens, num_seqs, max_blocks_per_seq, block_size);
+  mt_job* jobs = (mt_job*)calloc(n_threads, sizeof(mt_job));
+  pthread_t* th = (pthread_t*)calloc(n_threads, sizeof(pthread_t));
+  if (!jobs || !th) {
+    free(jobs);
+    free(th);
+    return -1;
+  }
+  int rc = 0;
+  for (int t = 0; t < n_threads; ++t) {
+    jobs[t] = (mt_job){a, out, num_seqs, n_threads, t, mc};
+    if (pthread_create(&th[t], NULL, mt_worker, &jobs[t])) {
+      n_threads = t;
+      rc = -1;
+      break;
+    }
+  }
+  for (int t = 0; t < n_threads; ++t) {
+    void* r = NULL;
+    pthread_join(th[t], &r);
+    if (r) rc = -1;
+  }
+  free(jobs);
+  free(th);
+  return rc;
+}

@@ -1,0 +1,137 @@
+/*
+ * rkv_oracle.h -- CPU restatement of rustral's paged-KV hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the
+ * checker (or the timed CPU baseline).  The product path (rustral_amd,
+ * librustral_kv.so) never links or calls it.
+ *
+ * rustral's own KV path cannot serve as the oracle: KVCache::append writes
+ * nothing (crates/nn/src/kv_cache.rs:197-210), get_range returns the whole
+ * cache (kv_cache.rs:229-243) and PagedCache has no storage
+ * (kv_cache.rs:399-409).  This file restates what those functions are
+ * documented to do, built from the ndarray primitive semantics the reference
+ * composes attention from.  Each function cites the file:line it follows.
+ *
+ * Layout shared with the GPU library (one pool per layer, K and V separate):
+ *     pool[num_blocks][num_kv_heads][block_size][head_dim]
+ * Token position p of a sequence lives in block block_table[p / block_size]
+ * at row p % block_size.  Query head h reads KV head h / (Hq / Hkv).
+ *
+ * Pinning status of every function is listed in oracle/README.md.
+ */
+#ifndef RKV_ORACLE_H
+#define RKV_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_F32 = 0, ORC_BF16 = 1 };
+
+/* fp32 -> bf16 round-to-nearest-even, NaN kept as a quiet NaN of the same
+ * sign.  Deviation from the reference's only converter, which truncates
+ * (crates/distributed/src/compression.rs:256-261). */
+uint16_t orc_bf16_from_f32(float x);
+float orc_f32_from_bf16(uint16_t b);
+void orc_bf16_from_f32_array(const float* x, uint16_t* y, int64_t n);
+void orc_f32_from_bf16_array(const uint16_t* x, float* y, int64_t n);
+
+/* KV append: the write KVCache::append intends (kv_cache.rs:172-216), into
+ * a paged pool.  Token t (0 <= t < n_tokens) of source row
+ * src[t*src_tok_stride + h*src_head_stride + d] goes to flat slot
+ * slot_mapping[t] = block * block_size + row.  Slots < 0 (padding) or
+ * >= num_blocks*block_size are skipped.  Returns 0, or -1 on bad args. */
+int orc_append(void* k_pool, void* v_pool, const float* k_new, const float* v_new,
+               const int64_t* slot_mapping, int64_t n_tokens, int num_kv_heads, int head_dim,
+               int block_size, int64_t num_blocks, int64_t src_tok_stride,
+               int64_t src_head_stride, int pool_dtype);
+
+/* KV gather: the slice KVCache::get_range intends (kv_cache.rs:229-243),
+ * reconstructed through block tables.  Sequence b's K (and V) are written in
+ * the KVCache layout [Hkv, L_b, D] (kv_cache.rs:139-142) at
+ *   out_offsets == NULL : out + (b*Hkv*max_ctx)   with row stride max_ctx
+ *   out_offsets != NULL : out + out_offsets[b]    with row stride L_b
+ * Only tokens < L_b are written; a block id outside [0, num_blocks) leaves
+ * its 16 rows untouched.  out_dtype may be the pool dtype or F32 (exact
+ * upcast of bf16). */
+int orc_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+               const int32_t* block_tables, int max_blocks_per_seq, const int32_t* ctx_lens,
+               const int64_t* out_offsets, int num_seqs, int num_kv_heads, int head_dim,
+               int block_size, int64_t num_blocks, int max_ctx, int pool_dtype, int out_dtype);
+
+/* Block copy for compaction: no reference function exists (PagedCache only
+ * allocates/frees, kv_cache.rs:413-431).  For every layer l and pair i,
+ * block pairs[2i+1] of layer l's pool becomes a copy of block pairs[2i].
+ * Layer l's pool starts at pool + l*layer_stride_bytes.  Pairs with an id
+ * outside [0, num_blocks) are skipped. */
+int orc_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int n_layers,
+                    const int32_t* pairs, int n_pairs, int64_t block_bytes, int64_t num_blocks);
+
+/* Row softmax: CpuOps::softmax_dim on the last axis
+ * (crates/ndarray-backend/src/lib.rs:1188-1227): max, exp(x-max), serial sum,
+ * multiply by 1/sum. */
+void orc_softmax_rows(const float* x, float* y, int rows, int cols);
+
+/* Greedy argmax: last index among equal maxima, as Iterator::max_by in
+ * CpuOps::argmax (ndarray-backend/src/lib.rs:430-437) and Sampler::greedy
+ * (crates/nn/src/continuous_batching.rs:458-462).  n == 0 -> -1. */
+int64_t orc_argmax(const float* x, int64_t n);
+
+/* Single-token decode attention over the paged pool, per (sequence b, query
+ * head h), following TapeMultiHeadAttention::forward_tape_with_mask
+ * (crates/nn/src/tape_transformer.rs:87-139) with ndarray op semantics:
+ *   s_j = (q . k_j) * scale          matmul naive order (lib.rs:207-217),
+ *                                    scale after the dot (attention.rs:127-134)
+ *   p   = softmax_dim(s)             (lib.rs:1188-1227)
+ *   o_d = sum_j p_j * v_j[d]         matmul naive order
+ * j runs over 0 <= j < L_b (no mask: decode attends to every cached token).
+ * L_b <= 0 gives a zero output; L_b is clamped to max_blocks_per_seq *
+ * block_size; tokens in blocks with an id outside [0, num_blocks) are left
+ * out of the softmax.  q and out are [B, Hq, D] fp32. */
+int orc_decode_attention(float* out, const float* q, const void* k_pool, const void* v_pool,
+                         const int32_t* block_tables, int max_blocks_per_seq,
+                         const int32_t* ctx_lens, int num_seqs, int num_q_heads, int num_kv_heads,
+                         int head_dim, int block_size, int64_t num_blocks, float scale,
+                         int pool_dtype);
+
+/* Same computation carried out in double precision (the reference's golden
+ * precedent: crates/core/tests/golden/mod.rs:4-26). */
+int orc_decode_attention_f64(double* out, const float* q, const void* k_pool,
+                             const void* v_pool, const int32_t* block_tables,
+                             int max_blocks_per_seq, const int32_t* ctx_lens, int num_seqs,
+                             int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                             int64_t num_blocks, float scale, int pool_dtype);
+
+/* Split-K form.  Pass 1 writes, per (b, h, partition p) of partition_size
+ * tokens: m = max_j s_j, l = sum_j e^{s_j-m}, acc[d] = sum_j e^{s_j-m} v_j[d]
+ * into m/l [B, Hq, max_parts] and acc [B, Hq, max_parts, D].  Pass 2 merges
+ * with the online-softmax rule of ContextParallel::update_online_softmax /
+ * finalize_output (crates/distributed/src/context_parallel.rs:300-333):
+ *   M = max_p m_p, o = sum_p e^{m_p-M} acc_p / sum_p e^{m_p-M} l_p. */
+int orc_decode_partials(float* m, float* l, float* acc, const float* q, const void* k_pool,
+                        const void* v_pool, const int32_t* block_tables, int max_blocks_per_seq,
+                        const int32_t* ctx_lens, int num_seqs, int num_q_heads, int num_kv_heads,
+                        int head_dim, int block_size, int64_t num_blocks, float scale,
+                        int pool_dtype, int partition_size, int max_parts);
+int orc_splitk_merge(float* out, const float* m, const float* l, const float* acc,
+                     const int32_t* ctx_lens, int max_blocks_per_seq, int block_size,
+                     int num_seqs, int num_q_heads, int head_dim, int partition_size,
+                     int max_parts);
+
+/* orc_decode_attention split over n_threads POSIX threads by (b, kv head);
+ * identical results (each output is computed by one thread in the same
+ * order).  Used only as the CPU baseline timing. */
+int orc_decode_attention_mt(float* out, const float* q, const void* k_pool, const void* v_pool,
+                            const int32_t* block_tables, int max_blocks_per_seq,
+                            const int32_t* ctx_lens, int num_seqs, int num_q_heads,
+                            int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                            float scale, int pool_dtype, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

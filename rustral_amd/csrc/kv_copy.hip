@@ -1,0 +1,243 @@
+// kv_copy.hip -- KV append (scatter into pages), gather (pages -> contiguous
+// KVCache layout) and block copy (compaction) for gfx950.
+//
+// All three are HBM-streaming copies.  Every lane moves 16 bytes per access
+// (global_load/store_dwordx4), consecutive lanes touch consecutive 16-byte
+// chunks of one (block, head) tile, so each wave moves 1 KiB contiguous
+// bytes per instruction.  No LDS: there is no reuse to stage.
+#include "common.hpp"
+
+namespace rkv {
+namespace {
+
+struct alignas(16) F8 {  // 8 floats = 32 bytes
+  float4 a, b;
+};
+
+__device__ __forceinline__ F8 load_f8(const float* p) {
+  const float4* v = reinterpret_cast<const float4*>(p);
+  return F8{v[0], v[1]};
+}
+
+__device__ __forceinline__ void store_f8(float* p, const F8& x) {
+  float4* v = reinterpret_cast<float4*>(p);
+  v[0] = x.a;
+  v[1] = x.b;
+}
+
+__device__ __forceinline__ uint4 f8_to_bf16x8(const F8& x) {
+  return make_uint4(pack_bf16x2(x.a.x, x.a.y), pack_bf16x2(x.a.z, x.a.w),
+                    pack_bf16x2(x.b.x, x.b.y), pack_bf16x2(x.b.z, x.b.w));
+}
+
+__device__ __forceinline__ F8 bf16x8_to_f8(const uint4& w) {
+  return F8{make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)),
+            make_float4(bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w))};
+}
+
+// ---- append -----------------------------------------------------------------
+// grid = (n_tokens, n_layers); each thread moves 8 elements of K and of V.
+template <bool BF16>
+__global__ __launch_bounds__(256) void append_kernel(
+    void* __restrict__ k_pool, void* __restrict__ v_pool, int64_t pool_layer_stride,
+    const float* __restrict__ k_new, const float* __restrict__ v_new, int64_t src_layer_stride,
+    int64_t src_tok_stride, int64_t src_head_stride, const int64_t* __restrict__ slot_mapping,
+    int num_kv_heads, int head_dim, int block_size, int64_t num_slots) {
+  const int t = blockIdx.x, layer = blockIdx.y;
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;  // padding or out-of-range slot
+  const int64_t blk = slot / block_size, row = slot % block_size;
+  const int chunks = head_dim >> 3;
+  const int units = num_kv_heads * chunks;
+  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+    const int h = u / chunks, c = u - h * chunks;
+    const int64_t src = layer * src_layer_stride + t * src_tok_stride + h * src_head_stride + c * 8;
+    const int64_t dst =
+        layer * pool_layer_stride + ((blk * num_kv_heads + h) * block_size + row) * head_dim + c * 8;
+    const F8 k = load_f8(k_new + src);
+    const F8 v = load_f8(v_new + src);
+    if constexpr (BF16) {
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(k_pool) + dst) = f8_to_bf16x8(k);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(v_pool) + dst) = f8_to_bf16x8(v);
+    } else {
+      store_f8(static_cast<float*>(k_pool) + dst, k);
+      store_f8(static_cast<float*>(v_pool) + dst, v);
+    }
+  }
+}
+
+// ---- gather -----------------------------------------------------------------
+// grid = (max_blocks_per_seq, num_seqs, 2 [K,V]).  One workgroup copies the
+// valid rows of logical block j of sequence b for every head.  Inside a
+// (block, head) tile the first nt rows are contiguous in the pool and in the
+// output, so the copy is a flat run of nt*head_dim elements per head.
+template <typename TIn, typename TOut>
+__global__ __launch_bounds__(256) void gather_kernel(
+    TOut* __restrict__ k_out, TOut* __restrict__ v_out, const TIn* __restrict__ k_pool,
+    const TIn* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
+    int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
+    const int64_t* __restrict__ out_offsets, int num_kv_heads, int head_dim, int block_size,
+    int64_t num_blocks, int max_ctx) {
+  const int j = blockIdx.x, b = blockIdx.y;
+  const bool is_v = blockIdx.z != 0;
+  int L = ctx_lens[b];
+  L = L < 0 ? 0 : L;
+  const int cap = max_blocks_per_seq * block_size;
+  L = L > cap ? cap : L;
+  int64_t seq_base;
+  int row_stride;  // output rows per head
+  if (out_offsets) {
+    seq_base = out_offsets[b];
+    if (seq_base < 0 || (seq_base & 7)) return;  // 16-byte vector stores need 8-element alignment
+    row_stride = L;
+  } else {
+    L = L > max_ctx ? max_ctx : L;
+    seq_base = (int64_t)b * num_kv_heads * max_ctx * head_dim;
+    row_stride = max_ctx;
+  }
+  const int p0 = j * block_size;
+  if (p0 >= L) return;
+  const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + j];
+  if (blk < 0 || blk >= num_blocks) return;
+  const int nt = (L - p0) < block_size ? (L - p0) : block_size;
+  const TIn* src_pool = is_v ? v_pool : k_pool;
+  TOut* dst_all = is_v ? v_out : k_out;
+  const int per_head = (nt * head_dim) >> 3;  // 8-element units per head
+  const int units = num_kv_heads * per_head;
+  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+    const int h = u / per_head, r = u - h * per_head;
+    const TIn* s = src_pool + ((int64_t)blk * num_kv_heads + h) * block_size * head_dim + r * 8;
+    TOut* d = dst_all + seq_base + ((int64_t)h * row_stride + p0) * head_dim + r * 8;
+    if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 2) {
+      *reinterpret_cast<uint4*>(d) = *reinterpret_cast<const uint4*>(s);
+    } else if constexpr (sizeof(TIn) == 2) {
+      store_f8(reinterpret_cast<float*>(d), bf16x8_to_f8(*reinterpret_cast<const uint4*>(s)));
+    } else {
+      store_f8(reinterpret_cast<float*>(d), load_f8(reinterpret_cast<const float*>(s)));
+    }
+  }
+}
+
+// ---- copy_blocks --------------------------------------------------------------
+// grid = (n_pairs, n_layers, 2 [K,V]); each workgroup copies one block.
+__global__ __launch_bounds__(256) void copy_blocks_kernel(
+    char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t layer_stride_bytes,
+    const int32_t* __restrict__ pairs, int64_t block_bytes, int64_t num_blocks) {
+  const int i = blockIdx.x, layer = blockIdx.y;
+  const int32_t src = pairs[2 * i], dst = pairs[2 * i + 1];
+  if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) return;
+  char* base = (blockIdx.z ? v_pool : k_pool) + layer * layer_stride_bytes;
+  const uint4* s = reinterpret_cast<const uint4*>(base + src * block_bytes);
+  uint4* d = reinterpret_cast<uint4*>(base + dst * block_bytes);
+  const int64_t n = block_bytes >> 4;
+  for (int64_t u = threadIdx.x; u < n; u += blockDim.x) d[u] = s[u];
+}
+
+int check_common(int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, int dtype) {
+  if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks < 0)
+    return fail(RKV_ERR_INVALID_ARG, "num_kv_heads, head_dim, block_size must be > 0");
+  if (head_dim % 8) return fail(RKV_ERR_UNSUPPORTED, "head_dim must be a multiple of 8");
+  if (dtype != RKV_F32 && dtype != RKV_BF16)
+    return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_F32 or RKV_BF16");
+  return RKV_OK;
+}
+
+}  // namespace
+}  // namespace rkv
+
+using namespace rkv;
+
+extern "C" int rkv_append(void* k_pool, void* v_pool, int64_t pool_layer_stride,
+                          const float* k_new, const float* v_new, int64_t src_layer_stride,
+                          int64_t src_tok_stride, int64_t src_head_stride,
+                          const int64_t* slot_mapping, int64_t n_tokens, int n_layers,
+                          int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                          int dtype, void* stream) {
+  clear_error();
+  if (int rc = check_common(num_kv_heads, head_dim, block_size, num_blocks, dtype)) return rc;
+  if (n_tokens < 0 || n_layers < 0) return fail(RKV_ERR_INVALID_ARG, "negative n_tokens/n_layers");
+  if (n_tokens == 0 || n_layers == 0) return RKV_OK;
+  if (!k_pool || !v_pool || !k_new || !v_new || !slot_mapping)
+    return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (n_tokens > 0x7fffffff || n_layers > 65535)
+    return fail(RKV_ERR_INVALID_ARG, "n_tokens or n_layers too large for one launch");
+  if ((src_layer_stride | src_tok_stride | src_head_stride) & 3)
+    return fail(RKV_ERR_INVALID_ARG, "source strides must be multiples of 4 elements");
+  if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(k_pool) || !aligned16(v_pool))
+    return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
+  if (n_layers > 1 && (pool_layer_stride % 8))
+    return fail(RKV_ERR_INVALID_ARG, "pool_layer_stride must be a multiple of 8 elements");
+  const int units = num_kv_heads * (head_dim / 8);
+  const int threads = units >= 256 ? 256 : ((units + 63) / 64) * 64;
+  dim3 grid((unsigned)n_tokens, (unsigned)n_layers);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n_slots = num_blocks * block_size;
+  if (dtype == RKV_BF16)
+    append_kernel<true><<<grid, threads, 0, s>>>(k_pool, v_pool, pool_layer_stride, k_new, v_new,
+                                                  src_layer_stride, src_tok_stride, src_head_stride,
+                                                  slot_mapping, num_kv_heads, head_dim, block_size,
+                                                  n_slots);
+  else
+    append_kernel<false><<<grid, threads, 0, s>>>(k_pool, v_pool, pool_layer_stride, k_new, v_new,
+                                                   src_layer_stride, src_tok_stride,
+                                                   src_head_stride, slot_mapping, num_kv_heads,
+                                                   head_dim, block_size, n_slots);
+  return check_launch("rkv_append");
+}
+
+extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* ctx_lens, const int64_t* out_offsets, int num_seqs,
+                          int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                          int max_ctx, int dtype, int out_dtype, void* stream) {
+  clear_error();
+  if (int rc = check_common(num_kv_heads, head_dim, block_size, num_blocks, dtype)) return rc;
+  if (out_dtype != dtype && out_dtype != RKV_F32)
+    return fail(RKV_ERR_INVALID_ARG, "out_dtype must equal dtype or be RKV_F32");
+  if (num_seqs < 0 || max_blocks_per_seq < 0)
+    return fail(RKV_ERR_INVALID_ARG, "negative num_seqs/max_blocks_per_seq");
+  if (num_seqs == 0 || max_blocks_per_seq == 0) return RKV_OK;
+  if (num_seqs > 65535) return fail(RKV_ERR_INVALID_ARG, "num_seqs > 65535");
+  if (!k_out || !v_out || !k_pool || !v_pool || !block_tables || !ctx_lens)
+    return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (!out_offsets && max_ctx <= 0)
+    return fail(RKV_ERR_INVALID_ARG, "padded output needs max_ctx > 0");
+  if (!aligned16(k_out) || !aligned16(v_out) || !aligned16(k_pool) || !aligned16(v_pool))
+    return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
+  dim3 grid((unsigned)max_blocks_per_seq, (unsigned)num_seqs, 2);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define RKV_GATHER(TI, TO)                                                                     \
+  gather_kernel<TI, TO><<<grid, 256, 0, s>>>(                                                  \
+      static_cast<TO*>(k_out), static_cast<TO*>(v_out), static_cast<const TI*>(k_pool),        \
+      static_cast<const TI*>(v_pool), block_tables, max_blocks_per_seq, ctx_lens, out_offsets, \
+      num_kv_heads, head_dim, block_size, num_blocks, max_ctx)
+  if (dtype == RKV_F32)
+    RKV_GATHER(float, float);
+  else if (out_dtype == RKV_F32)
+    RKV_GATHER(uint16_t, float);
+  else
+    RKV_GATHER(uint16_t, uint16_t);
+#undef RKV_GATHER
+  return check_launch("rkv_gather");
+}
+
+extern "C" int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,
+                               int n_layers, const int32_t* pairs, int n_pairs,
+                               int64_t block_bytes, int64_t num_blocks, void* stream) {
+  clear_error();
+  if (n_pairs < 0 || n_layers < 0) return fail(RKV_ERR_INVALID_ARG, "negative n_pairs/n_layers");
+  if (n_pairs == 0 || n_layers == 0) return RKV_OK;
+  if (!k_pool || !v_pool || !pairs) return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (block_bytes <= 0 || (block_bytes & 15))
+    return fail(RKV_ERR_INVALID_ARG, "block_bytes must be a positive multiple of 16");
+  if (n_layers > 65535) return fail(RKV_ERR_INVALID_ARG, "n_layers > 65535");
+  if (n_layers > 1 && (layer_stride_bytes & 15))
+    return fail(RKV_ERR_INVALID_ARG, "layer_stride_bytes must be a multiple of 16");
+  if (!aligned16(k_pool) || !aligned16(v_pool))
+    return fail(RKV_ERR_INVALID_ARG, "pools must be 16-byte aligned");
+  dim3 grid((unsigned)n_pairs, (unsigned)n_layers, 2);
+  copy_blocks_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<char*>(k_pool), static_cast<char*>(v_pool), layer_stride_bytes, pairs,
+      block_bytes, num_blocks);
+  return check_launch("rkv_copy_blocks");
+}

@@ -1,0 +1,171 @@
+"""torch-tensor front end of the paged-KV C ABI.
+
+Device memory and streams come from PyTorch; every computation is one call
+into librustral_kv.so on the tensor's current HIP stream.  Pools are
+``[num_blocks, Hkv, block_size, D]`` (or ``[n_layers, num_blocks, Hkv,
+block_size, D]`` for multi-layer append/copy) in float32 or bfloat16.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import RKV_BF16, RKV_F32, check, lib
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return RKV_F32
+    if t.dtype == torch.bfloat16:
+        return RKV_BF16
+    raise TypeError(f"KV pool dtype {t.dtype}: want float32 or bfloat16")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def append(k_pool: torch.Tensor, v_pool: torch.Tensor, k_new: torch.Tensor,
+           v_new: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Scatter new K/V rows into the pools (every layer in one launch).
+
+    k_pool/v_pool: [num_blocks, Hkv, BS, D] or [n_layers, num_blocks, Hkv, BS, D].
+    k_new/v_new:   float32 [n_tokens, Hkv, D] or [n_layers, n_tokens, Hkv, D].
+    slot_mapping:  int64 [n_tokens], slot = block * BS + row (< 0: skip).
+    """
+    _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    _dev(k_new, "k_new", torch.float32), _dev(v_new, "v_new", torch.float32)
+    _dev(slot_mapping, "slot_mapping", torch.int64)
+    multi = k_pool.dim() == 5
+    n_layers = k_pool.shape[0] if multi else 1
+    nb, hkv, bs, d = k_pool.shape[-4:]
+    if k_new.shape != v_new.shape or k_pool.shape != v_pool.shape:
+        raise ValueError("K and V shapes differ")
+    if k_new.shape[-2:] != (hkv, d) or k_new.dim() != (4 if multi else 3):
+        raise ValueError(f"k_new shape {tuple(k_new.shape)} does not match pool {tuple(k_pool.shape)}")
+    n_tok = k_new.shape[-3]
+    if slot_mapping.shape != (n_tok,):
+        raise ValueError("slot_mapping must be [n_tokens]")
+    if multi and k_new.shape[0] != n_layers:
+        raise ValueError("k_new must have one slice per pool layer")
+    pool_ls = nb * hkv * bs * d if multi else 0
+    src_ls = n_tok * hkv * d if multi else 0
+    check(lib().rkv_append(k_pool.data_ptr(), v_pool.data_ptr(), pool_ls, k_new.data_ptr(),
+                           v_new.data_ptr(), src_ls, hkv * d, d, slot_mapping.data_ptr(), n_tok,
+                           n_layers, hkv, d, bs, nb, _dtype_code(k_pool), _stream(k_pool)))
+
+
+def gather(k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+           ctx_lens: torch.Tensor, *, max_ctx: int | None = None,
+           out_offsets: torch.Tensor | None = None, out_total: int | None = None,
+           out_dtype: torch.dtype | None = None, k_out=None, v_out=None):
+    """Reconstruct contiguous per-sequence K/V (KVCache layout [Hkv, L, D]).
+
+    Padded: returns [B, Hkv, max_ctx, D].  Packed (out_offsets int64 [B] given):
+    returns flat tensors of out_total elements.  Untouched rows keep the
+    contents of k_out/v_out (zeros when allocated here).
+    """
+    _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
+    nb, hkv, bs, d = k_pool.shape
+    B, mbs = block_tables.shape
+    out_dtype = k_pool.dtype if out_dtype is None else out_dtype
+    if out_offsets is None:
+        if max_ctx is None:
+            max_ctx = mbs * bs
+        shape = (B, hkv, max_ctx, d)
+        off_ptr = None
+    else:
+        _dev(out_offsets, "out_offsets", torch.int64)
+        if out_total is None:
+            raise ValueError("packed gather needs out_total")
+        shape = (out_total,)
+        off_ptr = out_offsets.data_ptr()
+        max_ctx = 0
+    if k_out is None:
+        k_out = torch.zeros(shape, dtype=out_dtype, device=k_pool.device)
+        v_out = torch.zeros(shape, dtype=out_dtype, device=k_pool.device)
+    check(lib().rkv_gather(k_out.data_ptr(), v_out.data_ptr(), k_pool.data_ptr(),
+                           v_pool.data_ptr(), block_tables.data_ptr(), mbs, ctx_lens.data_ptr(),
+                           off_ptr, B, hkv, d, bs, nb, max_ctx, _dtype_code(k_pool),
+                           _dtype_code(k_out), _stream(k_pool)))
+    return k_out, v_out
+
+
+def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor) -> None:
+    """Block pairs[i,1] := block pairs[i,0] in every layer of the pools.
+
+    pairs: int32 [n_pairs, 2] on the device; destinations must not be sources.
+    """
+    _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool"), _dev(pairs, "pairs", torch.int32)
+    multi = k_pool.dim() == 5
+    n_layers = k_pool.shape[0] if multi else 1
+    per = k_pool[0] if multi else k_pool
+    nb = per.shape[0]
+    block_bytes = per[0].numel() * per.element_size()
+    layer_stride = per.numel() * per.element_size() if multi else 0
+    check(lib().rkv_copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), layer_stride, n_layers,
+                                pairs.data_ptr(), pairs.shape[0], block_bytes, nb,
+                                _stream(k_pool)))
+
+
+def workspace_bytes(num_seqs: int, num_q_heads: int, head_dim: int, max_context: int) -> int:
+    return int(lib().rkv_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_context, 0))
+
+
+def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                     block_tables: torch.Tensor, ctx_lens: torch.Tensor,
+                     scale: float | None = None, *, max_context: int | None = None,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                     passes: str = "both") -> torch.Tensor:
+    """Paged GQA decode attention: q [B, Hq, D] fp32 -> out [B, Hq, D] fp32.
+
+    passes: "both" (default), "partitions" or "merge" (the two launches of
+    the split-K algorithm, for callers that time or schedule them apart).
+    """
+    _dev(q, "q", torch.float32), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
+    nb, hkv, bs, d = k_pool.shape
+    B, hq, dq = q.shape
+    if dq != d:
+        raise ValueError("q head_dim does not match the pool")
+    mbs = block_tables.shape[1]
+    if max_context is None:
+        max_context = mbs * bs
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    need = workspace_bytes(B, hq, d, max_context)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    dt = _dtype_code(k_pool)
+    s = _stream(q)
+    if passes in ("both", "partitions"):
+        fn = lib().rkv_decode_attention if passes == "both" else lib().rkv_decode_attention_partitions
+        check(fn(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                 block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), B, hq, hkv, d, bs, nb,
+                 max_context, float(scale), dt, 0, ws_ptr, ws_len, s))
+    elif passes == "merge":
+        check(lib().rkv_decode_attention_merge(out.data_ptr(), ctx_lens.data_ptr(), mbs, B, hq, d,
+                                               bs, max_context, dt, 0, ws_ptr, ws_len, s))
+    else:
+        raise ValueError(f"passes={passes!r}")
+    return out
+
+
+__all__ = ["append", "gather", "copy_blocks", "decode_attention", "workspace_bytes", "_lib"]

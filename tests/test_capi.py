@@ -1,0 +1,88 @@
+"""CPU checks of the C ABI: the library loads, exports every declared symbol,
+and rejects bad arguments on the host before any launch (no GPU needed)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from rustral_amd import _lib
+from rustral_amd._lib import (RKV_BF16, RKV_ERR_INVALID_ARG, RKV_ERR_UNSUPPORTED,
+                              RKV_ERR_WORKSPACE, RKV_F32)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for f in os.listdir(inc):
+        if f.endswith(".h"):
+            text = open(os.path.join(inc, f)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names |= set(re.findall(r"\b(rkv_\w+)\s*\(", text))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for n in sorted(names):
+        assert hasattr(L, n), f"{n} declared in include/ but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert L.rkv_version() >= 100
+
+
+def _decode(**kw):
+    a = dict(out=16, q=16, k=16, v=16, bt=16, mbs=4, cl=16, B=2, hq=8, hkv=2, d=128, bs=16,
+             nb=10, maxc=64, scale=0.1, dt=RKV_BF16, ps=0, ws=None, wsb=0, s=None)
+    a.update(kw)
+    return _lib.lib().rkv_decode_attention(a["out"], a["q"], a["k"], a["v"], a["bt"], a["mbs"],
+                                           a["cl"], a["B"], a["hq"], a["hkv"], a["d"], a["bs"],
+                                           a["nb"], a["maxc"], a["scale"], a["dt"], a["ps"],
+                                           a["ws"], a["wsb"], a["s"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(d=48), RKV_ERR_UNSUPPORTED),
+    (dict(bs=32), RKV_ERR_UNSUPPORTED),
+    (dict(hq=6, hkv=2), RKV_ERR_UNSUPPORTED),     # G = 3
+    (dict(hq=7, hkv=2), RKV_ERR_INVALID_ARG),     # not a multiple
+    (dict(dt=5), RKV_ERR_INVALID_ARG),
+    (dict(q=None), RKV_ERR_INVALID_ARG),
+    (dict(out=8), RKV_ERR_INVALID_ARG),           # misaligned
+    (dict(maxc=1000, mbs=100), RKV_ERR_WORKSPACE),  # needs split-K partials
+    (dict(ps=128), RKV_ERR_UNSUPPORTED),
+])
+def test_decode_rejects_bad_arguments(kw, code):
+    assert _decode(**kw) == code
+    assert _lib.lib().rkv_last_error().decode()
+
+
+def test_decode_zero_sequences_is_a_no_op():
+    assert _decode(B=0, out=None, q=None) == 0
+    assert _lib.lib().rkv_last_error().decode() == ""
+
+
+def test_workspace_size():
+    L = _lib.lib()
+    assert L.rkv_decode_workspace_bytes(64, 32, 128, 256, 0) == 0  # one partition
+    ws = L.rkv_decode_workspace_bytes(64, 32, 128, 4096, 0)
+    rows = 64 * 32 * 16
+    assert ws >= rows * (128 + 2) * 4
+    assert L.rkv_decode_partition_size(0, 128, RKV_BF16) == 256
+
+
+def test_copy_kernels_reject_bad_arguments():
+    L = _lib.lib()
+    assert L.rkv_append(16, 16, 0, 16, 16, 0, 1024, 128, 16, 4, 1, 8, 12, 16, 10, RKV_F32,
+                        None) == RKV_ERR_UNSUPPORTED  # head_dim 12
+    assert L.rkv_append(16, 16, 0, 16, 16, 0, 1022, 128, 16, 4, 1, 8, 128, 16, 10, RKV_F32,
+                        None) == RKV_ERR_INVALID_ARG  # stride not a multiple of 4
+    assert L.rkv_append(16, 16, 0, 16, 16, 0, 1024, 128, 16, 0, 1, 8, 128, 16, 10, RKV_F32,
+                        None) == 0  # nothing to do
+    assert L.rkv_gather(16, 16, 16, 16, 16, 4, 16, None, 2, 8, 128, 16, 10, 64, RKV_F32, RKV_BF16,
+                        None) == RKV_ERR_INVALID_ARG  # f32 -> bf16 not offered
+    assert L.rkv_copy_blocks(16, 16, 0, 1, 16, 3, 100, 10, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_copy_blocks(16, 16, 0, 1, 16, 0, 4096, 10, None) == 0

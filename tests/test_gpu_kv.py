@@ -1,0 +1,147 @@
+"""GPU parity of append / gather / copy_blocks against the oracle: bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from rustral_amd import kv
+from tests.gpu_util import say, to_dev, to_np
+from tests.helpers import contexts, make_pool, make_tables
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hkv,d", [(8, 128), (4, 32), (2, 64)])
+def test_append_bitexact(dev, dtype, hkv, d):
+    say(f"append dtype={dtype} hkv={hkv} d={d}")
+    rng = np.random.default_rng(100 + d)
+    nb, bs, n = 50, 16, 300
+    kp, vp, _, _ = make_pool(rng, nb, hkv, bs, d, dtype)
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[::37] = -1
+    slots[5] = nb * bs + 1000  # out of range: skipped on both sides
+    kn = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    gk, gv = to_dev(kp, dev), to_dev(vp, dev)
+    kv.append(gk, gv, to_dev(kn, dev), to_dev(vn, dev), to_dev(slots, dev))
+    oracle.append(kp, vp, kn, vn, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(gk), kp)
+    assert np.array_equal(to_np(gv), vp)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_append_multi_layer_one_launch(dev, dtype):
+    say(f"append multi-layer dtype={dtype}")
+    rng = np.random.default_rng(7)
+    nl, nb, hkv, bs, d, n = 4, 40, 8, 16, 128, 64
+    kp = np.zeros((nl, nb, hkv, bs, d), np.float32)
+    vp = np.zeros_like(kp)
+    if dtype == "bf16":
+        kp, vp = kp.astype(np.uint16), vp.astype(np.uint16)
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    kn = rng.standard_normal((nl, n, hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((nl, n, hkv, d)).astype(np.float32)
+    gk, gv = to_dev(kp, dev), to_dev(vp, dev)
+    kv.append(gk, gv, to_dev(kn, dev), to_dev(vn, dev), to_dev(slots, dev))
+    for l in range(nl):
+        oracle.append(kp[l], vp[l], kn[l], vn[l], slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(gk), kp) and np.array_equal(to_np(gv), vp)
+
+
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_gather_bitexact_padded_and_packed(dev, dtype, out_f32):
+    say(f"gather dtype={dtype} out_f32={out_f32}")
+    rng = np.random.default_rng(11)
+    nb, hkv, bs, d = 400, 8, 16, 128
+    ctx = np.array([0, 1, 15, 16, 17, 255, 1000, 2049], np.int32)
+    kp, vp, _, _ = make_pool(rng, nb, hkv, bs, d, dtype)
+    tables = make_tables(rng, ctx, bs, nb)
+    tables[6, 3] = nb + 7  # invalid block id: its rows stay untouched
+    gk, gv = to_dev(kp, dev), to_dev(vp, dev)
+    gt, gc = to_dev(tables, dev), to_dev(ctx, dev)
+    odt = torch.float32 if out_f32 else None
+    ko, vo = kv.gather(gk, gv, gt, gc, max_ctx=int(ctx.max()), out_dtype=odt)
+    rk, rv = oracle.gather(kp, vp, tables, ctx, max_ctx=int(ctx.max()), out_f32=out_f32)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(ko), rk) and np.array_equal(to_np(vo), rv)
+    sizes = ctx.astype(np.int64) * hkv * d
+    off = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    total = int(sizes.sum())
+    ko, vo = kv.gather(gk, gv, gt, gc, out_offsets=to_dev(off, dev), out_total=total,
+                       out_dtype=odt)
+    rk, rv = oracle.gather(kp, vp, tables, ctx, out_offsets=off, out_f32=out_f32)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(ko), rk) and np.array_equal(to_np(vo), rv)
+
+
+def test_gather_of_append_roundtrip_config1_shape(dev):
+    """Config-1 shape (Hkv 8, D 128, BS 16, 65,536-block pool, 64 sequences with
+    contexts U[512, 4096]), two layers: append every token of every sequence,
+    gather, and get the appended rows back bit for bit (bf16 pool: their RNE
+    rounding, checked against the oracle's bit routine)."""
+    say("append+gather round trip, config-1 shape")
+    rng = np.random.default_rng(1)
+    nl, nb, hkv, bs, d, B = 2, 65536, 8, 16, 128, 64
+    ctx = contexts(rng, B, 512, 4096)
+    tables = make_tables(rng, ctx, bs, nb, max_blocks=4096 // bs)
+    pos = [np.arange(L) for L in ctx]
+    slots = np.concatenate([tables[b, p // bs].astype(np.int64) * bs + p % bs
+                            for b, p in enumerate(pos)])
+    n = slots.shape[0]
+    g = torch.Generator(device=dev).manual_seed(1)
+    kn = torch.randn((nl, n, hkv, d), generator=g, device=dev)
+    vn = torch.randn((nl, n, hkv, d), generator=g, device=dev)
+    gk = torch.zeros((nl, nb, hkv, bs, d), dtype=torch.bfloat16, device=dev)
+    gv = torch.zeros_like(gk)
+    kv.append(gk, gv, kn, vn, to_dev(slots, dev))
+    gt, gc = to_dev(tables, dev), to_dev(ctx, dev)
+    offs = np.concatenate([[0], np.cumsum(ctx.astype(np.int64))[:-1]])
+    for l in range(nl):
+        ko, vo = kv.gather(gk[l], gv[l], gt, gc, max_ctx=4096)
+        # compare a strided subset of sequences on the host, all of them on device
+        for b in range(0, B, 9):
+            L = int(ctx[b])
+            want_k = oracle.bf16_from_f32(
+                kn[l, offs[b]:offs[b] + L].cpu().numpy()).transpose(1, 0, 2)
+            assert np.array_equal(to_np(ko[b, :, :L]), want_k)
+        for b in range(B):
+            L = int(ctx[b])
+            sk = kn[l, offs[b]:offs[b] + L].to(torch.bfloat16).transpose(0, 1)
+            sv = vn[l, offs[b]:offs[b] + L].to(torch.bfloat16).transpose(0, 1)
+            assert torch.equal(ko[b, :, :L].view(torch.int16), sk.contiguous().view(torch.int16))
+            assert torch.equal(vo[b, :, :L].view(torch.int16), sv.contiguous().view(torch.int16))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_copy_blocks_bitexact_multi_layer(dev, dtype):
+    say(f"copy_blocks dtype={dtype}")
+    rng = np.random.default_rng(13)
+    nl, nb, hkv, bs, d = 3, 200, 8, 16, 128
+    kp = rng.standard_normal((nl, nb, hkv, bs, d)).astype(np.float32)
+    vp = rng.standard_normal((nl, nb, hkv, bs, d)).astype(np.float32)
+    if dtype == "bf16":
+        kp, vp = oracle.bf16_from_f32(kp), oracle.bf16_from_f32(vp)
+    perm = rng.permutation(nb)
+    pairs = np.stack([perm[:60], perm[60:120]], axis=1).astype(np.int32)
+    pairs = np.concatenate([pairs, [[1, nb], [-5, 3]]]).astype(np.int32)
+    gk, gv = to_dev(kp, dev), to_dev(vp, dev)
+    kv.copy_blocks(gk, gv, to_dev(pairs, dev))
+    oracle.copy_blocks(kp, vp, pairs)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(gk), kp) and np.array_equal(to_np(gv), vp)
+
+
+def test_empty_calls_are_no_ops(dev):
+    say("empty calls")
+    gk = torch.zeros((4, 2, 16, 32), device=dev)
+    gv = torch.zeros_like(gk)
+    kv.append(gk, gv, torch.zeros((0, 2, 32), device=dev), torch.zeros((0, 2, 32), device=dev),
+              torch.zeros((0,), dtype=torch.int64, device=dev))
+    kv.copy_blocks(gk, gv, torch.zeros((0, 2), dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert not gk.any()
