@@ -41,6 +41,8 @@ def parse():
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(nproc, 16)")
+    p.add_argument("--copy-only", action="store_true",
+                   help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -144,6 +146,10 @@ def main():
     from rustral_amd import kv
 
     dev = torch.device("cuda:0")
+    if args.copy_only:
+        gbps = copy_bandwidth(torch, dev, nbytes=1 << 30, reps=5)
+        print(json.dumps({"copy_bytes": 1 << 30, "reps": 6, "copy_GBps": round(gbps, 1)}))
+        return
     layers, ctx, ctx_d, nb, mbs = build_workload(torch, dev, args.layers)
     n_layers = len(layers)
     max_ctx = mbs * BS
@@ -223,7 +229,7 @@ def main():
         "measured_copy_GBps": round(copy_gbps, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "kernel": "decode_partition_kernel<bf16,128,4>",
+                     "kernel": "decode_stream_kernel<bf16, D=128, G=4> (one wave per 256-token partition)",
                      "traffic": traffic},
         "cpu_baseline": cpu,
     }

@@ -24,16 +24,21 @@
 //   M = max m_p;  out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.
 // Sequences that fit one partition are finished in pass 1.
 //
-// Scores are kept in the log2 domain: q is pre-multiplied by
-// scale * log2(e), so softmax uses exp2 (v_exp_f32) directly.
+// Scores are kept in the log2 domain: the dot product is multiplied by
+// scale * log2(e) (scale after the dot, as the reference applies it), so the
+// softmax uses exp2 (v_exp_f32) directly.
 #include "common.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace rkv {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+// Upper bound on partitions per sequence the merge pass accepts (LDS weights):
+// 1M tokens at 256 tokens per partition.
+constexpr int kMaxMergeParts = 4096;  // 16 KiB of merge weights in LDS
 
 template <typename T>
 struct Traits;
@@ -45,6 +50,19 @@ template <>
 struct Traits<uint16_t> {
   static constexpr int E = 8;
 };
+
+// Calls f(std::integral_constant<int, I>) for I = B .. E-1 in order.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// Matrix-core operand types (v_mfma_f32_16x16x32_bf16).
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 // Converts one 16-byte load into E floats.
 __device__ __forceinline__ void to_float(const uint4& w, float (&f)[8]) {
@@ -92,43 +110,24 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int slot = lane / LPT, dl = lane % LPT;
 
-  int L = ctx_lens[b];
-  L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
-  const int nparts = (L + P - 1) / P;
   const int64_t head0 = (int64_t)b * num_q_heads + kh * G;  // first query head row
-  if (L == 0) {
-    if (part == 0)
-      for (int o = tid; o < G * D; o += NT) out[head0 * D + o] = 0.0f;
-    return;
-  }
-  if (part >= nparts) return;
 
-  // ---- issue every K and V load of this wave ----
-  uint4 kr[TPW][NL], vr[TPW][NL];
-  bool tile_ok[TPW];
+  // Everything whose address does not depend on the context length is
+  // requested before the length arrives: the context length, this wave's
+  // block ids (index clamped into the table), the partition's first block id
+  // and the queries.  The KV loads then wait on one round trip instead of a
+  // chain of them.
+  int L = ctx_lens[b];
+  int32_t pbs[TPW];
+  const int lb0 = part * (P / BS);
+  const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
-    const int lb = part * (P / BS) + w + NW * i;  // logical block of the sequence
-    const int tbase = lb * BS;
-    int32_t pb = -1;
-    if (tbase < L) pb = block_tables[(int64_t)b * max_blocks_per_seq + lb];
-    const bool ok = (tbase < L) && pb >= 0 && pb < num_blocks;
-    tile_ok[i] = ok;
-    const int64_t base = ((int64_t)(ok ? pb : 0) * num_kv_heads + kh) * BS * D + dl * E;
-#pragma unroll
-    for (int n = 0; n < NL; ++n) {
-      const int row = n * TPL + slot;
-      if (ok && tbase + row < L) {
-        kr[i][n] = *reinterpret_cast<const uint4*>(k_pool + base + row * D);
-        vr[i][n] = *reinterpret_cast<const uint4*>(v_pool + base + row * D);
-      } else {
-        kr[i][n] = make_uint4(0, 0, 0, 0);
-        vr[i][n] = make_uint4(0, 0, 0, 0);
-      }
-    }
+    const int lb = lb0 + w + NW * i;
+    const int lbc = lb < max_blocks_per_seq ? lb : max_blocks_per_seq - 1;
+    pbs[i] = lbc >= 0 ? tab[lbc] : -1;
   }
-
-  // ---- queries, pre-scaled into the exp2 domain ----
+  int32_t pb_first = lb0 < max_blocks_per_seq ? tab[lb0] : -1;
   float qf[G][E];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -136,12 +135,49 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
 #pragma unroll
     for (int e = 0; e < E; e += 4) {
       const float4 v = *reinterpret_cast<const float4*>(qp + e);
-      qf[g][e + 0] = v.x * q_scale;
-      qf[g][e + 1] = v.y * q_scale;
-      qf[g][e + 2] = v.z * q_scale;
-      qf[g][e + 3] = v.w * q_scale;
+      qf[g][e + 0] = v.x;
+      qf[g][e + 1] = v.y;
+      qf[g][e + 2] = v.z;
+      qf[g][e + 3] = v.w;
     }
   }
+  L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
+  const int nparts = (L + P - 1) / P;
+  if (L == 0) {
+    if (part == 0)
+      for (int o = tid; o < G * D; o += NT) out[head0 * D + o] = 0.0f;
+    return;
+  }
+  if (part >= nparts) return;
+
+  // ---- issue every K load, then every V load, of this wave ----
+  // Loads are unconditional so the compiler keeps them back to back.  A tile
+  // past the context or with an invalid block id re-reads the partition's
+  // first tile (already requested by wave 0, so the L2 serves it), or block 0
+  // when that id is invalid too; its scores are masked and its V is zeroed.
+  if (pb_first < 0 || pb_first >= num_blocks) pb_first = 0;
+  int64_t base[TPW];
+  bool tile_ok[TPW], tile_full[TPW];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int tbase = (lb0 + w + NW * i) * BS;
+    const int32_t pb = pbs[i];
+    const bool ok = (tbase < L) && pb >= 0 && pb < num_blocks;
+    tile_ok[i] = ok;
+    tile_full[i] = ok && tbase + BS <= L;
+    base[i] = ((int64_t)(ok ? pb : pb_first) * num_kv_heads + kh) * BS * D + dl * E;
+  }
+  uint4 kr[TPW][NL], vr[TPW][NL];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i)
+#pragma unroll
+    for (int n = 0; n < NL; ++n)
+      kr[i][n] = *reinterpret_cast<const uint4*>(k_pool + base[i] + (n * TPL + slot) * D);
+#pragma unroll
+  for (int i = 0; i < TPW; ++i)
+#pragma unroll
+    for (int n = 0; n < NL; ++n)
+      vr[i][n] = *reinterpret_cast<const uint4*>(v_pool + base[i] + (n * TPL + slot) * D);
 
   // ---- phase 1: scores ----
   const int tok0 = part * P;
@@ -157,7 +193,7 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
         float a = 0.0f;
 #pragma unroll
         for (int e = 0; e < E; ++e) a = fmaf(qf[g][e], kf[e], a);
-        s[g] = group_sum<LPT>(a);
+        s[g] = group_sum<LPT>(a) * q_scale;  // scale after the dot
       }
       const int tp = (w + NW * i) * BS + n * TPL + slot;  // token within the partition
       const bool valid = tile_ok[i] && (tok0 + tp < L);
@@ -228,6 +264,12 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
     for (int e = 0; e < E; ++e) acc[g][e] = 0.0f;
 #pragma unroll
   for (int i = 0; i < TPW; ++i) {
+    if (!tile_full[i]) {  // wave-uniform: only the last tile of a sequence, or a bad id
+      const int tbase = (lb0 + w + NW * i) * BS;
+#pragma unroll
+      for (int n = 0; n < NL; ++n)
+        if (!tile_ok[i] || tbase + n * TPL + slot >= L) vr[i][n] = make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
       float vf[E];
@@ -279,77 +321,456 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
   }
 }
 
-// grid = (num_q_heads, num_seqs), D threads (>= 64).
+// ---- streaming variant: one wave per partition --------------------------------
+// One 64-lane wave owns one (partition of NTILE blocks, KV head, sequence)
+// item and streams its 2*NTILE (block, head) tiles -- the K tiles, then the V
+// tiles -- through a ring of R register tiles: the loads of tile t + R are
+// issued as soon as tile t has been consumed, so a wave always has R tiles
+// (R KiB x 4 for bf16 D=128) in flight and its arithmetic overlaps its own
+// loads.  There are no cross-wave barriers; scores live in wave-private LDS.
+// Lane mapping and arithmetic are those of decode_partition_kernel, except
+// that for bf16 pools QK^T runs on the matrix cores (MFMA = true): one
+// v_mfma_f32_16x16x32_bf16 per 32 dims of a 16-token tile with
+//   A (16 x 32) = queries: rows 0..G-1 = bf16(q) of the G heads, rows
+//                 G..2G-1 = bf16(q - bf16(q)), other rows zero.  hi + lo keeps
+//                 ~16 significant bits of q: scores as accurate as fp32 dots.
+//   B (32 x 16) = K^T of the tile: lane l loads 16 bytes of token row l % 16
+//                 at dims 32c + 8 (l / 16) straight from the pool.
+//   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
+// (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
+// D[4(l/16)+r][l%16].)  PV stays on the VALU.
+template <typename T, int D, int G, int BS, int NTILE, int R, int KHW>
+__global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
+    float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
+    const float* __restrict__ q, const void* __restrict__ k_pool_,
+    const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
+    int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens, int ctx_cap, int num_kv_heads,
+    int64_t num_blocks, float q_scale, int max_parts) {
+  const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
+  const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
+  constexpr int E = Traits<T>::E;
+  constexpr int LPT = D / E;     // lanes per token row
+  constexpr int TPL = 64 / LPT;  // token rows per wave-load
+  constexpr int NL = BS / TPL;   // wave-loads per tile
+  constexpr int P = NTILE * BS;  // tokens per partition
+  constexpr int NT = 2 * NTILE;  // tiles streamed: K then V
+  static_assert(D % E == 0 && 64 % LPT == 0 && BS % TPL == 0 && R >= 1 && R <= NT,
+                "unsupported tile shape");
+
+  __shared__ __align__(16) float s_pw[KHW][P * G];  // per wave: scores, then probabilities
+
+  // KHW waves = KHW consecutive KV heads of one (partition, sequence): the
+  // waves stay co-scheduled and read the adjacent head tiles of each block
+  // (KHW * 4 KiB contiguous for bf16 D=128) at the same time.
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kh = blockIdx.x * KHW + w, part = blockIdx.y, b = blockIdx.z;
+  float* __restrict__ s_p = s_pw[w];
+  const int num_q_heads = num_kv_heads * G;
+  const int lane = threadIdx.x & 63;
+  const int slot = lane / LPT, dl = lane % LPT;
+  const int64_t head0 = (int64_t)b * num_q_heads + kh * G;
+
+  // Requests that do not depend on the context length go out first.
+  int L = ctx_lens[b];
+  const int lb0 = part * NTILE;
+  const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
+  int32_t pb[NTILE];
+#pragma unroll
+  for (int i = 0; i < NTILE; ++i) {
+    const int lb = lb0 + i;
+    const int lbc = lb < max_blocks_per_seq ? lb : max_blocks_per_seq - 1;
+    pb[i] = lbc >= 0 ? tab[lbc] : -1;
+  }
+  constexpr bool MFMA = sizeof(T) == 2 && 2 * G <= 16;
+  constexpr int NC = D / 32;                     // MFMAs per tile (bf16: == NL)
+  const int kt = lane & 15, kq = lane >> 4;      // MFMA lanes: token row, k-quarter
+  // VALU path: this lane's E dims of each head.  MFMA path: the A operand
+  // row kt (hi rows 0..G-1, lo rows G..2G-1) at dims 32c + 8 kq .. + 8.
+  constexpr int QN = MFMA ? NC * 8 : G * E;
+  float qv[QN];
+  if constexpr (MFMA) {
+    const int qrow = kt < G ? kt : (kt < 2 * G ? kt - G : 0);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float4* qp = reinterpret_cast<const float4*>(q + (head0 + qrow) * D + 32 * c + 8 * kq);
+      const float4 x = qp[0], y = qp[1];
+      qv[c * 8 + 0] = x.x; qv[c * 8 + 1] = x.y; qv[c * 8 + 2] = x.z; qv[c * 8 + 3] = x.w;
+      qv[c * 8 + 4] = y.x; qv[c * 8 + 5] = y.y; qv[c * 8 + 6] = y.z; qv[c * 8 + 7] = y.w;
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float* qp = q + (head0 + g) * D + dl * E;
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(qp + e);
+        qv[g * E + e + 0] = v.x;
+        qv[g * E + e + 1] = v.y;
+        qv[g * E + e + 2] = v.z;
+        qv[g * E + e + 3] = v.w;
+      }
+    }
+  }
+  L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
+  const int nparts = (L + P - 1) / P;
+  if (L == 0) {
+    if (part == 0)
+      for (int o = lane; o < G * D; o += 64) out[head0 * D + o] = 0.0f;
+    return;
+  }
+  if (part >= nparts) return;
+
+  // Tile i of the partition is block lb0 + i.  A tile past the context, or
+  // with an invalid id, re-reads tile 0 (an L2 hit) and is masked.
+  const int32_t pb0 = (pb[0] >= 0 && pb[0] < num_blocks) ? pb[0] : 0;
+  int64_t base[NTILE];  // wave-uniform element offset of each (block, head) tile
+  bool ok[NTILE], full[NTILE];
+#pragma unroll
+  for (int i = 0; i < NTILE; ++i) {
+    const int tbase = (lb0 + i) * BS;
+    ok[i] = tbase < L && pb[i] >= 0 && pb[i] < num_blocks;
+    full[i] = ok[i] && tbase + BS <= L;
+    base[i] = ((int64_t)(ok[i] ? pb[i] : pb0) * num_kv_heads + kh) * BS * D;
+  }
+  // this lane's first element in a tile, and the stride between its loads
+  const T* __restrict__ kl = MFMA ? k_pool + kt * D + 8 * kq : k_pool + slot * D + dl * E;
+  const T* __restrict__ vl = v_pool + slot * D + dl * E;
+  constexpr int KSTEP = MFMA ? 32 : TPL * D;
+  constexpr int VSTEP = TPL * D;
+
+  uint4 ring[R][NL];
+#pragma unroll
+  for (int t = 0; t < R; ++t) {
+    const T* pool = t < NTILE ? kl : vl;
+    const int step = t < NTILE ? KSTEP : VSTEP;
+#pragma unroll
+    for (int n = 0; n < NL; ++n)
+      ring[t][n] = *reinterpret_cast<const uint4*>(pool + base[t % NTILE] + n * step);
+  }
+
+  // MFMA A operands: q split into bf16 hi + lo rows (after the ring loads
+  // are issued, so the conversion overlaps them)
+  uint4 qa[MFMA ? NC : 1];
+  if constexpr (MFMA) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t hi = bf16_rne(qv[c * 8 + e]);
+        const uint32_t lo = bf16_rne(qv[c * 8 + e] - __uint_as_float(hi << 16));
+        h[e] = kt < G ? hi : (kt < 2 * G ? lo : 0u);
+      }
+      qa[c] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                         h[6] | (h[7] << 16));
+    }
+  }
+
+  const int tok0 = part * P;
+  float acc[G][E];
+  float m[G], l[G];
+  // The 2*NTILE steps are instantiated one by one (static_for) so that every
+  // ring slot is a fixed set of registers.
+  static_for<0, NT>([&](auto tc) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value;
+    constexpr int i = t % NTILE;
+    uint4* tile = ring[t % R];
+    if constexpr (t < NTILE) {
+      // ---- QK^T for the 16 tokens of tile i ----
+      if constexpr (MFMA) {
+        f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[c]),
+                                                        __builtin_bit_cast(bf16x8_t, tile[c]),
+                                                        sacc, 0, 0, 0);
+        const int tp = i * BS + kt;  // token of this lane's column
+        const bool valid = ok[i] && (tok0 + tp < L);
+        if constexpr (G == 1) {
+          if (kq == 0) s_p[tp] = valid ? (sacc[0] + sacc[1]) * q_scale : -INFINITY;
+        } else if constexpr (G == 2) {
+          if (kq == 0) {
+            s_p[tp * 2 + 0] = valid ? (sacc[0] + sacc[2]) * q_scale : -INFINITY;
+            s_p[tp * 2 + 1] = valid ? (sacc[1] + sacc[3]) * q_scale : -INFINITY;
+          }
+        } else {
+          constexpr int XOR = G == 4 ? 16 : 32;  // lanes between hi and lo rows
+          float sc[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[r] = (sacc[r] + __shfl_xor(sacc[r], XOR)) * q_scale;
+          if (lane < XOR) {  // lanes kq * 16 + kt hold heads 4 kq .. 4 kq + 3
+            *reinterpret_cast<float4*>(&s_p[tp * G + 4 * kq]) =
+                valid ? make_float4(sc[0], sc[1], sc[2], sc[3])
+                      : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+          float kf[E];
+          to_float(tile[n], kf);
+          float sc[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) a = fmaf(qv[g * E + e], kf[e], a);
+            sc[g] = group_sum<LPT>(a) * q_scale;  // scale after the dot
+          }
+          const int tp = i * BS + n * TPL + slot;
+          const bool valid = ok[i] && (tok0 + tp < L);
+          if (dl == 0) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) s_p[tp * G + g] = valid ? sc[g] : -INFINITY;
+          }
+        }
+      }
+      if constexpr (t == NTILE - 1) {
+        // ---- softmax statistics over the partition (this wave only) ----
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // LDS writes above ...
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads below
+#pragma unroll
+        for (int g = 0; g < G; ++g) m[g] = -INFINITY;
+#pragma unroll
+        for (int x = lane; x < P; x += 64)
+#pragma unroll
+          for (int g = 0; g < G; ++g) m[g] = fmaxf(m[g], s_p[x * G + g]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          m[g] = wave_max(m[g]);
+          l[g] = 0.0f;
+        }
+#pragma unroll
+        for (int x = lane; x < P; x += 64)
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float sv = s_p[x * G + g];
+            const float pv = (sv == -INFINITY) ? 0.0f : exp2f(sv - m[g]);
+            s_p[x * G + g] = pv;
+            l[g] += pv;
+          }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          l[g] = wave_sum(l[g]);
+#pragma unroll
+          for (int e = 0; e < E; ++e) acc[g][e] = 0.0f;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    } else {
+      // ---- PV for the 16 tokens of tile i ----
+      // Rows past the context (or of a bad block id) are zeroed with selects,
+      // not branches: branches here let the compiler sink every PV FMA to the
+      // end of the kernel and keep all V tiles live.
+      const int tbase = (lb0 + i) * BS;
+#pragma unroll
+      for (int n = 0; n < NL; ++n) {
+        const bool keep = ok[i] & (tbase + n * TPL + slot < L);
+        uint4 vv = tile[n];
+        vv.x = keep ? vv.x : 0u;
+        vv.y = keep ? vv.y : 0u;
+        vv.z = keep ? vv.z : 0u;
+        vv.w = keep ? vv.w : 0u;
+        float vf[E];
+        to_float(vv, vf);
+        const int tp = i * BS + n * TPL + slot;
+        float pr[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) pr[g] = s_p[tp * G + g];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < E; ++e) acc[g][e] = fmaf(pr[g], vf[e], acc[g][e]);
+      }
+    }
+    if constexpr (t + R < NT) {  // refill the slot just consumed
+      constexpr int tn = t + R;
+      const T* pool = tn < NTILE ? kl : vl;
+      constexpr int step = tn < NTILE ? KSTEP : VSTEP;
+#pragma unroll
+      for (int n = 0; n < NL; ++n)
+        tile[n] = *reinterpret_cast<const uint4*>(pool + base[tn % NTILE] + n * step);
+    }
+    // keep the ring a ring: the scheduler may not hoist later refills above
+    // this step's arithmetic (that would need all 2*NTILE tiles in registers)
+    __builtin_amdgcn_sched_barrier(0);
+  });
+
+  // sum over the TPL token rows, then lanes of row 0 hold the result
+#pragma unroll
+  for (int o = LPT; o < 64; o <<= 1)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float* dst;
+      float scl = 1.0f;
+      if (nparts == 1) {
+        dst = out + (head0 + g) * D + dl * E;
+        scl = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+      } else {
+        const int64_t row = (head0 + g) * max_parts + part;
+        dst = part_acc + row * D + dl * E;
+        if (dl == 0) {
+          part_ml[row * 2 + 0] = m[g];
+          part_ml[row * 2 + 1] = l[g];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < E; e += 4)
+        *reinterpret_cast<float4*>(dst + e) =
+            make_float4(acc[g][e] * scl, acc[g][e + 1] * scl, acc[g][e + 2] * scl,
+                        acc[g][e + 3] * scl);
+    }
+  }
+}
+
+// grid = (num_q_heads, num_seqs), one wave per (query head, sequence).
+// Partition statistics are read by all lanes at once (lane p holds
+// partition p, p + 64, ...), weights go through LDS, then every lane sums
+// D/64 output dims over the partitions with independent loads.
 template <int D>
-__global__ __launch_bounds__(D < 64 ? 64 : D) void decode_merge_kernel(
+__global__ __launch_bounds__(64) void decode_merge_kernel(
     float* __restrict__ out, const float* __restrict__ part_acc,
     const float* __restrict__ part_ml, const int32_t* __restrict__ ctx_lens, int ctx_cap,
     int num_q_heads, int P, int max_parts) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  constexpr int DPL = D < 64 ? 1 : D / 64;  // dims per lane
+  extern __shared__ float s_w[];            // max_parts weights (dynamic LDS)
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   int L = ctx_lens[b];
   L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
   const int np = (L + P - 1) / P;
-  if (np <= 1 || d >= D) return;
+  if (np <= 1) return;
   const int64_t row0 = ((int64_t)b * num_q_heads + h) * max_parts;
   float M = -INFINITY;
-  for (int p = 0; p < np; ++p) M = fmaxf(M, part_ml[(row0 + p) * 2]);
-  float num = 0.0f, den = 0.0f;
-  if (M != -INFINITY) {
-    for (int p = 0; p < np; ++p) {
-      const float m = part_ml[(row0 + p) * 2];
-      const float wgt = (m == -INFINITY) ? 0.0f : exp2f(m - M);
-      den = fmaf(wgt, part_ml[(row0 + p) * 2 + 1], den);
-      num = fmaf(wgt, part_acc[(row0 + p) * D + d], num);
-    }
+  for (int p = lane; p < np; p += 64) M = fmaxf(M, part_ml[(row0 + p) * 2]);
+  M = wave_max(M);
+  float den = 0.0f;
+  for (int p = lane; p < np; p += 64) {
+    const float m = part_ml[(row0 + p) * 2];
+    const float wgt = (m == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m - M);
+    s_w[p] = wgt;
+    den = fmaf(wgt, part_ml[(row0 + p) * 2 + 1], den);
   }
-  out[((int64_t)b * num_q_heads + h) * D + d] = den > 0.0f ? num / den : 0.0f;
+  den = wave_sum(den);
+  __syncthreads();
+  float num[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) num[j] = 0.0f;
+  if (lane * DPL < D) {
+#pragma unroll 4
+    for (int p = 0; p < np; ++p) {
+      const float wgt = s_w[p];
+      const float* a = part_acc + (row0 + p) * D + lane * DPL;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) num[j] = fmaf(wgt, a[j], num[j]);
+    }
+    float* o = out + ((int64_t)b * num_q_heads + h) * D + lane * DPL;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) o[j] = den > 0.0f ? num[j] / den : 0.0f;
+  }
 }
 
 // ---- dispatch ----------------------------------------------------------------
 
 constexpr int kBS = 16;
-constexpr int kP = 256;  // tokens per partition
+// Tokens per partition and waves per workgroup (bf16 pools; fp32 D=128 uses
+// twice the waves so a wave holds at most 16 16-byte K+V loads per lane).
+#ifndef RKV_DECODE_P
+#define RKV_DECODE_P 256
+#endif
+#ifndef RKV_DECODE_NW
+#define RKV_DECODE_NW 4
+#endif
+constexpr int kP = RKV_DECODE_P;
+#ifndef RKV_DECODE_STREAM
+#define RKV_DECODE_STREAM 1
+#endif
+#ifndef RKV_DECODE_RING_LOADS
+#define RKV_DECODE_RING_LOADS 16
+#endif
+constexpr bool kStream = RKV_DECODE_STREAM != 0;
+
 
 struct Launch {
   int nw = 0;
+  int khw = 0;  // streaming kernel: KV heads (waves) per workgroup
   void (*kernel)(float*, float*, float*, const float*, const void*, const void*, const int32_t*,
                  int, const int32_t*, int, int, int64_t, float, int) = nullptr;
 };
 
-template <typename T, int D, int G, int NW>
+// Ring depth of the streaming kernel: 32 16-byte loads per lane in flight
+// (128 VGPRs), at most every tile of the partition.
+template <typename T, int D>
+constexpr int ring_for() {
+  constexpr int nl = kBS / (64 / (D / Traits<T>::E));
+  constexpr int r = RKV_DECODE_RING_LOADS / nl;
+  constexpr int nt = 2 * (kP / kBS);
+  return r < 1 ? 1 : (r > nt ? nt : r);
+}
+
+template <typename T, int D, int G, int NW, int KHW>
 Launch make_launch() {
-  constexpr int TPW = kP / (NW * kBS);
   Launch l;
-  l.nw = NW;
-  l.kernel = &decode_partition_kernel<T, D, G, kBS, NW, TPW>;
+  if constexpr (kStream) {
+    l.nw = KHW;
+    l.khw = KHW;
+    l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), KHW>;
+  } else {
+    constexpr int TPW = kP / (NW * kBS);
+    static_assert(TPW >= 1 && TPW * NW * kBS == kP, "partition must split evenly over waves");
+    l.nw = NW;
+    l.kernel = &decode_partition_kernel<T, D, G, kBS, NW, TPW>;
+  }
   return l;
 }
 
-// (T, D) -> waves per workgroup; tiles per wave = kP / (NW * 16).  Chosen so
-// a wave holds at most 16 16-byte K+V loads per lane (64 VGPRs each of K, V).
 template <typename T, int D>
 constexpr int waves_for() {
-  return (sizeof(T) == 4 && D == 128) ? 8 : 4;
+  constexpr int nw = RKV_DECODE_NW;
+  return (sizeof(T) == 4 && D == 128 && kP / (nw * kBS) > 2) ? nw * 2 : nw;
+}
+
+#ifndef RKV_DECODE_KHW
+#define RKV_DECODE_KHW 1
+#endif
+
+template <typename T, int D, int G>
+Launch pick_khw(int hkv) {
+  constexpr int NW = waves_for<T, D>();
+  // largest KV-head group <= RKV_DECODE_KHW that divides num_kv_heads
+  if constexpr (RKV_DECODE_KHW >= 8)
+    if (hkv % 8 == 0) return make_launch<T, D, G, NW, 8>();
+  if constexpr (RKV_DECODE_KHW >= 4)
+    if (hkv % 4 == 0) return make_launch<T, D, G, NW, 4>();
+  if constexpr (RKV_DECODE_KHW >= 2)
+    if (hkv % 2 == 0) return make_launch<T, D, G, NW, 2>();
+  return make_launch<T, D, G, NW, 1>();
 }
 
 template <typename T, int D>
-Launch pick_g(int G) {
-  constexpr int NW = waves_for<T, D>();
+Launch pick_g(int G, int hkv) {
   switch (G) {
-    case 1: return make_launch<T, D, 1, NW>();
-    case 2: return make_launch<T, D, 2, NW>();
-    case 4: return make_launch<T, D, 4, NW>();
-    case 8: return make_launch<T, D, 8, NW>();
+    case 1: return pick_khw<T, D, 1>(hkv);
+    case 2: return pick_khw<T, D, 2>(hkv);
+    case 4: return pick_khw<T, D, 4>(hkv);
+    case 8: return pick_khw<T, D, 8>(hkv);
     default: return Launch{};
   }
 }
 
 template <typename T>
-Launch pick_d(int D, int G) {
+Launch pick_d(int D, int G, int hkv) {
   switch (D) {
-    case 32: return pick_g<T, 32>(G);
-    case 64: return pick_g<T, 64>(G);
-    case 128: return pick_g<T, 128>(G);
+    case 32: return pick_g<T, 32>(G, hkv);
+    case 64: return pick_g<T, 64>(G, hkv);
+    case 128: return pick_g<T, 128>(G, hkv);
     default: return Launch{};
   }
 }
@@ -399,12 +820,15 @@ int validate(const DecodeArgs& a, int& max_parts) {
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(RKV_ERR_UNSUPPORTED, "num_q_heads / num_kv_heads must be 1, 2, 4 or 8");
   if (a.partition_size > 0 && a.partition_size != kP)
-    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be 256 (or <= 0 for the default)");
+    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
   if (a.num_seqs > 65535 || a.num_kv_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_kv_heads must be <= 65535");
   if (a.max_context < 0) return fail(RKV_ERR_INVALID_ARG, "max_context must be >= 0");
+  if (a.num_blocks < 1) return fail(RKV_ERR_INVALID_ARG, "num_blocks must be >= 1");
   const int cap = ctx_cap_of(a.max_context, a.max_blocks_per_seq, a.block_size);
   max_parts = cap <= 0 ? 1 : (cap + kP - 1) / kP;
+  if (max_parts > kMaxMergeParts)
+    return fail(RKV_ERR_UNSUPPORTED, "max_context / partition size above 4096 partitions");
   if (a.num_seqs == 0) return RKV_OK;
   if (!a.out || !a.q || !a.k_pool || !a.v_pool || !a.block_tables || !a.ctx_lens)
     return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
@@ -427,12 +851,16 @@ void split_ws(void* ws, int B, int Hq, int D, int max_parts, float*& acc, float*
 
 int launch_partitions(const DecodeArgs& a, int max_parts) {
   const int G = a.num_q_heads / a.num_kv_heads;
-  Launch l = a.dtype == RKV_BF16 ? pick_d<uint16_t>(a.head_dim, G) : pick_d<float>(a.head_dim, G);
+
+  Launch l = a.dtype == RKV_BF16 ? pick_d<uint16_t>(a.head_dim, G, a.num_kv_heads)
+                                  : pick_d<float>(a.head_dim, G, a.num_kv_heads);
   if (!l.kernel) return fail(RKV_ERR_UNSUPPORTED, "no decode kernel for this shape");
   float *acc = nullptr, *ml = nullptr;
   if (max_parts > 1) split_ws(a.workspace, a.num_seqs, a.num_q_heads, a.head_dim, max_parts, acc, ml);
   const int cap = ctx_cap_of(a.max_context, a.max_blocks_per_seq, a.block_size);
-  dim3 grid((unsigned)max_parts, (unsigned)a.num_kv_heads, (unsigned)a.num_seqs);
+  dim3 grid = l.khw ? dim3((unsigned)(a.num_kv_heads / l.khw), (unsigned)max_parts,
+                           (unsigned)a.num_seqs)
+                    : dim3((unsigned)max_parts, (unsigned)a.num_kv_heads, (unsigned)a.num_seqs);
   hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), 0, a.stream, a.out, acc, ml, a.q, a.k_pool,
                      a.v_pool, a.block_tables, a.max_blocks_per_seq, a.ctx_lens, cap,
                      a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts);
@@ -445,18 +873,19 @@ int launch_merge(float* out, const int32_t* ctx_lens, int num_seqs, int num_q_he
   float *acc = nullptr, *ml = nullptr;
   split_ws(ws, num_seqs, num_q_heads, head_dim, max_parts, acc, ml);
   dim3 grid((unsigned)num_q_heads, (unsigned)num_seqs);
+  const size_t lds = (size_t)max_parts * sizeof(float);
   switch (head_dim) {
     case 32:
-      decode_merge_kernel<32><<<grid, 64, 0, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
+      decode_merge_kernel<32><<<grid, 64, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
                                                        kP, max_parts);
       break;
     case 64:
-      decode_merge_kernel<64><<<grid, 64, 0, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
+      decode_merge_kernel<64><<<grid, 64, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
                                                        kP, max_parts);
       break;
     default:
-      decode_merge_kernel<128><<<grid, 128, 0, stream>>>(out, acc, ml, ctx_lens, cap,
-                                                         num_q_heads, kP, max_parts);
+      decode_merge_kernel<128><<<grid, 64, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
+                                                        kP, max_parts);
       break;
   }
   return check_launch("decode_merge_kernel");
@@ -512,11 +941,13 @@ extern "C" int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens,
   if (head_dim != 32 && head_dim != 64 && head_dim != 128)
     return fail(RKV_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128");
   if (partition_size > 0 && partition_size != kP)
-    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be 256 (or <= 0 for the default)");
+    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
   if (num_seqs > 65535 || num_q_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_q_heads must be <= 65535");
   const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
   const int max_parts = cap <= 0 ? 1 : (cap + kP - 1) / kP;
+  if (max_parts > kMaxMergeParts)
+    return fail(RKV_ERR_UNSUPPORTED, "max_context / partition size above 4096 partitions");
   if (max_parts <= 1 || num_seqs == 0) return RKV_OK;
   if (!out || !ctx_lens) return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
   const size_t need = ws_bytes(num_seqs, num_q_heads, head_dim, max_parts);
