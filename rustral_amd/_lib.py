@@ -13,6 +13,7 @@ from .build import LIB_PATH
 RKV_F32, RKV_BF16 = 0, 1
 RKV_OK = 0
 RKV_ERR_INVALID_ARG, RKV_ERR_UNSUPPORTED, RKV_ERR_WORKSPACE, RKV_ERR_HIP = -1, -2, -3, -4
+RKV_ERR_OOM = -5
 
 # Every symbol include/rustral_kv.h declares, with (restype, argtypes).
 _p, _i, _i64, _f, _sz = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
@@ -30,6 +31,30 @@ SIGNATURES = {
     "rkv_decode_attention_partitions": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
                                              _i64, _i, _f, _i, _i, _p, _sz, _p]),
     "rkv_decode_attention_merge": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    # include/rustral_serving.h (host memory)
+    "rkv_bm_create": (_p, [_i64, _i]),
+    "rkv_bm_destroy": (None, [_p]),
+    "rkv_bm_allocate": (_i64, [_p, _i64, _i64, _p, _i64]),
+    "rkv_bm_reserve": (_i64, [_p, _i64, _i64]),
+    "rkv_bm_free": (_i64, [_p, _i64]),
+    "rkv_bm_num_free": (_i64, [_p]),
+    "rkv_bm_num_blocks": (_i64, [_p]),
+    "rkv_bm_block_size": (_i, [_p]),
+    "rkv_bm_table": (_i64, [_p, _i64, _p, _i64]),
+    "rkv_bm_free_list": (_i64, [_p, _p, _i64]),
+    "rkv_bm_fill_tables": (_i, [_p, _p, _i, _p, _i]),
+    "rkv_bm_plan_compaction": (_i64, [_p, _i64, _p, _i64]),
+    "rkv_sched_create": (_p, [_i64, _i, _i, _i]),
+    "rkv_sched_destroy": (None, [_p]),
+    "rkv_sched_add_request": (_i64, [_p, _p, _i, _i, _i]),
+    "rkv_sched_schedule": (_i, [_p]),
+    "rkv_sched_batch_dims": (_i, [_p, _p, _p, _p]),
+    "rkv_sched_batch": (_i, [_p, _p, _p, _p, _p, _p, _p, _i]),
+    "rkv_sched_update": (_i, [_p, _p, _p, _i]),
+    "rkv_sched_stats": (_i, [_p, _p]),
+    "rkv_sched_generated": (_i64, [_p, _i64, _p, _i64]),
+    "rkv_sched_block_manager": (_p, [_p]),
+    "rkv_sampler_greedy": (_i, [_p, _i]),
 }
 
 
