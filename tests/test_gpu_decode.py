@@ -106,12 +106,13 @@ def test_decode_block_permutation_invariance_bitexact(dev):
     assert np.array_equal(a, b)
 
 
-def test_decode_invalid_blocks_and_context_clamp(dev):
-    say("decode invalid block ids / clamp")
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_decode_invalid_blocks_and_context_clamp(dev, dtype):
+    say(f"decode invalid block ids / clamp dtype={dtype}")
     rng = np.random.default_rng(7)
     hkv, bs, d, hq = 2, 16, 64, 4
     ctx = np.int32([300, 5000])  # 5000 > max_blocks*bs: clamped to 320
-    q, kp, vp, _, _, tables = case(7, 2, hq, hkv, d, np.int32([320, 320]), "f32")
+    q, kp, vp, _, _, tables = case(7, 2, hq, hkv, d, np.int32([320, 320]), dtype)
     tables[0, 4] = -1          # invalid ids: those tokens are left out
     tables[0, 7] = 10 ** 6
     scale = 0.125
@@ -170,3 +171,31 @@ def test_decode_two_passes_match_fused_call(dev):
     kv.decode_attention(*args, 0.1, max_context=3008, out=b, workspace=ws, passes="merge")
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (8, 8, 64), (16, 2, 32)])
+def test_decode_many_sequences_with_empty_ones(dev, hq, hkv, d):
+    """More than 64 sequences (the work plan scans lengths 64 at a time),
+    empty sequences between long ones, lengths on tile boundaries."""
+    say(f"decode many sequences hq={hq} hkv={hkv} d={d}")
+    rng = np.random.default_rng(hq * 7 + d)
+    ctx = rng.integers(0, 700, size=300).astype(np.int32)
+    ctx[::7] = 0
+    ctx[3::11] = 16 * rng.integers(1, 40, size=len(ctx[3::11]))
+    ctx[5] = 1
+    q, kp, vp, _, _, tables = case(9, len(ctx), hq, hkv, d, ctx, "bf16")
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    got = run_gpu(dev, q, kp, vp, tables, ctx, scale)
+    want = oracle.decode_attention(q, kp, vp, tables, ctx, scale, n_threads=16)
+    assert_allclose_ref(got, want, RTOL, ATOL, "many sequences vs oracle")
+    assert not got[ctx == 0].any()
+
+
+def test_decode_is_deterministic(dev):
+    say("decode run-to-run determinism")
+    rng = np.random.default_rng(10)
+    ctx = contexts(rng, 40, 1, 5000)
+    q, kp, vp, _, _, tables = case(10, 40, 32, 8, 128, ctx, "bf16")
+    a = run_gpu(dev, q, kp, vp, tables, ctx, 0.09)
+    b = run_gpu(dev, q, kp, vp, tables, ctx, 0.09)
+    assert np.array_equal(a, b)
