@@ -1,0 +1,123 @@
+/*
+ * rustral_model.h -- the model glue around the paged-KV path in
+ * librustral_kv.so: the TensorOps subset a decoder step needs on the device,
+ * a greedy decoder built from them and the paged-KV
+ * entry points of rustral_kv.h, and the seeded parameter generator.
+ *
+ * Conventions are those of rustral_kv.h (device pointers unless marked host,
+ * opaque stream, int status + rkv_last_error()).  Every op is fp32 and sums
+ * in the order the reference's ndarray backend does (serial sums, no fused
+ * multiply-add), so linear, layer_norm, add and argmax give the same bits as
+ * that CPU path; gelu uses the device tanhf (within a few ulps of libm).
+ */
+#ifndef RUSTRAL_MODEL_H
+#define RUSTRAL_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- TensorOps subset ----------------------------------------------------- */
+
+/* out[t][i] = table[ids[t]][i] + pe[positions[t]][i].
+ * Replaces TensorOps::gather_rows (crates/ndarray-backend/src/lib.rs:462-475)
+ * followed by PositionalEncoding's add (crates/nn/src/transformer.rs:64-104).
+ * An id outside [0, vocab) or a position outside [0, max_len) gives a row of
+ * NaN (the reference returns CoreError::InvalidArgument).  pe may be NULL
+ * (no positional term). */
+int rkv_embed(float* out, const float* table, const int32_t* ids, const float* pe,
+              const int32_t* positions, int n_tokens, int vocab, int dim, int max_len,
+              void* stream);
+
+/* y[r][o] = sum_i x[r][i] * w[o][i] + b[o], the sum serial in i.
+ * Replaces TensorOps::linear (lib.rs:478-534) + add_row_vector (:318-341).
+ * w is [out_dim][in_dim] (the reference's Linear layout); b may be NULL. */
+int rkv_linear(float* y, const float* x, const float* w, const float* b, int rows, int in_dim,
+               int out_dim, void* stream);
+
+/* Per row: mean and biased variance by serial sums, then
+ * (x - mean) / sqrt(var + eps) * g + b.  Replaces LayerNorm::forward
+ * (crates/nn/src/normalization.rs:113-157).  dim <= 8192. */
+int rkv_layer_norm(float* y, const float* x, const float* g, const float* b, int rows, int dim,
+                   float eps, void* stream);
+
+/* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).  Replaces TensorOps::gelu
+ * (lib.rs:565-598). */
+int rkv_gelu(float* y, const float* x, int64_t n, void* stream);
+
+/* y = a + b element-wise.  Replaces TensorOps::add (lib.rs:283-315). */
+int rkv_add(float* y, const float* a, const float* b, int64_t n, void* stream);
+
+/* out[r] = index of the maximum of row r (n columns), the LAST one among
+ * equal maxima; NaN compares equal to everything, as in TensorOps::argmax
+ * (lib.rs:430-437) and Sampler::greedy (crates/nn/src/continuous_batching.rs:
+ * 458-462), i.e. the result is that of a left-to-right scan that moves to
+ * element i unless the current best is greater. */
+int rkv_argmax(int32_t* out, const float* x, int rows, int n, void* stream);
+
+/* ---- greedy decoder ------------------------------------
+ * Pre-LN causal decoder: x = E[id] + PE[pos]; per layer h = LN1(x),
+ * q,k,v = h W^T + b, K/V appended to a paged fp32 pool (16-token blocks from
+ * a host block manager), a = paged decode attention (rkv_decode_attention)
+ * W_o^T + b_o, x += a, x += W_2 gelu(W_1 LN2(x) + b_1) + b_2; logits =
+ * LN_f(x) W_lm^T; next id = argmax.  The prompt is fed one token per step
+ * (equal to a causal prefill: each step attends to the cache including
+ * itself).  Follows tape_transformer.rs:87-139 (per-head attention) and
+ * :209-247 (pre-LN block), transformer.rs:69-82 (PE) and :789 (lm_head
+ * without bias).
+ *
+ * Parameters: one fp32 host array, in this order (kvd = n_kv_heads*d_head):
+ *   embed[V][d]
+ *   per layer: ln1_g[d] ln1_b[d] wq[d][d] bq[d] wk[kvd][d] bk[kvd] wv[kvd][d]
+ *              bv[kvd] wo[d][d] bo[d] ln2_g[d] ln2_b[d] w1[f][d] b1[f]
+ *              w2[d][f] b2[d]
+ *   lnf_g[d] lnf_b[d] lm_head[V][d]                                          */
+typedef struct {
+  int vocab, d_model, n_heads, n_kv_heads, d_ff, n_layers, max_seq;
+  float eps;
+} rkv_decoder_config;
+
+typedef struct rkv_decoder rkv_decoder;
+
+/* Floats in the parameter array of a configuration (-1 if invalid). */
+int64_t rkv_decoder_param_count(const rkv_decoder_config* cfg);
+
+/* Random initialisation (host): every weight matrix and the embedding
+ * N(0, std^2) from one rkv_fill_normal stream (seed) in parameter order;
+ * layer-norm gains 1, biases and betas 0.  The reference's normal_parameter
+ * draws U[-scale, scale) from rand's StdRng (crates/ndarray-backend/src/
+ * lib.rs:132-146), which this build does not reproduce. */
+int rkv_decoder_init_params(const rkv_decoder_config* cfg, uint64_t seed, float std,
+                            float* host_params);
+
+/* Uploads host_params (rkv_decoder_param_count floats) and allocates the
+ * paged KV pools (ceil(max_seq / 16) blocks per layer) on the current
+ * device.  NULL on failure (rkv_last_error).  Supported: d_model / n_heads in
+ * {32, 64, 128}, n_heads / n_kv_heads in {1, 2, 4, 8}. */
+rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const float* host_params,
+                                int64_t n_params, void* stream);
+void rkv_decoder_destroy(rkv_decoder* dec);
+
+/* Greedy generation of n_new tokens after n_prompt prompt ids (host arrays).
+ * out_tokens: host [n_new]; out_logits: host [n_new][vocab] or NULL.
+ * n_prompt + n_new - 1 <= max_seq.  Synchronizes the stream at the end. */
+int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int n_prompt, int n_new,
+                         int32_t* out_tokens, float* out_logits);
+
+/* ---- seeded generator (host) -------------------------------------------------
+ * PCG64 (XSL-RR 128/64; state' = state * 0x2360ED051FC65DA44385DF649FCCF645
+ * + inc, output from state') with state = seed and inc = 0xDA3E39CB94B95BDB *
+ * 2 + 1, the stream numpy's PCG64 gives with that state; uniforms
+ * u = (x >> 11) * 2^-53; normals by Box-Muller in double,
+ * sqrt(-2 ln(1 - u1)) * (cos, sin)(2 pi u2), both used, rounded to fp32
+ * after scaling by std. */
+int rkv_rng_raw(uint64_t seed, uint64_t* out, int64_t n);
+int rkv_fill_normal(float* out, int64_t n, uint64_t seed, float std);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RUSTRAL_MODEL_H */

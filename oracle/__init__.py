@@ -63,7 +63,14 @@ def _declare(L):
     L.orc_decode_partials.argtypes = [_p, _p] + dec + [C.c_int, C.c_int]
     L.orc_splitk_merge.argtypes = [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int,
                                    C.c_int, C.c_int, C.c_int]
-    for name in ("orc_append", "orc_gather", "orc_copy_blocks", "orc_decode_attention",
+    L.orc_decoder_param_count.restype = _i64
+    L.orc_decoder_param_count.argtypes = [_p]
+    L.orc_linear.argtypes = [_p, _p, _p, _p, C.c_int, C.c_int, C.c_int]
+    L.orc_layer_norm.argtypes = [_p, _p, _p, _p, C.c_int, C.c_int, _f32]
+    L.orc_gelu.argtypes = [_p, _p, _i64]
+    L.orc_positional_encoding.argtypes = [_p, C.c_int, C.c_int]
+    L.orc_decoder_generate.argtypes = [_p, _p, _p, C.c_int, C.c_int, _p, _p]
+    for name in ("orc_decoder_generate", "orc_append", "orc_gather", "orc_copy_blocks", "orc_decode_attention",
                  "orc_decode_attention_f64", "orc_decode_attention_mt", "orc_decode_partials",
                  "orc_splitk_merge"):
         getattr(L, name).restype = C.c_int
@@ -220,3 +227,73 @@ def decode_splitk(q, k_pool, v_pool, block_tables, ctx_lens, scale, partition_si
     _check(lib().orc_splitk_merge(_ptr(out), _ptr(m), _ptr(l), _ptr(acc), _ptr(keep[2]), mbs, bs,
                                   B, hq, d, partition_size, max_parts), "orc_splitk_merge")
     return out, (m, l, acc)
+
+
+# ---- config-0 decoder ----------------------------------------------------------
+
+class DecoderConfig(C.Structure):
+    """orc_decoder_config (rkv_oracle.h); the same field order as the product's
+    rkv_decoder_config."""
+    _fields_ = [("vocab", C.c_int), ("d_model", C.c_int), ("n_heads", C.c_int),
+                ("n_kv_heads", C.c_int), ("d_ff", C.c_int), ("n_layers", C.c_int),
+                ("max_seq", C.c_int), ("eps", C.c_float)]
+
+
+# BASELINE configs[0]: 2 layers, d_model 128, 4 heads (head_dim 32), MLP 512,
+# vocab 1000; 32 prompt ids + 64 greedy tokens = 96 positions.
+CONFIG0 = dict(vocab=1000, d_model=128, n_heads=4, n_kv_heads=4, d_ff=512, n_layers=2,
+               max_seq=128, eps=1e-5)
+
+
+def decoder_config(**kw) -> DecoderConfig:
+    d = dict(CONFIG0)
+    d.update(kw)
+    return DecoderConfig(**d)
+
+
+def decoder_param_count(cfg: DecoderConfig) -> int:
+    return int(lib().orc_decoder_param_count(C.byref(cfg)))
+
+
+def linear(x, w, b=None):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    rows, in_dim = x.shape
+    out_dim = w.shape[0]
+    y = np.empty((rows, out_dim), np.float32)
+    lib().orc_linear(_ptr(y), _ptr(x), _ptr(w),
+                     None if b is None else _ptr(np.ascontiguousarray(b, np.float32)),
+                     rows, in_dim, out_dim)
+    return y
+
+
+def layer_norm(x, g, b, eps=1e-5):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_layer_norm(_ptr(y), _ptr(x), _ptr(np.ascontiguousarray(g, np.float32)),
+                         _ptr(np.ascontiguousarray(b, np.float32)), x.shape[0], x.shape[1], eps)
+    return y
+
+
+def gelu(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_gelu(_ptr(y), _ptr(x), x.size)
+    return y
+
+
+def positional_encoding(max_len, d_model):
+    pe = np.empty((max_len, d_model), np.float32)
+    lib().orc_positional_encoding(_ptr(pe), max_len, d_model)
+    return pe
+
+
+def decoder_generate(cfg: DecoderConfig, params, prompt, n_new, *, logits=False):
+    params = np.ascontiguousarray(params, np.float32)
+    assert params.size == decoder_param_count(cfg)
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    toks = np.empty(n_new, np.int32)
+    lg = np.empty((n_new, cfg.vocab), np.float32) if logits else None
+    _check(lib().orc_decoder_generate(C.byref(cfg), _ptr(params), _ptr(prompt), len(prompt),
+                                      n_new, _ptr(toks), _ptr(lg)), "orc_decoder_generate")
+    return (toks, lg) if logits else toks

@@ -470,3 +470,165 @@ int orc_decode_attention_mt(float* out, const float* q, const void* k_pool, cons
   free(th);
   return rc;
 }
+
+/* ---- config-0 decoder ----------------------------------------------------- */
+
+int64_t orc_decoder_param_count(const orc_decoder_config* c) {
+  const int64_t d = c->d_model, V = c->vocab, f = c->d_ff;
+  const int64_t kvd = (int64_t)c->n_kv_heads * (d / c->n_heads);
+  const int64_t per_layer = 2 * d + (d * d + d) + 2 * (kvd * d + kvd) + (d * d + d) + 2 * d +
+                            (f * d + f) + (d * f + d);
+  return V * d + c->n_layers * per_layer + 2 * d + V * d;
+}
+
+void orc_linear(float* y, const float* x, const float* w, const float* b, int rows, int in_dim,
+                int out_dim) {
+  for (int r = 0; r < rows; ++r)
+    for (int o = 0; o < out_dim; ++o) {
+      float sum = 0.0f; /* sum += x * w, in order (lib.rs:519-525) */
+      for (int i = 0; i < in_dim; ++i) sum += x[(int64_t)r * in_dim + i] * w[(int64_t)o * in_dim + i];
+      y[(int64_t)r * out_dim + o] = b ? sum + b[o] : sum;
+    }
+}
+
+void orc_layer_norm(float* y, const float* x, const float* g, const float* b, int rows, int dim,
+                    float eps) {
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (int64_t)r * dim;
+    float sum = 0.0f;
+    for (int i = 0; i < dim; ++i) sum += xr[i];
+    const float mean = sum / (float)dim;
+    float vs = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+      const float t = xr[i] - mean;
+      vs += t * t; /* powi(2) */
+    }
+    const float var = vs / (float)dim;
+    const float sd = sqrtf(var + eps);
+    for (int i = 0; i < dim; ++i) y[(int64_t)r * dim + i] = (xr[i] - mean) / sd * g[i] + b[i];
+  }
+}
+
+void orc_gelu(float* y, const float* x, int64_t n) {
+  const float k = sqrtf(2.0f / 3.14159265358979323846f);
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = x[i];
+    const float x3 = v * v * v;
+    const float xp = v + 0.044715f * x3;
+    const float t = tanhf(k * xp);
+    y[i] = 0.5f * v * (1.0f + t);
+  }
+}
+
+void orc_positional_encoding(float* pe, int max_len, int d_model) {
+  for (int pos = 0; pos < max_len; ++pos)
+    for (int i = 0; i < d_model; ++i) {
+      const float angle = (float)pos / powf(10000.0f, (float)(2 * (i / 2)) / (float)d_model);
+      pe[(int64_t)pos * d_model + i] = (i % 2 == 0) ? sinf(angle) : cosf(angle);
+    }
+}
+
+int orc_decoder_generate(const orc_decoder_config* c, const float* params,
+                         const int32_t* prompt, int n_prompt, int n_new, int32_t* out_tokens,
+                         float* out_logits) {
+  if (!c || !params || !prompt || !out_tokens || n_prompt < 1 || n_new < 0) return -1;
+  if (n_new == 0) return 0;
+  const int d = c->d_model, V = c->vocab, f = c->d_ff, H = c->n_heads, Hk = c->n_kv_heads;
+  if (d % H || H % Hk) return -1;
+  const int dh = d / H, kvd = Hk * dh, G = H / Hk;
+  const int total = n_prompt + (n_new > 0 ? n_new - 1 : 0);
+  if (total > c->max_seq) return -1;
+  const float scale = 1.0f / sqrtf((float)dh); /* tape_transformer.rs:75 */
+
+  float* pe = malloc(sizeof(float) * (size_t)c->max_seq * d);
+  float* kc = malloc(sizeof(float) * (size_t)c->n_layers * c->max_seq * kvd);
+  float* vc = malloc(sizeof(float) * (size_t)c->n_layers * c->max_seq * kvd);
+  float* x = malloc(sizeof(float) * d);
+  float* h = malloc(sizeof(float) * d);
+  float* q = malloc(sizeof(float) * d);
+  float* o = malloc(sizeof(float) * d);
+  float* a = malloc(sizeof(float) * d);
+  float* ff = malloc(sizeof(float) * f);
+  float* ff2 = malloc(sizeof(float) * f);
+  float* s = malloc(sizeof(float) * c->max_seq);
+  float* logits = malloc(sizeof(float) * V);
+  if (!pe || !kc || !vc || !x || !h || !q || !o || !a || !ff || !ff2 || !s || !logits) return -1;
+  orc_positional_encoding(pe, c->max_seq, d);
+
+  int32_t cur = prompt[0];
+  int produced = 0;
+  for (int pos = 0; pos < total; ++pos) {
+    const float* emb = params + (int64_t)cur * d;
+    for (int i = 0; i < d; ++i) x[i] = emb[i] + pe[(int64_t)pos * d + i];
+    const float* p = params + (int64_t)V * d;
+    for (int l = 0; l < c->n_layers; ++l) {
+      const float *ln1g = p, *ln1b = p + d;
+      p += 2 * d;
+      const float *wq = p, *bq = p + (int64_t)d * d;
+      p += (int64_t)d * d + d;
+      const float *wk = p, *bk = p + (int64_t)kvd * d;
+      p += (int64_t)kvd * d + kvd;
+      const float *wv = p, *bv = p + (int64_t)kvd * d;
+      p += (int64_t)kvd * d + kvd;
+      const float *wo = p, *bo = p + (int64_t)d * d;
+      p += (int64_t)d * d + d;
+      const float *ln2g = p, *ln2b = p + d;
+      p += 2 * d;
+      const float *w1 = p, *b1 = p + (int64_t)f * d;
+      p += (int64_t)f * d + f;
+      const float *w2 = p, *b2 = p + (int64_t)d * f;
+      p += (int64_t)d * f + d;
+
+      float* kl = kc + ((int64_t)l * c->max_seq + pos) * kvd;
+      float* vl = vc + ((int64_t)l * c->max_seq + pos) * kvd;
+      orc_layer_norm(h, x, ln1g, ln1b, 1, d, c->eps);
+      orc_linear(q, h, wq, bq, 1, d, d);
+      orc_linear(kl, h, wk, bk, 1, d, kvd);
+      orc_linear(vl, h, wv, bv, 1, d, kvd);
+      for (int hh = 0; hh < H; ++hh) { /* per head, as tape_transformer.rs:98-128 */
+        const int kh = hh / G;
+        float mx = -INFINITY;
+        for (int j = 0; j <= pos; ++j) {
+          const float* kj = kc + ((int64_t)l * c->max_seq + j) * kvd + kh * dh;
+          float dot = 0.0f;
+          for (int e = 0; e < dh; ++e) dot += q[hh * dh + e] * kj[e];
+          s[j] = dot * scale;
+          mx = fmaxf(mx, s[j]);
+        }
+        float sum = 0.0f;
+        for (int j = 0; j <= pos; ++j) {
+          s[j] = expf(s[j] - mx);
+          sum += s[j];
+        }
+        const float inv = 1.0f / sum;
+        for (int e = 0; e < dh; ++e) o[hh * dh + e] = 0.0f;
+        for (int j = 0; j <= pos; ++j) {
+          const float pj = s[j] * inv;
+          const float* vj = vc + ((int64_t)l * c->max_seq + j) * kvd + kh * dh;
+          for (int e = 0; e < dh; ++e) o[hh * dh + e] += pj * vj[e];
+        }
+      }
+      orc_linear(a, o, wo, bo, 1, d, d);
+      for (int i = 0; i < d; ++i) x[i] = x[i] + a[i];
+      orc_layer_norm(h, x, ln2g, ln2b, 1, d, c->eps);
+      orc_linear(ff, h, w1, b1, 1, d, f);
+      orc_gelu(ff2, ff, f);
+      orc_linear(a, ff2, w2, b2, 1, f, d);
+      for (int i = 0; i < d; ++i) x[i] = x[i] + a[i];
+    }
+    const float *lnfg = p, *lnfb = p + d, *wlm = p + 2 * d;
+    if (pos + 1 < n_prompt) {
+      cur = prompt[pos + 1];
+      continue;
+    }
+    orc_layer_norm(h, x, lnfg, lnfb, 1, d, c->eps);
+    orc_linear(logits, h, wlm, NULL, 1, d, V);
+    const int32_t next = (int32_t)orc_argmax(logits, V);
+    if (out_logits) memcpy(out_logits + (int64_t)produced * V, logits, sizeof(float) * V);
+    out_tokens[produced++] = next;
+    cur = next;
+  }
+  free(pe); free(kc); free(vc); free(x); free(h); free(q); free(o); free(a);
+  free(ff); free(ff2); free(s); free(logits);
+  return 0;
+}

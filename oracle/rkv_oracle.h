@@ -18,7 +18,8 @@
  * Token position p of a sequence lives in block block_table[p / block_size]
  * at row p % block_size.  Query head h reads KV head h / (Hq / Hkv).
  *
- * Pinning status of every function is listed in oracle/README.md.
+ * How each function is pinned is listed in the tests (tests/test_oracle.py,
+ * tests/test_model.py).
  */
 #ifndef RKV_ORACLE_H
 #define RKV_ORACLE_H
@@ -130,6 +131,58 @@ int orc_decode_attention_mt(float* out, const float* q, const void* k_pool, cons
                             const int32_t* ctx_lens, int num_seqs, int num_q_heads,
                             int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
                             float scale, int pool_dtype, int n_threads);
+
+/* ---- config-0 decoder: the model glue around the path ------------------
+ * A pre-LN causal decoder with KV-cached single-token steps:
+ *   x = E[id] + PE[pos]                  Embedding gather_rows (lib.rs:462-475),
+ *                                        sinusoidal PE (transformer.rs:69-82)
+ *   per layer:  h = LN1(x); q,k,v = h W^T + b; cache k,v at pos;
+ *               a = MHA(q, cache[0..pos]) W_o^T + b_o;  x = x + a
+ *               h = LN2(x); x = x + (gelu(h W_1^T + b_1)) W_2^T + b_2
+ *                                        (tape_transformer.rs:209-247 block order,
+ *                                        :87-139 per-head attention)
+ *   logits = LN_f(x) W_lm^T              (lm_head has no bias, transformer.rs:789)
+ *   next = argmax(logits)                (orc_argmax)
+ * The prompt is fed one token per step (equal to a causal prefill).
+ * Parameters are one float array in this order (kvd = n_kv_heads * d_head):
+ *   embed[V][d]
+ *   per layer: ln1_g[d] ln1_b[d] wq[d][d] bq[d] wk[kvd][d] bk[kvd] wv[kvd][d]
+ *              bv[kvd] wo[d][d] bo[d] ln2_g[d] ln2_b[d] w1[f][d] b1[f]
+ *              w2[d][f] b2[d]
+ *   lnf_g[d] lnf_b[d] lm_head[V][d]
+ * Weights are [out][in] as the reference's Linear stores them. */
+typedef struct {
+  int vocab, d_model, n_heads, n_kv_heads, d_ff, n_layers, max_seq;
+  float eps;
+} orc_decoder_config;
+
+int64_t orc_decoder_param_count(const orc_decoder_config* c);
+
+/* CpuOps::linear (lib.rs:478-534): y[r][o] = sum_i x[r][i] * w[o][i], summed
+ * serially in i without fused multiply-add, then add_row_vector (:318-341)
+ * of b (skipped if b is NULL). */
+void orc_linear(float* y, const float* x, const float* w, const float* b, int rows, int in_dim,
+                int out_dim);
+
+/* LayerNorm::forward (crates/nn/src/normalization.rs:113-157): per row,
+ * mean = serial sum / n, var = serial sum of (x-mean)^2 / n,
+ * y = (x - mean) / sqrt(var + eps) * g + b. */
+void orc_layer_norm(float* y, const float* x, const float* g, const float* b, int rows, int dim,
+                    float eps);
+
+/* CpuOps::gelu (lib.rs:565-598), tanh form, element-wise. */
+void orc_gelu(float* y, const float* x, int64_t n);
+
+/* PositionalEncoding::new (crates/nn/src/transformer.rs:69-82): pe[pos][i] =
+ * sin or cos of pos / 10000^(2*(i/2)/d), in fp32. */
+void orc_positional_encoding(float* pe, int max_len, int d_model);
+
+/* Greedy generation: feeds n_prompt prompt ids, then n_new - 1 generated ids,
+ * writing the n_new generated ids (and, if out_logits != NULL, the logits
+ * [n_new][vocab] each was chosen from).  Returns 0, or -1 on bad args. */
+int orc_decoder_generate(const orc_decoder_config* c, const float* params,
+                         const int32_t* prompt, int n_prompt, int n_new, int32_t* out_tokens,
+                         float* out_logits);
 
 #ifdef __cplusplus
 }

@@ -55,6 +55,20 @@ SIGNATURES = {
     "rkv_sched_generated": (_i64, [_p, _i64, _p, _i64]),
     "rkv_sched_block_manager": (_p, [_p]),
     "rkv_sampler_greedy": (_i, [_p, _i]),
+    # include/rustral_model.h
+    "rkv_embed": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "rkv_linear": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
+    "rkv_layer_norm": (_i, [_p, _p, _p, _p, _i, _i, _f, _p]),
+    "rkv_gelu": (_i, [_p, _p, _i64, _p]),
+    "rkv_add": (_i, [_p, _p, _p, _i64, _p]),
+    "rkv_argmax": (_i, [_p, _p, _i, _i, _p]),
+    "rkv_decoder_param_count": (_i64, [_p]),
+    "rkv_decoder_init_params": (_i, [_p, C.c_uint64, _f, _p]),
+    "rkv_decoder_create": (_p, [_p, _p, _i64, _p]),
+    "rkv_decoder_destroy": (None, [_p]),
+    "rkv_decoder_generate": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rkv_rng_raw": (_i, [C.c_uint64, _p, _i64]),
+    "rkv_fill_normal": (_i, [_p, _i64, C.c_uint64, _f]),
 }
 
 

@@ -1,0 +1,150 @@
+"""The model glue around the paged-KV path: device TensorOps subset, the
+greedy decoder of BASELINE configs[0], and the seeded parameter generator
+(include/rustral_model.h, implemented in csrc/model_ops.hip and
+csrc/decoder.hip).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from ._lib import RkvError, check, lib
+from .kv import _dev, _stream
+
+
+class DecoderConfig(C.Structure):
+    """rkv_decoder_config."""
+    _fields_ = [("vocab", C.c_int), ("d_model", C.c_int), ("n_heads", C.c_int),
+                ("n_kv_heads", C.c_int), ("d_ff", C.c_int), ("n_layers", C.c_int),
+                ("max_seq", C.c_int), ("eps", C.c_float)]
+
+
+# 2 layers, d_model 128, 4 heads x 32, MLP 512, vocab 1000.
+CONFIG0 = dict(vocab=1000, d_model=128, n_heads=4, n_kv_heads=4, d_ff=512, n_layers=2,
+               max_seq=128, eps=1e-5)
+
+
+def config(**kw) -> DecoderConfig:
+    d = dict(CONFIG0)
+    d.update(kw)
+    return DecoderConfig(**d)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def param_count(cfg: DecoderConfig) -> int:
+    n = lib().rkv_decoder_param_count(C.byref(cfg))
+    if n < 0:
+        raise ValueError("invalid decoder configuration")
+    return int(n)
+
+
+def init_params(cfg: DecoderConfig, seed: int = 0, std: float = 0.02) -> np.ndarray:
+    """Random parameters: N(0, std^2) weights in parameter order from one
+    seeded stream, unit layer-norm gains, zero biases."""
+    out = np.empty(param_count(cfg), np.float32)
+    check(lib().rkv_decoder_init_params(C.byref(cfg), seed, std, _p(out)))
+    return out
+
+
+def rng_raw(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    check(lib().rkv_rng_raw(seed, _p(out), n))
+    return out
+
+
+def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    check(lib().rkv_fill_normal(_p(out), n, seed, std))
+    return out
+
+
+class Decoder:
+    """Greedy decoder on the current device (rkv_decoder_*)."""
+
+    def __init__(self, cfg: DecoderConfig, params: np.ndarray, device=None):
+        params = np.ascontiguousarray(params, np.float32)
+        dev = torch.device("cuda:0") if device is None else torch.device(device)
+        self._stream = torch.cuda.current_stream(dev).cuda_stream
+        self.cfg = cfg
+        h = lib().rkv_decoder_create(C.byref(cfg), _p(params), params.size, self._stream)
+        if not h:
+            raise RkvError(-1, lib().rkv_last_error().decode())
+        self._h = h
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().rkv_decoder_destroy(self._h)
+            self._h = None
+
+    def generate(self, prompt, n_new: int, *, logits: bool = False):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        toks = np.empty(max(n_new, 1), np.int32)
+        lg = np.empty((max(n_new, 1), self.cfg.vocab), np.float32) if logits else None
+        check(lib().rkv_decoder_generate(self._h, _p(prompt), len(prompt), n_new, _p(toks),
+                                         None if lg is None else _p(lg)))
+        toks = toks[:n_new]
+        return (toks, lg[:n_new]) if logits else toks
+
+
+# ---- device ops on torch tensors ---------------------------------------------------
+
+def linear(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(x, "x", torch.float32), _dev(w, "w", torch.float32)
+    rows, in_dim = x.shape
+    out_dim = w.shape[0]
+    y = torch.empty((rows, out_dim), dtype=torch.float32, device=x.device)
+    check(lib().rkv_linear(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+                           None if b is None else _dev(b, "b", torch.float32).data_ptr(),
+                           rows, in_dim, out_dim, _stream(x)))
+    return y
+
+
+def layer_norm(x: torch.Tensor, g: torch.Tensor, b: torch.Tensor, eps: float = 1e-5):
+    _dev(x, "x", torch.float32)
+    y = torch.empty_like(x)
+    check(lib().rkv_layer_norm(y.data_ptr(), x.data_ptr(), g.data_ptr(), b.data_ptr(),
+                               x.shape[0], x.shape[1], eps, _stream(x)))
+    return y
+
+
+def gelu(x: torch.Tensor) -> torch.Tensor:
+    _dev(x, "x", torch.float32)
+    y = torch.empty_like(x)
+    check(lib().rkv_gelu(y.data_ptr(), x.data_ptr(), x.numel(), _stream(x)))
+    return y
+
+
+def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    _dev(a, "a", torch.float32), _dev(b, "b", torch.float32)
+    y = torch.empty_like(a)
+    check(lib().rkv_add(y.data_ptr(), a.data_ptr(), b.data_ptr(), a.numel(), _stream(a)))
+    return y
+
+
+def argmax(x: torch.Tensor) -> torch.Tensor:
+    _dev(x, "x", torch.float32)
+    rows, n = x.shape
+    out = torch.empty(rows, dtype=torch.int32, device=x.device)
+    check(lib().rkv_argmax(out.data_ptr(), x.data_ptr(), rows, n, _stream(x)))
+    return out
+
+
+def embed(table: torch.Tensor, ids: torch.Tensor, pe: torch.Tensor | None = None,
+          positions: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(table, "table", torch.float32), _dev(ids, "ids", torch.int32)
+    vocab, dim = table.shape
+    out = torch.empty((ids.numel(), dim), dtype=torch.float32, device=table.device)
+    check(lib().rkv_embed(out.data_ptr(), table.data_ptr(), ids.data_ptr(),
+                          None if pe is None else pe.data_ptr(),
+                          None if positions is None else positions.data_ptr(), ids.numel(), vocab,
+                          dim, 0 if pe is None else pe.shape[0], _stream(table)))
+    return out
+
+
+__all__ = ["DecoderConfig", "CONFIG0", "config", "param_count", "init_params", "rng_raw",
+           "fill_normal", "Decoder", "linear", "layer_norm", "gelu", "add", "argmax", "embed"]
