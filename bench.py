@@ -43,6 +43,10 @@ def parse():
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(nproc, 16)")
     p.add_argument("--copy-only", action="store_true",
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
+    p.add_argument("--workload", default="config2",
+                   choices=["config1", "config2", "config3", "config4"],
+                   help="config2 (default): the headline decode line; the others print "
+                        "their own line (BASELINE.json configs[1], [3], [4])")
     return p.parse_args()
 
 
@@ -129,23 +133,322 @@ def cpu_baseline(torch, layers, ctx, threads):
 
 
 def traffic_from_profiles():
+    """HBM bytes per launch of the partition kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a 1 GiB copy)."""
     p = os.path.join(ROOT, "profiles", "decode_config2_traffic.json")
     if os.path.exists(p):
         with open(p) as f:
-            return json.load(f)
+            return json.load(f).get("traffic_bytes_per_launch")
     return None
+
+
+# ---- other BASELINE configs (one JSON line each; not the headline) ---------------
+
+def _timed(torch, fn, reps):
+    """Average ms of fn() over reps calls, HIP events on the current stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _line(metric, value, unit, ms, args, dtype, config, **extra):
+    d = {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1,
+         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+         "data": "synthetic", "config": config}
+    d["pct_hbm_peak"] = round(100 * value / HBM_PEAK_GBPS, 2) if unit == "GB/s" else None
+    d.update(extra)
+    return d
+
+
+def run_config1(torch, dev, args):
+    """32 layers, Hkv 8, D 128, BS 16; 64 sequences each appending
+    one token per step into a 65,536-block pool (random tables), gather of
+    contexts U[512, 4096].  bf16: 32 distinct layer pools (128 GiB);
+    fp32: 16 layer pools (128 GiB; 32 would not fit next to the rest)."""
+    import numpy as np
+    from rustral_amd import kv
+    rng = np.random.default_rng(1)
+    nb, hkv, bs, d, B = 65536, HKV, BS, D, 64
+    ctx = rng.integers(512, 4096 + 1, size=B).astype(np.int32)
+    need = (ctx + bs - 1) // bs
+    mbs = 4096 // bs + 1
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.full((B, mbs), -1, np.int32)
+    o = 0
+    for b in range(B):
+        n = int(need[b]) + 2                       # room for 16+ appended tokens
+        tables[b, :n] = perm[o:o + n]
+        o += n
+    res = {}
+    for dtype, n_layers in (("bf16", 32), ("f32", 16)):
+        tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+        s_pool = 2 if dtype == "bf16" else 4
+        kp = torch.empty((n_layers, nb, hkv, bs, d), dtype=tdt, device=dev)
+        vp = torch.empty_like(kp)
+        g = torch.Generator(device=dev).manual_seed(1)
+        kn = torch.randn((n_layers, B, hkv, d), generator=g, device=dev)
+        vn = torch.randn((n_layers, B, hkv, d), generator=g, device=dev)
+        steps = max(args.steps, 4)
+        slot_sets = []
+        for s in range(16):                       # token L + s of every sequence, cycled
+            p = ctx + s
+            slot_sets.append(torch.from_numpy(
+                tables[np.arange(B), p // bs].astype(np.int64) * bs + p % bs).to(dev))
+        it = iter(range(10 ** 9))
+        def app():
+            i = next(it) % len(slot_sets)
+            kv.append(kp, vp, kn, vn, slot_sets[i])
+        for _ in range(args.warmup):
+            app()
+        ms_app = _timed(torch, app, steps)
+        app_bytes = n_layers * B * hkv * d * 2 * (4 + s_pool) + B * 8
+        # bulk: the 16 steps' tokens (1024 per layer) in one launch, as a
+        # prefill or a batch of queued steps would append them
+        knb = torch.randn((n_layers, 16 * B, hkv, d), generator=g, device=dev)
+        vnb = torch.randn_like(knb)
+        bulk_slots = torch.cat(slot_sets)
+        def bulk():
+            kv.append(kp, vp, knb, vnb, bulk_slots)
+        bulk()
+        ms_bulk = _timed(torch, bulk, steps)
+        bulk_bytes = n_layers * 16 * B * hkv * d * 2 * (4 + s_pool) + 16 * B * 8
+        del knb, vnb
+        gt, gc = torch.from_numpy(tables).to(dev), torch.from_numpy(ctx).to(dev)
+        offs = torch.from_numpy(np.concatenate([[0], np.cumsum(ctx.astype(np.int64) * hkv * d)[:-1]])).to(dev)
+        total = int(ctx.astype(np.int64).sum()) * hkv * d
+        outs = {}
+        for odt, name in ((tdt, "same"), (torch.float32, "f32")):
+            if name == "f32" and dtype == "f32":
+                continue
+            ko = torch.empty(total, dtype=odt, device=dev)
+            vo = torch.empty_like(ko)
+            li = iter(range(10 ** 9))
+            def gat():
+                l = next(li) % n_layers
+                kv.gather(kp[l], vp[l], gt, gc, out_offsets=offs, out_total=total, k_out=ko, v_out=vo)
+            gat()
+            ms_g = _timed(torch, gat, n_layers)
+            s_out = 2 if odt == torch.bfloat16 else 4
+            g_bytes = int(ctx.astype(np.int64).sum()) * hkv * d * 2 * (s_pool + s_out) + int(need.sum()) * 4
+            outs[name] = {"us_per_call": round(1e3 * ms_g, 2), "GBps": round(g_bytes / (ms_g * 1e-3) / 1e9, 1),
+                          "bytes_per_call": g_bytes}
+        res[dtype] = {"layers": n_layers, "append": {
+            "us_per_step": round(1e3 * ms_app, 2), "bytes_per_step": app_bytes,
+            "GBps": round(app_bytes / (ms_app * 1e-3) / 1e9, 1)},
+            "append_bulk_16_steps": {"us_per_launch": round(1e3 * ms_bulk, 2),
+                                     "bytes_per_launch": bulk_bytes,
+                                     "GBps": round(bulk_bytes / (ms_bulk * 1e-3) / 1e9, 1)},
+            "gather_packed": outs}
+        del kp, vp, kn, vn
+        torch.cuda.empty_cache()
+    a = res["bf16"]["append"]
+    gb = res["bf16"]["gather_packed"]["same"]
+    return _line("KV append GB/s per step (64 tokens x 32 layers, one launch), bf16 pool", a["GBps"],
+                 "GB/s", a["us_per_step"] / 1e3, args, "bf16",
+                 {"workload": "configs[1] KV append + gather microbench", "num_kv_heads": hkv,
+                  "head_dim": d, "block_size": bs, "pool_blocks": nb, "sequences": B,
+                  "context": [512, 4096]},
+                 gather_GBps_bf16=gb["GBps"],
+                 append_bulk_GBps_bf16=res["bf16"]["append_bulk_16_steps"]["GBps"], results=res)
+
+
+def _decode_layers(torch, dev, B, lo, hi, seed, n_layers):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(lo, hi + 1, size=B).astype(np.int32)
+    need = (ctx.astype(np.int64) + BS - 1) // BS
+    nb = int(need.sum())
+    mbs = (hi + BS - 1) // BS
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers = []
+    for _ in range(n_layers):
+        k = torch.randn((nb, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((nb, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
+        q = torch.randn((B, HQ, D), generator=g, device=dev)
+        perm = torch.randperm(nb, generator=g, device=dev).to(torch.int32).cpu().numpy()
+        tab = np.full((B, mbs), -1, np.int32)
+        o = 0
+        for b in range(B):
+            tab[b, :need[b]] = perm[o:o + need[b]]
+            o += int(need[b])
+        layers.append((q, k, v, torch.from_numpy(tab).to(dev)))
+    return layers, ctx, torch.from_numpy(ctx).to(dev), mbs * BS
+
+
+def run_config3(torch, dev, args):
+    """B 8, Hq 32, Hkv 8, D 128, bf16, contexts U[16384, 65536],
+    permuted blocks; two-pass split-K.  8 layer pools (10.7 GB) rotate so no
+    call re-reads the previous one's bytes from the 256 MB Infinity Cache."""
+    from rustral_amd import kv
+    n_layers = 8
+    layers, ctx, ctx_d, max_ctx = _decode_layers(torch, dev, 8, 16384, 65536, 3, n_layers)
+    ws = torch.empty(kv.workspace_bytes(8, HQ, D, max_ctx), dtype=torch.uint8, device=dev)
+    out = torch.empty((8, HQ, D), device=dev)
+    scale = 1.0 / math.sqrt(D)
+    it = iter(range(10 ** 9))
+    def call():
+        q, k, v, t = layers[next(it) % n_layers]
+        kv.decode_attention(q, k, v, t, ctx_d, scale, max_context=max_ctx, out=out, workspace=ws)
+    for _ in range(max(args.warmup, 1) * n_layers):
+        call()
+    reps = max(args.steps, 4) * n_layers
+    ms = _timed(torch, call, reps)
+    nbytes = algorithmic_bytes(ctx)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return _line("long-context split-K paged decode GB/s (% of HBM peak)", gbps, "GB/s", ms, args,
+                 "bf16", {"workload": "configs[3] long-context split-K decode", "batch": 8,
+                          "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "block_size": BS,
+                          "context": [16384, 65536], "mean_context": float(ctx.mean())},
+                 us_per_call=round(1e3 * ms, 2), algorithmic_bytes_per_call=nbytes,
+                 calls_timed=reps)
+
+
+def run_config4(torch, dev, args):
+    """continuous-batching step mix.  256 running sequences with
+    contexts U[1, 8192] (seed 4) in 32 layer pools of 80,000 blocks (bf16,
+    168 GB), blocks handed out one at a time round-robin by the host block
+    manager (so finished sequences leave holes).  One step: 10% of the
+    sequences finish (blocks freed), the block manager plans a compaction of
+    up to 25% of the live blocks and copy_blocks moves them (all layers, K and
+    V, one launch), 10% new sequences are admitted with 128-token prefills
+    appended in bulk (one launch for all layers), then one decode token for
+    every running sequence: append (one launch) + 32 decode-attention calls.
+    Hq = 32 (GQA 4:1) is assumed; BASELINE does not state it."""
+    import numpy as np
+    from rustral_amd import kv
+    from rustral_amd.serving import PagedCache
+    rng = np.random.default_rng(4)
+    n_layers, nblk, B, pre = 32, 80000, 256, 128
+    n_turn = B // 10                                 # finish / admit per step
+    blk_bytes = HKV * BS * D * 2
+    kp = torch.empty((n_layers, nblk, HKV, BS, D), dtype=torch.bfloat16, device=dev)
+    vp = torch.empty_like(kp)
+    kp.fill_(0.01), vp.fill_(-0.01)
+    cache = PagedCache(BS, nblk)
+    ctx = {i: int(c) for i, c in enumerate(rng.integers(1, 8192 + 1, size=B))}
+    next_id = B
+    pending = {i: -(-c // BS) for i, c in ctx.items()}
+    while pending:                                   # round-robin, one block at a time
+        for i in list(pending):
+            assert cache.allocate(i, BS) is not None
+            pending[i] -= 1
+            if pending[i] == 0:
+                del pending[i]
+    g = torch.Generator(device=dev).manual_seed(4)
+    kn_pre = torch.randn((n_layers, n_turn * pre, HKV, D), generator=g, device=dev)
+    vn_pre = torch.randn_like(kn_pre)
+    kn_dec = torch.randn((n_layers, B, HKV, D), generator=g, device=dev)
+    vn_dec = torch.randn_like(kn_dec)
+    q = torch.randn((B, HQ, D), generator=g, device=dev)
+    out = torch.empty_like(q)
+    ws = torch.empty(kv.workspace_bytes(B, HQ, D, 8192 + 64 * BS), dtype=torch.uint8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    steps = []
+    for step in range(args.warmup + max(args.steps, 3)):
+        t_host = time.perf_counter()
+        ids = sorted(ctx)
+        n_fin = n_turn
+        for i in rng.choice(ids, size=n_fin, replace=False).tolist():
+            cache.free(i)
+            del ctx[i]
+        live = sum(len(cache.table(i)) for i in ctx)
+        pairs = cache.plan_compaction(live // 4)
+        admitted = []
+        for _ in range(n_fin):
+            cache.allocate(next_id, pre)
+            ctx[next_id] = pre
+            admitted.append(next_id)
+            next_id += 1
+        slots_pre = np.concatenate([np.asarray(cache.table(i), np.int64)[np.arange(pre) // BS] * BS
+                                    + np.arange(pre) % BS for i in admitted])
+        ids = sorted(ctx)
+        for i in ids:                                  # room for the decode token
+            cache.reserve(i, ctx[i] + 1)
+        mb = max(len(cache.table(i)) for i in ids)
+        tables = cache.fill_tables(ids, mb)
+        cl = np.array([ctx[i] for i in ids], np.int32)
+        pos = cl.astype(np.int64)
+        slots_dec = tables[np.arange(len(ids)), pos // BS].astype(np.int64) * BS + pos % BS
+        for i in ids:
+            ctx[i] += 1
+        cl_after = cl + 1
+        d_pairs = torch.from_numpy(pairs.astype(np.int32)).to(dev)
+        d_spre = torch.from_numpy(slots_pre).to(dev)
+        d_sdec = torch.from_numpy(slots_dec).to(dev)
+        d_tab = torch.from_numpy(tables).to(dev)
+        d_ctx = torch.from_numpy(cl_after).to(dev)
+        n_pre = len(slots_pre)
+        torch.cuda.synchronize()
+        t_host = time.perf_counter() - t_host
+        e = [ev() for _ in range(5)]
+        e[0].record()
+        if len(pairs):
+            kv.copy_blocks(kp, vp, d_pairs)
+        e[1].record()
+        kv.append(kp, vp, kn_pre, vn_pre, d_spre)
+        e[2].record()
+        nb_ = len(ids)
+        assert nb_ == B and n_pre == n_turn * pre
+        kv.append(kp, vp, kn_dec, vn_dec, d_sdec)
+        e[3].record()
+        for l in range(n_layers):
+            kv.decode_attention(q, kp[l], vp[l], d_tab, d_ctx, scale,
+                                max_context=mb * BS, out=out, workspace=ws)
+        e[4].record()
+        torch.cuda.synchronize()
+        if step < args.warmup:
+            continue
+        ms = [e[i].elapsed_time(e[i + 1]) for i in range(4)]
+        copy_b = len(pairs) * n_layers * 2 * blk_bytes * 2
+        pre_b = n_pre * n_layers * HKV * D * 2 * (4 + 2) + n_pre * 8
+        dec_app_b = nb_ * n_layers * HKV * D * 2 * (4 + 2) + nb_ * 8
+        attn_b = n_layers * (int(cl_after.astype(np.int64).sum()) * HKV * D * 2 * 2
+                             + nb_ * HQ * D * 8 + int(sum(-(-c // BS) for c in cl_after)) * 4)
+        steps.append(dict(pairs=len(pairs), live_blocks=live, prefill_tokens=n_pre,
+                          running=nb_, ms=ms, host_ms=1e3 * t_host,
+                          bytes=[copy_b, pre_b, dec_app_b, attn_b]))
+    n = len(steps)
+    ms = np.array([s["ms"] for s in steps]).mean(0)
+    by = np.array([s["bytes"] for s in steps], np.float64).mean(0)
+    gbps = by / (ms * 1e-3) / 1e9
+    total_ms = float(ms.sum())
+    total_gbps = float(by.sum() / (total_ms * 1e-3) / 1e9)
+    comps = ["copy_blocks", "prefill_append", "decode_append", "decode_attention_32_layers"]
+    return _line("continuous-batching step GB/s (append + copy + decode attention)", total_gbps,
+                 "GB/s", total_ms, args, "bf16",
+                 {"workload": "configs[4] continuous-batching step mix", "running": B,
+                  "layers": n_layers, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
+                  "block_size": BS, "pool_blocks_per_layer": nblk, "prefill": pre},
+                 components={c: {"ms": round(float(m), 3), "GBps": round(float(gb), 1),
+                                 "bytes": int(b)} for c, m, gb, b in zip(comps, ms, gbps, by)},
+                 decode_tokens_per_s=round(float(np.mean([s["running"] for s in steps]))
+                                           / (total_ms * 1e-3), 1),
+                 steps_detail=[{k: v for k, v in s.items() if k != "bytes"} for s in steps[:n]])
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the path would shard by sequence or KV head, see DESIGN.md)", file=sys.stderr)
+              "(the path shards by sequence or KV head with no exchange, so the one-GPU "
+              "figure is the per-GPU figure)", file=sys.stderr)
         sys.exit(2)
     import torch
     from rustral_amd import kv
 
     dev = torch.device("cuda:0")
+    if args.workload != "config2":
+        line = {"config1": run_config1, "config3": run_config3,
+                "config4": run_config4}[args.workload](torch, dev, args)
+        print(json.dumps(line), flush=True)
+        return
     if args.copy_only:
         gbps = copy_bandwidth(torch, dev, nbytes=1 << 30, reps=5)
         print(json.dumps({"copy_bytes": 1 << 30, "reps": 6, "copy_GBps": round(gbps, 1)}))

@@ -631,49 +631,80 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
   }
 }
 
-// grid = (num_q_heads, num_seqs), one wave per (query head, sequence).
-// Partition statistics are read by all lanes at once (lane p holds
-// partition p, p + 64, ...), weights go through LDS, then every lane sums
-// D/64 output dims over the partitions with independent loads.
+// grid = (num_q_heads, num_seqs), one workgroup of kMergeWaves waves per
+// (query head, sequence).  All threads take the partition maxima and the
+// weights 2^(m_p - M) (kept in LDS); then lane l of a wave reads float4 c =
+// l % (D/4) of partition rows p = l / (D/4) + ..., so one wave instruction
+// covers 64 / (D/4) partitions (2 for D = 128) and the kMergeWaves waves
+// split the partitions; per-row sums meet through shuffles and LDS.
+constexpr int kMergeWaves = 4;
+
 template <int D>
-__global__ __launch_bounds__(64) void decode_merge_kernel(
+__global__ __launch_bounds__(64 * kMergeWaves) void decode_merge_kernel(
     float* __restrict__ out, const float* __restrict__ part_acc,
     const float* __restrict__ part_ml, const int32_t* __restrict__ ctx_lens, int ctx_cap,
     int num_q_heads, int P, int max_parts) {
-  constexpr int DPL = D < 64 ? 1 : D / 64;  // dims per lane
-  extern __shared__ float s_w[];            // max_parts weights (dynamic LDS)
-  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  constexpr int NT = 64 * kMergeWaves;
+  constexpr int V4 = D / 4;        // float4 per partition row
+  constexpr int RPW = 64 / V4;     // partition rows per wave instruction
+  extern __shared__ float s_w[];   // max_parts weights (dynamic LDS)
+  __shared__ float s_red[kMergeWaves];
+  __shared__ __align__(16) float s_acc[kMergeWaves][D];
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
   int L = ctx_lens[b];
   L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
   const int np = (L + P - 1) / P;
   if (np <= 1) return;
   const int64_t row0 = ((int64_t)b * num_q_heads + h) * max_parts;
   float M = -INFINITY;
-  for (int p = lane; p < np; p += 64) M = fmaxf(M, part_ml[(row0 + p) * 2]);
+  for (int p = tid; p < np; p += NT) M = fmaxf(M, part_ml[(row0 + p) * 2]);
   M = wave_max(M);
+  if (lane == 0) s_red[w] = M;
+  __syncthreads();
+  M = s_red[0];
+#pragma unroll
+  for (int x = 1; x < kMergeWaves; ++x) M = fmaxf(M, s_red[x]);
+  __syncthreads();
   float den = 0.0f;
-  for (int p = lane; p < np; p += 64) {
+  for (int p = tid; p < np; p += NT) {
     const float m = part_ml[(row0 + p) * 2];
     const float wgt = (m == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(m - M);
     s_w[p] = wgt;
     den = fmaf(wgt, part_ml[(row0 + p) * 2 + 1], den);
   }
   den = wave_sum(den);
+  if (lane == 0) s_red[w] = den;
   __syncthreads();
-  float num[DPL];
+  den = 0.0f;
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) num[j] = 0.0f;
-  if (lane * DPL < D) {
+  for (int x = 0; x < kMergeWaves; ++x) den += s_red[x];
+  // weighted sum of the acc rows
+  const int r = lane / V4, c = lane % V4;
+  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
-    for (int p = 0; p < np; ++p) {
-      const float wgt = s_w[p];
-      const float* a = part_acc + (row0 + p) * D + lane * DPL;
+  for (int p = w * RPW + r; p < np; p += kMergeWaves * RPW) {
+    const float wgt = s_w[p];
+    const float4 a = *reinterpret_cast<const float4*>(part_acc + (row0 + p) * D + 4 * c);
+    num.x = fmaf(wgt, a.x, num.x);
+    num.y = fmaf(wgt, a.y, num.y);
+    num.z = fmaf(wgt, a.z, num.z);
+    num.w = fmaf(wgt, a.w, num.w);
+  }
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) num[j] = fmaf(wgt, a[j], num[j]);
-    }
-    float* o = out + ((int64_t)b * num_q_heads + h) * D + lane * DPL;
+  for (int o = V4; o < 64; o <<= 1) {
+    num.x += __shfl_xor(num.x, o);
+    num.y += __shfl_xor(num.y, o);
+    num.z += __shfl_xor(num.z, o);
+    num.w += __shfl_xor(num.w, o);
+  }
+  if (r == 0) *reinterpret_cast<float4*>(&s_acc[w][4 * c]) = num;
+  __syncthreads();
+  for (int dd = tid; dd < D; dd += NT) {
+    float v = 0.0f;
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) o[j] = den > 0.0f ? num[j] / den : 0.0f;
+    for (int x = 0; x < kMergeWaves; ++x) v += s_acc[x][dd];
+    out[((int64_t)b * num_q_heads + h) * D + dd] = den > 0.0f ? v / den : 0.0f;
   }
 }
 
@@ -876,15 +907,15 @@ int launch_merge(float* out, const int32_t* ctx_lens, int num_seqs, int num_q_he
   const size_t lds = (size_t)max_parts * sizeof(float);
   switch (head_dim) {
     case 32:
-      decode_merge_kernel<32><<<grid, 64, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
+      decode_merge_kernel<32><<<grid, 64 * kMergeWaves, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
                                                        kP, max_parts);
       break;
     case 64:
-      decode_merge_kernel<64><<<grid, 64, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
+      decode_merge_kernel<64><<<grid, 64 * kMergeWaves, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
                                                        kP, max_parts);
       break;
     default:
-      decode_merge_kernel<128><<<grid, 64, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
+      decode_merge_kernel<128><<<grid, 64 * kMergeWaves, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
                                                         kP, max_parts);
       break;
   }
