@@ -1,24 +1,31 @@
 // paged_decode.hip -- single-token paged decode attention with GQA, split-K,
 // for gfx950 (CDNA4, wave64).
 //
-// Pass 1 (decode_partition_kernel): one workgroup per (partition of P tokens,
-// KV head, sequence).  The G = Hq/Hkv query heads that share a KV head are
-// served by the same workgroup, so every K/V byte is read from HBM once.
+// Pass 1 splits every sequence into partitions of P tokens and produces, per
+// (partition, query head), the partial softmax state (m, l, acc); the G =
+// Hq/Hkv query heads that share a KV head are served together, so every K/V
+// byte is read from HBM once.  Two implementations of pass 1 share the lane
+// mapping and the arithmetic:
+//   * decode_stream_kernel (the default): SPLIT waves per (partition, KV
+//     head, sequence), each streaming a slice of the partition's K and V
+//     tiles through a register ring, QK^T on the matrix cores for bf16
+//     pools; the waves combine their states in LDS.
+//   * decode_partition_kernel (RKV_DECODE_STREAM=0): NW waves that issue all
+//     their K and V loads before any arithmetic.
+// Common to both:
 //   * Lane mapping: a wave reads one (block, head) tile [BS][D] as NL
 //     coalesced 1 KiB loads: lane l takes 16 bytes of token row l / LPT at
 //     dims (l % LPT) * E ... + E, where E = 16 / sizeof(elem) and
 //     LPT = D / E lanes cover one row.
-//   * QK^T: each lane multiplies its E key elements with the matching E
-//     elements of the G (pre-scaled) queries held in registers, then a DPP
-//     sum over the LPT lanes of the row gives the G scores of that token.
-//   * Scores go to LDS; the workgroup takes the max and the sum of
-//     exp2(s - max) over the partition (two-pass softmax inside the
-//     partition: no running rescale of the accumulators).
+//   * QK^T (VALU form): each lane multiplies its E key elements with the
+//     matching E elements of the G (pre-scaled) queries held in registers,
+//     then a DPP sum over the LPT lanes of the row gives the G scores.
+//   * Scores go to LDS; the max and the sum of exp2(s - max) are taken over
+//     the scores in LDS before PV (two-pass softmax inside the partition: no
+//     running rescale of the accumulators).
 //   * PV: the same lane mapping over V; each lane accumulates
 //     p[g][token] * v for its E dims, then lanes of different rows and
 //     different waves are summed (shuffles + LDS).
-//   * All K and V loads of a wave's tiles are issued before any math, so a
-//     wave keeps TPW * NL * 2 16-byte loads in flight.
 // Pass 2 (decode_merge_kernel): per (query head, sequence) merge of the
 // partition partials m (max), l (sum), acc (unnormalised PV):
 //   M = max m_p;  out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.
@@ -37,7 +44,7 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 // Upper bound on partitions per sequence the merge pass accepts (LDS weights):
-// 1M tokens at 256 tokens per partition.
+// 2M tokens at 512 tokens per partition.
 constexpr int kMaxMergeParts = 4096;  // 16 KiB of merge weights in LDS
 
 template <typename T>
@@ -321,13 +328,16 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
   }
 }
 
-// ---- streaming variant: one wave per partition --------------------------------
-// One 64-lane wave owns one (partition of NTILE blocks, KV head, sequence)
-// item and streams its 2*NTILE (block, head) tiles -- the K tiles, then the V
-// tiles -- through a ring of R register tiles: the loads of tile t + R are
-// issued as soon as tile t has been consumed, so a wave always has R tiles
-// (R KiB x 4 for bf16 D=128) in flight and its arithmetic overlaps its own
-// loads.  There are no cross-wave barriers; scores live in wave-private LDS.
+// ---- streaming variant ---------------------------------------------------------
+// SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
+// item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
+// tiles, then the V tiles -- through a ring of R register tiles: the loads of
+// tile t + R are issued as soon as tile t has been consumed, so a wave always
+// has R tiles (R KiB x 4 for bf16 D=128) in flight and its arithmetic overlaps
+// its own loads.  Scores live in wave-private LDS; the only barrier is the
+// final combine of the SPLIT softmax states (m, l, acc) through LDS.  (KHW > 1
+// instead puts KHW adjacent KV heads of one partition in a workgroup, one wave
+// each, with SPLIT = 1.)
 // Lane mapping and arithmetic are those of decode_partition_kernel, except
 // that for bf16 pools QK^T runs on the matrix cores (MFMA = true): one
 // v_mfma_f32_16x16x32_bf16 per 32 dims of a 16-token tile with
@@ -339,8 +349,8 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
 //   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
 // (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
 // D[4(l/16)+r][l%16].)  PV stays on the VALU.
-template <typename T, int D, int G, int BS, int NTILE, int R, int KHW>
-__global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
+template <typename T, int D, int G, int BS, int NTILE, int R, int KHW, int SPLIT>
+__global__ __launch_bounds__(64 * KHW * SPLIT) void decode_stream_kernel(
     float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
     const float* __restrict__ q, const void* __restrict__ k_pool_,
     const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
@@ -353,17 +363,22 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
   constexpr int TPL = 64 / LPT;  // token rows per wave-load
   constexpr int NL = BS / TPL;   // wave-loads per tile
   constexpr int P = NTILE * BS;  // tokens per partition
-  constexpr int NT = 2 * NTILE;  // tiles streamed: K then V
+  constexpr int NTW = NTILE / SPLIT;  // tiles of the partition this wave streams
+  constexpr int NT = 2 * NTW;    // tiles streamed: K then V
   static_assert(D % E == 0 && 64 % LPT == 0 && BS % TPL == 0 && R >= 1 && R <= NT,
                 "unsupported tile shape");
+  static_assert(NTILE % SPLIT == 0 && (SPLIT == 1 || KHW == 1), "SPLIT waves share one KV head");
 
-  __shared__ __align__(16) float s_pw[KHW][P * G];  // per wave: scores, then probabilities
+  __shared__ __align__(16) float s_pw[KHW * SPLIT][NTW * BS * G];  // per wave: scores, then probabilities
 
   // KHW waves = KHW consecutive KV heads of one (partition, sequence): the
   // waves stay co-scheduled and read the adjacent head tiles of each block
   // (KHW * 4 KiB contiguous for bf16 D=128) at the same time.
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kh = blockIdx.x * KHW + w, part = blockIdx.y, b = blockIdx.z;
+  // SPLIT > 1: the SPLIT waves stream consecutive NTW-tile slices of one
+  // partition and combine their softmax states in LDS at the end.
+  const int kh = blockIdx.x * KHW + (SPLIT > 1 ? 0 : w), part = blockIdx.y, b = blockIdx.z;
+  const int sub = SPLIT > 1 ? w : 0;
   float* __restrict__ s_p = s_pw[w];
   const int num_q_heads = num_kv_heads * G;
   const int lane = threadIdx.x & 63;
@@ -372,11 +387,11 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
 
   // Requests that do not depend on the context length go out first.
   int L = ctx_lens[b];
-  const int lb0 = part * NTILE;
+  const int lb0 = part * NTILE + sub * NTW;  // first tile (block index) of this wave
   const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
-  int32_t pb[NTILE];
+  int32_t pb[NTW];
 #pragma unroll
-  for (int i = 0; i < NTILE; ++i) {
+  for (int i = 0; i < NTW; ++i) {
     const int lb = lb0 + i;
     const int lbc = lb < max_blocks_per_seq ? lb : max_blocks_per_seq - 1;
     pb[i] = lbc >= 0 ? tab[lbc] : -1;
@@ -411,10 +426,11 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
       }
     }
   }
+
   L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
   const int nparts = (L + P - 1) / P;
   if (L == 0) {
-    if (part == 0)
+    if (part == 0 && sub == 0)
       for (int o = lane; o < G * D; o += 64) out[head0 * D + o] = 0.0f;
     return;
   }
@@ -423,10 +439,10 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
   // Tile i of the partition is block lb0 + i.  A tile past the context, or
   // with an invalid id, re-reads tile 0 (an L2 hit) and is masked.
   const int32_t pb0 = (pb[0] >= 0 && pb[0] < num_blocks) ? pb[0] : 0;
-  int64_t base[NTILE];  // wave-uniform element offset of each (block, head) tile
-  bool ok[NTILE], full[NTILE];
+  int64_t base[NTW];  // wave-uniform element offset of each (block, head) tile
+  bool ok[NTW], full[NTW];
 #pragma unroll
-  for (int i = 0; i < NTILE; ++i) {
+  for (int i = 0; i < NTW; ++i) {
     const int tbase = (lb0 + i) * BS;
     ok[i] = tbase < L && pb[i] >= 0 && pb[i] < num_blocks;
     full[i] = ok[i] && tbase + BS <= L;
@@ -441,11 +457,11 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
   uint4 ring[R][NL];
 #pragma unroll
   for (int t = 0; t < R; ++t) {
-    const T* pool = t < NTILE ? kl : vl;
-    const int step = t < NTILE ? KSTEP : VSTEP;
+    const T* pool = t < NTW ? kl : vl;
+    const int step = t < NTW ? KSTEP : VSTEP;
 #pragma unroll
     for (int n = 0; n < NL; ++n)
-      ring[t][n] = *reinterpret_cast<const uint4*>(pool + base[t % NTILE] + n * step);
+      ring[t][n] = *reinterpret_cast<const uint4*>(pool + base[t % NTW] + n * step);
   }
 
   // MFMA A operands: q split into bf16 hi + lo rows (after the ring loads
@@ -466,16 +482,16 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
     }
   }
 
-  const int tok0 = part * P;
+  const int tok0 = lb0 * BS;  // first token of this wave's slice
   float acc[G][E];
   float m[G], l[G];
-  // The 2*NTILE steps are instantiated one by one (static_for) so that every
+  // The 2*NTW steps are instantiated one by one (static_for) so that every
   // ring slot is a fixed set of registers.
   static_for<0, NT>([&](auto tc) __attribute__((always_inline)) {
     constexpr int t = decltype(tc)::value;
-    constexpr int i = t % NTILE;
+    constexpr int i = t % NTW;
     uint4* tile = ring[t % R];
-    if constexpr (t < NTILE) {
+    if constexpr (t < NTW) {
       // ---- QK^T for the 16 tokens of tile i ----
       if constexpr (MFMA) {
         f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -525,7 +541,7 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
           }
         }
       }
-      if constexpr (t == NTILE - 1) {
+      if constexpr (t == NTW - 1) {
         // ---- softmax statistics over the partition (this wave only) ----
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // LDS writes above ...
         __builtin_amdgcn_wave_barrier();
@@ -533,7 +549,7 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
 #pragma unroll
         for (int g = 0; g < G; ++g) m[g] = -INFINITY;
 #pragma unroll
-        for (int x = lane; x < P; x += 64)
+        for (int x = lane; x < NTW * BS; x += 64)
 #pragma unroll
           for (int g = 0; g < G; ++g) m[g] = fmaxf(m[g], s_p[x * G + g]);
 #pragma unroll
@@ -542,7 +558,7 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
           l[g] = 0.0f;
         }
 #pragma unroll
-        for (int x = lane; x < P; x += 64)
+        for (int x = lane; x < NTW * BS; x += 64)
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             const float sv = s_p[x * G + g];
@@ -588,14 +604,14 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
     }
     if constexpr (t + R < NT) {  // refill the slot just consumed
       constexpr int tn = t + R;
-      const T* pool = tn < NTILE ? kl : vl;
-      constexpr int step = tn < NTILE ? KSTEP : VSTEP;
+      const T* pool = tn < NTW ? kl : vl;
+      constexpr int step = tn < NTW ? KSTEP : VSTEP;
 #pragma unroll
       for (int n = 0; n < NL; ++n)
-        tile[n] = *reinterpret_cast<const uint4*>(pool + base[tn % NTILE] + n * step);
+        tile[n] = *reinterpret_cast<const uint4*>(pool + base[tn % NTW] + n * step);
     }
     // keep the ring a ring: the scheduler may not hoist later refills above
-    // this step's arithmetic (that would need all 2*NTILE tiles in registers)
+    // this step's arithmetic (that would need all 2*NTW tiles in registers)
     __builtin_amdgcn_sched_barrier(0);
   });
 
@@ -606,27 +622,73 @@ __global__ __launch_bounds__(64 * KHW) void decode_stream_kernel(
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int e = 0; e < E; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
-  if (slot == 0) {
+  if constexpr (SPLIT == 1) {
+    if (slot == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float* dst;
-      float scl = 1.0f;
-      if (nparts == 1) {
-        dst = out + (head0 + g) * D + dl * E;
-        scl = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
-      } else {
-        const int64_t row = (head0 + g) * max_parts + part;
-        dst = part_acc + row * D + dl * E;
+      for (int g = 0; g < G; ++g) {
+        float* dst;
+        float scl = 1.0f;
+        if (nparts == 1) {
+          dst = out + (head0 + g) * D + dl * E;
+          scl = l[g] > 0.0f ? 1.0f / l[g] : 0.0f;
+        } else {
+          const int64_t row = (head0 + g) * max_parts + part;
+          dst = part_acc + row * D + dl * E;
+          if (dl == 0) {
+            part_ml[row * 2 + 0] = m[g];
+            part_ml[row * 2 + 1] = l[g];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < E; e += 4)
+          *reinterpret_cast<float4*>(dst + e) =
+              make_float4(acc[g][e] * scl, acc[g][e + 1] * scl, acc[g][e + 2] * scl,
+                          acc[g][e + 3] * scl);
+      }
+    }
+  } else {
+    // Combine the SPLIT slices: M = max m_s, w_s = 2^(m_s - M),
+    // l = sum w_s l_s, acc = sum w_s acc_s (a slice without a valid token has
+    // m = -inf and weight 0).
+    __shared__ float s_cm[SPLIT][G], s_cl[SPLIT][G];
+    __shared__ __align__(16) float s_cacc[SPLIT][G * D];
+    if (slot == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4)
+          *reinterpret_cast<float4*>(&s_cacc[sub][g * D + dl * E + e]) =
+              make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
         if (dl == 0) {
-          part_ml[row * 2 + 0] = m[g];
-          part_ml[row * 2 + 1] = l[g];
+          s_cm[sub][g] = m[g];
+          s_cl[sub][g] = l[g];
         }
       }
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < G * D; o += 64 * SPLIT) {
+      const int g = o / D, d = o - g * D;
+      float M = s_cm[0][g];
 #pragma unroll
-      for (int e = 0; e < E; e += 4)
-        *reinterpret_cast<float4*>(dst + e) =
-            make_float4(acc[g][e] * scl, acc[g][e + 1] * scl, acc[g][e + 2] * scl,
-                        acc[g][e + 3] * scl);
+      for (int x = 1; x < SPLIT; ++x) M = fmaxf(M, s_cm[x][g]);
+      float ls = 0.0f, v = 0.0f;
+#pragma unroll
+      for (int x = 0; x < SPLIT; ++x) {
+        const float mx = s_cm[x][g];
+        const float wx = (mx == -INFINITY) ? 0.0f : exp2f(mx - M);
+        ls = fmaf(wx, s_cl[x][g], ls);
+        v = fmaf(wx, s_cacc[x][o], v);
+      }
+      if (nparts == 1) {
+        out[(head0 + g) * D + d] = ls > 0.0f ? v / ls : 0.0f;
+      } else {
+        const int64_t row = (head0 + g) * max_parts + part;
+        part_acc[row * D + d] = v;
+        if (d == 0) {
+          part_ml[row * 2 + 0] = M;
+          part_ml[row * 2 + 1] = ls;
+        }
+      }
     }
   }
 }
@@ -714,7 +776,7 @@ constexpr int kBS = 16;
 // Tokens per partition and waves per workgroup (bf16 pools; fp32 D=128 uses
 // twice the waves so a wave holds at most 16 16-byte K+V loads per lane).
 #ifndef RKV_DECODE_P
-#define RKV_DECODE_P 256
+#define RKV_DECODE_P 512
 #endif
 #ifndef RKV_DECODE_NW
 #define RKV_DECODE_NW 4
@@ -736,13 +798,19 @@ struct Launch {
                  int, const int32_t*, int, int, int64_t, float, int) = nullptr;
 };
 
-// Ring depth of the streaming kernel: 32 16-byte loads per lane in flight
-// (128 VGPRs), at most every tile of the partition.
+#ifndef RKV_DECODE_SPLIT
+#define RKV_DECODE_SPLIT 4
+#endif
+// Waves per partition of the streaming kernel (each streams a slice).
+constexpr int kSplit = RKV_DECODE_SPLIT;
+
+// Ring depth of the streaming kernel: RKV_DECODE_RING_LOADS 16-byte loads per
+// lane in flight, at most every tile of the wave's slice.
 template <typename T, int D>
 constexpr int ring_for() {
   constexpr int nl = kBS / (64 / (D / Traits<T>::E));
   constexpr int r = RKV_DECODE_RING_LOADS / nl;
-  constexpr int nt = 2 * (kP / kBS);
+  constexpr int nt = 2 * (kP / kBS) / kSplit;
   return r < 1 ? 1 : (r > nt ? nt : r);
 }
 
@@ -750,9 +818,10 @@ template <typename T, int D, int G, int NW, int KHW>
 Launch make_launch() {
   Launch l;
   if constexpr (kStream) {
-    l.nw = KHW;
+    constexpr int S = KHW == 1 ? kSplit : 1;
+    l.nw = KHW * S;
     l.khw = KHW;
-    l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), KHW>;
+    l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), KHW, S>;
   } else {
     constexpr int TPW = kP / (NW * kBS);
     static_assert(TPW >= 1 && TPW * NW * kBS == kP, "partition must split evenly over waves");

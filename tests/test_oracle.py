@@ -289,7 +289,7 @@ def test_decode_invalid_block_ids_are_left_out():
         assert np.abs(got[0, h] - (p / p.sum()) @ V).max() < 1e-5
 
 
-@pytest.mark.parametrize("psize", [16, 48, 256])
+@pytest.mark.parametrize("psize", [16, 48, 256, 512])
 def test_splitk_merge_equals_single_pass(psize):
     rng = np.random.default_rng(10)
     hkv, bs, d, hq = 2, 16, 64, 8
