@@ -44,9 +44,9 @@ def parse():
     p.add_argument("--copy-only", action="store_true",
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
-                   choices=["config1", "config2", "config3", "config4"],
+                   choices=["config0", "config1", "config2", "config3", "config4"],
                    help="config2 (default): the headline decode line; the others print "
-                        "their own line (BASELINE.json configs[1], [3], [4])")
+                        "their own line (BASELINE.json configs[0], [1], [3], [4])")
     return p.parse_args()
 
 
@@ -166,6 +166,50 @@ def _line(metric, value, unit, ms, args, dtype, config, **extra):
     return d
 
 
+def run_config0(torch, dev, args):
+    """the 2-layer decoder (d 128, 4 heads of 32, MLP 512, vocab
+    1000, fp32) with weights N(0, 0.02) from seed 0, a 32-id prompt (seed 0)
+    and 64 greedy tokens through the paged fp32 KV cache, batch 1.  One step =
+    one generated token (the prompt is fed one token per step as well, so a
+    generation is 95 decoder steps).  The cpu_baseline leg runs the C oracle's
+    decoder on the same weights and prompt; its tokens must equal the GPU's."""
+    import numpy as np
+    from rustral_amd import model
+    cfg = model.config()
+    params = model.init_params(cfg, seed=0, std=0.02)
+    prompt = np.random.default_rng(0).integers(0, 1000, 32).astype(np.int32)
+    n_new = 64
+    dec = model.Decoder(cfg, params)
+    for _ in range(max(args.warmup, 1)):
+        toks = dec.generate(prompt, n_new)
+    reps = max(args.steps // 4, 3)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        toks = dec.generate(prompt, n_new)       # synchronizes at its end
+    dt = (time.perf_counter() - t0) / reps
+    gpu_tps = n_new / dt
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+        ocfg = oracle.decoder_config()
+        t0 = time.perf_counter()
+        want = oracle.decoder_generate(ocfg, params, prompt, n_new)
+        cdt = time.perf_counter() - t0
+        cpu = {"value": round(n_new / cdt, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"oracle/rkv_oracle.c decoder, the same 32-id prompt + {n_new} greedy "
+                         f"tokens, one thread, {cdt:.3f} s",
+               "tokens_equal_gpu": bool(np.array_equal(want, toks))}
+    steps = len(prompt) + n_new - 1
+    return _line("configs[0] greedy decode tokens/s, batch 1 (GPU tokens checked against the CPU decoder)",
+                 gpu_tps, "tokens/s", 1e3 * dt / steps, args, "fp32",
+                 {"workload": "configs[0] tiny decoder, 2 layers, d_model 128, 4 heads x 32, "
+                              "d_ff 512, vocab 1000, paged fp32 KV (16-token blocks)",
+                  "prompt": int(len(prompt)), "generated": n_new, "batch": 1},
+                 ms_per_generation=round(1e3 * dt, 3), decoder_steps=steps,
+                 us_per_decoder_step=round(1e6 * dt / steps, 2), cpu_baseline=cpu)
+
+
 def run_config1(torch, dev, args):
     """32 layers, Hkv 8, D 128, BS 16; 64 sequences each appending
     one token per step into a 65,536-block pool (random tables), gather of
@@ -208,6 +252,22 @@ def run_config1(torch, dev, args):
             app()
         ms_app = _timed(torch, app, steps)
         app_bytes = n_layers * B * hkv * d * 2 * (4 + s_pool) + B * 8
+        # the same 16 per-step launches captured once in a HIP graph and
+        # replayed, as a serving loop captures its step (no host launch cost)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for s in slot_sets:
+                kv.append(kp, vp, kn, vn, s)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            for s in slot_sets:
+                kv.append(kp, vp, kn, vn, s)
+        graph.replay()
+        ms_graph = _timed(torch, graph.replay, max(steps // 4, 3)) / len(slot_sets)
+        del graph
         # bulk: the 16 steps' tokens (1024 per layer) in one launch, as a
         # prefill or a batch of queued steps would append them
         knb = torch.randn((n_layers, 16 * B, hkv, d), generator=g, device=dev)
@@ -241,20 +301,24 @@ def run_config1(torch, dev, args):
         res[dtype] = {"layers": n_layers, "append": {
             "us_per_step": round(1e3 * ms_app, 2), "bytes_per_step": app_bytes,
             "GBps": round(app_bytes / (ms_app * 1e-3) / 1e9, 1)},
+            "append_graph": {"us_per_step": round(1e3 * ms_graph, 2), "bytes_per_step": app_bytes,
+                             "GBps": round(app_bytes / (ms_graph * 1e-3) / 1e9, 1)},
             "append_bulk_16_steps": {"us_per_launch": round(1e3 * ms_bulk, 2),
                                      "bytes_per_launch": bulk_bytes,
                                      "GBps": round(bulk_bytes / (ms_bulk * 1e-3) / 1e9, 1)},
             "gather_packed": outs}
         del kp, vp, kn, vn
         torch.cuda.empty_cache()
-    a = res["bf16"]["append"]
+    a = res["bf16"]["append_graph"]
     gb = res["bf16"]["gather_packed"]["same"]
-    return _line("KV append GB/s per step (64 tokens x 32 layers, one launch), bf16 pool", a["GBps"],
+    return _line("KV append GB/s per step (64 tokens x 32 layers, one launch per step; 16 steps "
+                 "replayed from a HIP graph), bf16 pool", a["GBps"],
                  "GB/s", a["us_per_step"] / 1e3, args, "bf16",
                  {"workload": "configs[1] KV append + gather microbench", "num_kv_heads": hkv,
                   "head_dim": d, "block_size": bs, "pool_blocks": nb, "sequences": B,
                   "context": [512, 4096]},
                  gather_GBps_bf16=gb["GBps"],
+                 append_eager_GBps_bf16=res["bf16"]["append"]["GBps"],
                  append_bulk_GBps_bf16=res["bf16"]["append_bulk_16_steps"]["GBps"], results=res)
 
 
@@ -445,7 +509,7 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.workload != "config2":
-        line = {"config1": run_config1, "config3": run_config3,
+        line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
                 "config4": run_config4}[args.workload](torch, dev, args)
         print(json.dumps(line), flush=True)
         return

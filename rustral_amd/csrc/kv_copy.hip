@@ -37,25 +37,28 @@ __device__ __forceinline__ F8 bf16x8_to_f8(const uint4& w) {
 
 // ---- append -----------------------------------------------------------------
 // grid = (n_tokens, n_layers); each thread moves 8 elements of K and of V.
+// The source rows do not depend on the slot, so the first chunk's K/V loads
+// are issued before the slot is waited on (straight-line code; the loop for
+// further chunks only runs when Hkv * D / 8 exceeds the workgroup).  bs_log2
+// is log2(block_size) for a power-of-two block size, else -1 (division).
 template <bool BF16>
 __global__ __launch_bounds__(256) void append_kernel(
     void* __restrict__ k_pool, void* __restrict__ v_pool, int64_t pool_layer_stride,
     const float* __restrict__ k_new, const float* __restrict__ v_new, int64_t src_layer_stride,
     int64_t src_tok_stride, int64_t src_head_stride, const int64_t* __restrict__ slot_mapping,
-    int num_kv_heads, int head_dim, int block_size, int64_t num_slots) {
+    int num_kv_heads, int head_dim, int block_size, int bs_log2, int64_t num_slots) {
   const int t = blockIdx.x, layer = blockIdx.y;
-  const int64_t slot = slot_mapping[t];
-  if (slot < 0 || slot >= num_slots) return;  // padding or out-of-range slot
-  const int64_t blk = slot / block_size, row = slot % block_size;
   const int chunks = head_dim >> 3;
   const int units = num_kv_heads * chunks;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+  const int64_t src0 = layer * src_layer_stride + t * src_tok_stride;
+  auto src_of = [&](int u) {
     const int h = u / chunks, c = u - h * chunks;
-    const int64_t src = layer * src_layer_stride + t * src_tok_stride + h * src_head_stride + c * 8;
+    return src0 + h * src_head_stride + c * 8;
+  };
+  auto put = [&](int u, int64_t blk, int64_t row, const F8& k, const F8& v) {
+    const int h = u / chunks, c = u - h * chunks;
     const int64_t dst =
         layer * pool_layer_stride + ((blk * num_kv_heads + h) * block_size + row) * head_dim + c * 8;
-    const F8 k = load_f8(k_new + src);
-    const F8 v = load_f8(v_new + src);
     if constexpr (BF16) {
       *reinterpret_cast<uint4*>(static_cast<uint16_t*>(k_pool) + dst) = f8_to_bf16x8(k);
       *reinterpret_cast<uint4*>(static_cast<uint16_t*>(v_pool) + dst) = f8_to_bf16x8(v);
@@ -63,6 +66,22 @@ __global__ __launch_bounds__(256) void append_kernel(
       store_f8(static_cast<float*>(k_pool) + dst, k);
       store_f8(static_cast<float*>(v_pool) + dst, v);
     }
+  };
+  const int u0 = threadIdx.x;
+  F8 k0, v0;
+  if (u0 < units) {
+    k0 = load_f8(k_new + src_of(u0));
+    v0 = load_f8(v_new + src_of(u0));
+  }
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;  // padding or out-of-range slot
+  const int64_t blk = bs_log2 >= 0 ? slot >> bs_log2 : slot / block_size;
+  const int64_t row = slot - blk * block_size;
+  if (u0 < units) put(u0, blk, row, k0, v0);
+  for (int u = u0 + blockDim.x; u < units; u += blockDim.x) {
+    const F8 k = load_f8(k_new + src_of(u));
+    const F8 v = load_f8(v_new + src_of(u));
+    put(u, blk, row, k, v);
   }
 }
 
@@ -172,16 +191,17 @@ extern "C" int rkv_append(void* k_pool, void* v_pool, int64_t pool_layer_stride,
   dim3 grid((unsigned)n_tokens, (unsigned)n_layers);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t n_slots = num_blocks * block_size;
+  const int bs_log2 = (block_size & (block_size - 1)) ? -1 : __builtin_ctz((unsigned)block_size);
   if (dtype == RKV_BF16)
     append_kernel<true><<<grid, threads, 0, s>>>(k_pool, v_pool, pool_layer_stride, k_new, v_new,
                                                   src_layer_stride, src_tok_stride, src_head_stride,
                                                   slot_mapping, num_kv_heads, head_dim, block_size,
-                                                  n_slots);
+                                                  bs_log2, n_slots);
   else
     append_kernel<false><<<grid, threads, 0, s>>>(k_pool, v_pool, pool_layer_stride, k_new, v_new,
                                                    src_layer_stride, src_tok_stride,
                                                    src_head_stride, slot_mapping, num_kv_heads,
-                                                   head_dim, block_size, n_slots);
+                                                   head_dim, block_size, bs_log2, n_slots);
   return check_launch("rkv_append");
 }
 

@@ -51,6 +51,68 @@ def test_append_multi_layer_one_launch(dev, dtype):
     assert np.array_equal(to_np(gk), kp) and np.array_equal(to_np(gv), vp)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hkv,d,bs", [(32, 128, 16), (8, 128, 12), (3, 40, 5)])
+def test_append_wide_rows_and_other_block_sizes(dev, dtype, hkv, d, bs):
+    """Hkv*D/8 above the 256-thread workgroup (the kernel's chunk loop) and
+    block sizes that are not a power of two (slot / block_size by division)."""
+    say(f"append wide/odd dtype={dtype} hkv={hkv} d={d} bs={bs}")
+    rng = np.random.default_rng(hkv * 1000 + d + bs)
+    n = 200
+    nb = n // bs + 10
+    kp, vp, _, _ = make_pool(rng, nb, hkv, bs, d, dtype)
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[::11] = -1
+    kn = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    gk, gv = to_dev(kp, dev), to_dev(vp, dev)
+    kv.append(gk, gv, to_dev(kn, dev), to_dev(vn, dev), to_dev(slots, dev))
+    oracle.append(kp, vp, kn, vn, slots)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(gk), kp)
+    assert np.array_equal(to_np(gv), vp)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_append_graph_replay_matches_eager(dev, dtype):
+    """Per-step appends captured in a HIP graph (as a serving loop captures a
+    step): every replay, with eager work and synchronisation between the
+    replays, writes exactly what the eager calls write."""
+    say(f"append graph replay dtype={dtype}")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    nl, nb, hkv, bs, d, n = 3, 64, 8, 16, 128, 48
+    g = torch.Generator(device=dev).manual_seed(5)
+    perm = torch.randperm(nb * bs, generator=g, device=dev)
+    slot_sets = [perm[i * n:(i + 1) * n].to(torch.int64).contiguous() for i in range(4)]
+    kn = torch.empty((nl, n, hkv, d), device=dev)
+    vn = torch.empty_like(kn)
+    kp = torch.zeros((nl, nb, hkv, bs, d), dtype=tdt, device=dev)
+    vp = torch.zeros_like(kp)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                      # warm-up outside the capture
+        for s in slot_sets:
+            kv.append(kp, vp, kn.normal_(generator=g), vn.normal_(generator=g), s)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for s in slot_sets:
+            kv.append(kp, vp, kn, vn, s)
+    for rep in range(4):
+        kp.zero_(), vp.zero_()
+        kn.normal_(generator=g), vn.normal_(generator=g)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ek, ev = torch.zeros_like(kp), torch.zeros_like(vp)
+        for s in slot_sets:
+            kv.append(ek, ev, kn, vn, s)
+        torch.cuda.synchronize()
+        assert torch.equal(kp, ek) and torch.equal(vp, ev), f"replay {rep}"
+        assert int((kp != 0).sum()) > 0
+
+
 @pytest.mark.parametrize("out_f32", [False, True])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_gather_bitexact_padded_and_packed(dev, dtype, out_f32):
