@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--copy-only", action="store_true",
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
-                   choices=["config0", "config1", "config2", "config3", "config4"],
+                   choices=["config0", "config1", "config2", "config3", "config4", "prefill"],
                    help="config2 (default): the headline decode line; the others print "
                         "their own line (BASELINE.json configs[0], [1], [3], [4])")
     return p.parse_args()
@@ -373,6 +373,92 @@ def run_config3(torch, dev, args):
                  calls_timed=reps)
 
 
+def prefill_bytes_flops(n_new, ctx, hq=HQ, hkv=HKV, d=D, s_kv=2):
+    """Algorithmic bytes and flops of one causal prefill call.  Bytes: q read
+    and out written (fp32), each sequence's K and V read once per KV head
+    (positions 0 .. ctx-1), block ids, q_start and ctx_lens.  Flops: 2 * D per
+    (query, key) pair for QK^T and again for PV, over the causal pairs."""
+    nbytes = flops = 0
+    for n, L in zip(n_new, ctx):
+        n, L = int(n), int(L)
+        nbytes += n * hq * d * 4 * 2 + L * hkv * d * 2 * s_kv + ((L + BS - 1) // BS) * 4 + 8
+        pairs = sum(L - n + i + 1 for i in range(n))
+        flops += pairs * hq * d * 4
+    return nbytes, flops
+
+
+def run_prefill(torch, dev, args):
+    """Causal prefill over the paged pool at configs[4]'s admission shape: 25
+    sequences x 128 new prompt tokens (ctx == 128), Hq 32, Hkv 8, D 128, bf16
+    pool, 32 layers (distinct q and pools per layer), one call per layer.  A
+    second figure: a chunked prefill of 512 new tokens after 3584 cached ones
+    for 8 sequences (the compute-heavy end)."""
+    import numpy as np
+    from rustral_amd import kv
+    g = torch.Generator(device=dev).manual_seed(7)
+
+    def layers_for(n_new, ctx, n_layers):
+        need = [(int(L) + BS - 1) // BS for L in ctx]
+        nb = int(sum(need))
+        qs = torch.from_numpy(np.concatenate([[0], np.cumsum(n_new)]).astype(np.int32)).to(dev)
+        cl = torch.from_numpy(np.asarray(ctx, np.int32)).to(dev)
+        out = []
+        for _ in range(n_layers):
+            k = torch.randn((nb, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
+            v = torch.randn((nb, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
+            q = torch.randn((int(sum(n_new)), HQ, D), generator=g, device=dev)
+            perm = torch.randperm(nb, generator=g, device=dev).to(torch.int32).cpu().numpy()
+            t = np.full((len(ctx), max(need)), -1, np.int32)
+            o = 0
+            for b, n in enumerate(need):
+                t[b, :n] = perm[o:o + n]
+                o += n
+            out.append((q, k, v, torch.from_numpy(t).to(dev), torch.empty_like(q)))
+        return out, qs, cl
+
+    def measure(n_new, ctx, n_layers, reps_per_layer):
+        layers, qs, cl = layers_for(n_new, ctx, n_layers)
+        mq = int(max(n_new))
+        it = iter(range(10 ** 9))
+        def call():
+            q, k, v, t, o = layers[next(it) % n_layers]
+            kv.prefill_attention(q, k, v, t, qs, cl, 1.0 / math.sqrt(D), max_q_len=mq, out=o)
+        for _ in range(n_layers):
+            call()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(n_layers * reps_per_layer)]
+        torch.cuda.synchronize()
+        for a, e in ev:
+            a.record()
+            call()
+            e.record()
+        torch.cuda.synchronize()
+        us = 1e3 * sum(a.elapsed_time(e) for a, e in ev) / len(ev)
+        del layers
+        torch.cuda.empty_cache()
+        return us
+
+    n_adm = np.full(25, 128, np.int32)
+    us_adm = measure(n_adm, n_adm, 32, max(args.steps // 4, 3))
+    b_adm, f_adm = prefill_bytes_flops(n_adm, n_adm)
+    n_chk = np.full(8, 512, np.int32)
+    c_chk = np.full(8, 4096, np.int32)
+    us_chk = measure(n_chk, c_chk, 8, max(args.steps // 4, 3))
+    b_chk, f_chk = prefill_bytes_flops(n_chk, c_chk)
+    gbps = b_adm / (us_adm * 1e-6) / 1e9
+    return _line("causal prefill over paged KV GB/s (configs[4] admissions: 25 x 128 tokens)", gbps,
+                 "GB/s", us_adm / 1e3, args, "bf16",
+                 {"workload": "paged causal prefill, configs[4] admission shape", "sequences": 25,
+                  "new_tokens": 128, "context": 128, "num_q_heads": HQ, "num_kv_heads": HKV,
+                  "head_dim": D, "block_size": BS, "layers": 32},
+                 us_per_call=round(us_adm, 2), algorithmic_bytes_per_call=b_adm,
+                 flops_per_call=f_adm, tflops=round(f_adm / (us_adm * 1e-6) / 1e12, 2),
+                 chunked_512_after_3584={"sequences": 8, "us_per_call": round(us_chk, 2),
+                                         "bytes": b_chk, "flops": f_chk,
+                                         "GBps": round(b_chk / (us_chk * 1e-6) / 1e9, 1),
+                                         "tflops": round(f_chk / (us_chk * 1e-6) / 1e12, 2)})
+
+
 def run_config4(torch, dev, args):
     """continuous-batching step mix.  256 running sequences with
     contexts U[1, 8192] (seed 4) in 32 layer pools of 80,000 blocks (bf16,
@@ -510,6 +596,7 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload != "config2":
         line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
+                "prefill": run_prefill,
                 "config4": run_config4}[args.workload](torch, dev, args)
         print(json.dumps(line), flush=True)
         return

@@ -150,6 +150,31 @@ int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens, int max_bloc
                                int max_context, int dtype, int partition_size,
                                const void* workspace, size_t workspace_bytes, void* stream);
 
+/* Causal prefill attention over the paged pool (many new query tokens per
+ * sequence).  Sequence b owns query rows q_start[b] .. q_start[b+1]-1 of q
+ * and out ([total, num_q_heads, head_dim] fp32, total = q_start[num_seqs]);
+ * its n_b new tokens are the last n_b of its ctx_lens[b] cached tokens (their
+ * K/V appended beforehand with rkv_append), so new token i sits at position
+ * p = ctx_lens[b] - n_b + i and attends to positions 0 .. p:
+ *   out[row][h][:] = softmax_{j<=p}((q[row][h] . K[b][kv(h)][j]) * scale) @ V
+ * Replaces the per-head recipe of TapeMultiHeadAttention::forward_tape_with_mask
+ * (crates/nn/src/tape_transformer.rs:87-139) with the additive causal mask of
+ * causal_mask_tape (:276-296; -1e9 above the diagonal gives a zero weight),
+ * reading K/V through block tables; ctx_lens[b] == n_b is the reference's
+ * square case, a larger ctx_lens[b] a chunked prefill after cached tokens.
+ * max_q_len: host-side bound on the n_b (it sizes the grid); only the first
+ * max_q_len new tokens of a sequence are computed, later rows are not
+ * written.  Rows with p < 0 are zero; positions at or beyond
+ * max_blocks_per_seq*block_size and blocks with an invalid id are left out.
+ * block_size 16; head_dim 32, 64 or 128; num_q_heads / num_kv_heads 1, 2, 4
+ * or 8.  No workspace. */
+int rkv_prefill_attention(float* out, const float* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* q_start, const int32_t* ctx_lens, int num_seqs,
+                          int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                          int64_t num_blocks, int max_q_len, float scale, int dtype,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,6 +63,8 @@ def _declare(L):
     L.orc_decode_partials.argtypes = [_p, _p] + dec + [C.c_int, C.c_int]
     L.orc_splitk_merge.argtypes = [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int,
                                    C.c_int, C.c_int, C.c_int]
+    L.orc_prefill_attention.argtypes = [_p, _p, _p, _p, _p, C.c_int, _p, _p, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_int, _i64, _f32, C.c_int]
     L.orc_decoder_param_count.restype = _i64
     L.orc_decoder_param_count.argtypes = [_p]
     L.orc_linear.argtypes = [_p, _p, _p, _p, C.c_int, C.c_int, C.c_int]
@@ -72,7 +74,7 @@ def _declare(L):
     L.orc_decoder_generate.argtypes = [_p, _p, _p, C.c_int, C.c_int, _p, _p]
     for name in ("orc_decoder_generate", "orc_append", "orc_gather", "orc_copy_blocks", "orc_decode_attention",
                  "orc_decode_attention_f64", "orc_decode_attention_mt", "orc_decode_partials",
-                 "orc_splitk_merge"):
+                 "orc_splitk_merge", "orc_prefill_attention"):
         getattr(L, name).restype = C.c_int
 
 
@@ -227,6 +229,24 @@ def decode_splitk(q, k_pool, v_pool, block_tables, ctx_lens, scale, partition_si
     _check(lib().orc_splitk_merge(_ptr(out), _ptr(m), _ptr(l), _ptr(acc), _ptr(keep[2]), mbs, bs,
                                   B, hq, d, partition_size, max_parts), "orc_splitk_merge")
     return out, (m, l, acc)
+
+
+def prefill_attention(q, k_pool, v_pool, block_tables, q_start, ctx_lens, scale):
+    """Causal prefill over the paged pool: q/out [total, Hq, D]; sequence b
+    owns rows q_start[b] .. q_start[b+1]-1, at positions ctx_lens[b] - n_b + i."""
+    nb, hkv, bs, d = k_pool.shape
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    qs = np.ascontiguousarray(q_start, dtype=np.int32)
+    cl = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    total, hq, _ = q.shape
+    assert qs[-1] <= total and len(qs) == len(cl) + 1
+    out = np.zeros_like(q)
+    _check(lib().orc_prefill_attention(_ptr(out), _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(bt),
+                                       bt.shape[1], _ptr(qs), _ptr(cl), len(cl), hq, hkv, d, bs,
+                                       nb, float(scale), _dtype_code(k_pool)),
+           "orc_prefill_attention")
+    return out
 
 
 # ---- config-0 decoder ----------------------------------------------------------

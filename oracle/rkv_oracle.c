@@ -267,6 +267,36 @@ int orc_decode_attention(float* out, const float* q, const void* k_pool, const v
   return 0;
 }
 
+int orc_prefill_attention(float* out, const float* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* q_start, const int32_t* ctx_lens, int num_seqs,
+                          int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                          int64_t num_blocks, float scale, int pool_dtype) {
+  if (!out || !q_start ||
+      check_dec(q, k_pool, v_pool, block_tables, ctx_lens, num_q_heads, num_kv_heads, head_dim,
+                block_size))
+    return -1;
+  const int cap = max_blocks_per_seq * block_size;
+  float* s = (float*)malloc(sizeof(float) * (cap > 0 ? cap : 1));
+  if (!s) return -1;
+  for (int b = 0; b < num_seqs; ++b) {
+    const int n = q_start[b + 1] - q_start[b];
+    for (int i = 0; i < n; ++i) {
+      const int64_t row = (int64_t)q_start[b] + i;
+      const int p = ctx_lens[b] - n + i;
+      int L = p + 1; /* the token attends to positions 0 .. p (causal) */
+      /* one decode row: sequence b's table, context L, this token's queries */
+      dec_args a = {q + row * num_q_heads * head_dim, k_pool, v_pool,
+                    block_tables + (int64_t)b * max_blocks_per_seq, &L, max_blocks_per_seq,
+                    num_q_heads, num_kv_heads, head_dim, block_size, pool_dtype, num_blocks, scale};
+      for (int h = 0; h < num_q_heads; ++h)
+        decode_one_f32(&a, 0, h, out + (row * num_q_heads + h) * head_dim, s);
+    }
+  }
+  free(s);
+  return 0;
+}
+
 int orc_decode_attention_f64(double* out, const float* q, const void* k_pool,
                              const void* v_pool, const int32_t* block_tables,
                              int max_blocks_per_seq, const int32_t* ctx_lens, int num_seqs,

@@ -123,6 +123,23 @@ int orc_splitk_merge(float* out, const float* m, const float* l, const float* ac
                      int num_seqs, int num_q_heads, int head_dim, int partition_size,
                      int max_parts);
 
+/* Causal prefill attention over the paged pool.  Sequence b has n_b =
+ * q_start[b+1] - q_start[b] new query tokens (rows q_start[b] .. of q/out,
+ * [total, Hq, D] fp32) whose K/V are already in the pool; token i sits at
+ * position p = ctx_lens[b] - n_b + i and attends to positions 0 .. p.  This
+ * is the per-head recipe of forward_tape_with_mask
+ * (crates/nn/src/tape_transformer.rs:87-139) with the additive causal mask of
+ * causal_mask_tape (:276-296): -1e9 above the diagonal, which underflows to a
+ * zero weight in the softmax, so masked positions drop out exactly.  The
+ * reference's square case is ctx_lens[b] == n_b; a larger ctx_lens[b] is a
+ * chunked prefill after ctx_lens[b] - n_b cached tokens.  Each row is
+ * orc_decode_attention's computation with L = p + 1 (p < 0: zero row). */
+int orc_prefill_attention(float* out, const float* q, const void* k_pool, const void* v_pool,
+                          const int32_t* block_tables, int max_blocks_per_seq,
+                          const int32_t* q_start, const int32_t* ctx_lens, int num_seqs,
+                          int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                          int64_t num_blocks, float scale, int pool_dtype);
+
 /* orc_decode_attention split over n_threads POSIX threads by (b, kv head);
  * identical results (each output is computed by one thread in the same
  * order).  Used only as the CPU baseline timing. */

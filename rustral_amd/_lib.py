@@ -31,6 +31,8 @@ SIGNATURES = {
     "rkv_decode_attention_partitions": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
                                              _i64, _i, _f, _i, _i, _p, _sz, _p]),
     "rkv_decode_attention_merge": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "rkv_prefill_attention": (_i, [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i,
+                                   _f, _i, _p]),
     # include/rustral_serving.h (host memory)
     "rkv_bm_create": (_p, [_i64, _i]),
     "rkv_bm_destroy": (None, [_p]),

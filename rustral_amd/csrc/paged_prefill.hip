@@ -1,0 +1,389 @@
+// paged_prefill.hip -- causal prefill attention over the paged KV pool, for
+// gfx950 (CDNA4, wave64): many new query tokens per sequence attend to the
+// cached tokens and to each other (causal), reading K/V through the block
+// table.  The new tokens' K/V are appended to the pool first (rkv_append).
+//
+// One workgroup per (tile of 16 * QS query tokens, KV head, sequence), G * QS
+// waves: wave (g, t) serves query head kh * G + g for the t-th 16-token
+// sub-tile, so each K/V byte staged in LDS serves G heads x QS sub-tiles.
+// The workgroup walks the 16-token blocks, KB per iteration, from position 0
+// to the tile's last query position:
+//   * stage: the KB blocks' K tiles (row-major, rows padded) and V tiles
+//     (stored transposed, V^T[dim][key]) go through registers into LDS,
+//     double buffered: the next iteration's loads are in flight while this
+//     one is computed.  A wave skips the arithmetic of key blocks that lie
+//     entirely after its last query (causal).
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = K rows from LDS, B = Q^T
+//     (queries of the 16 tokens, split hi + lo bf16 so the scores carry ~16
+//     significant bits of q).  Result: lane l holds S^T[key 4(l/16)+r][row
+//     l%16] -- every value a lane holds belongs to query row l % 16.
+//   * causal mask (key position > query position -> excluded), then an
+//     online softmax per row: running max m and sum l, the accumulator
+//     rescaled by 2^(m_old - m_new).  Scores carry scale * log2(e) (exp2).
+//   * O^T += V^T P^T on v_mfma_f32_16x16x16_bf16: A = V^T from LDS, B = P^T,
+//     which is exactly the S^T layout above (no cross-lane moves); P is split
+//     hi + lo like q.  Result: lane l holds O^T[dim 16c + 4(l/16)+r][row l%16].
+// fp32 pools split K and V into hi + lo bf16 as well (three products each).
+// MFMA lane layouts (gfx950): 16x16x32: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16];
+// 16x16x16: A[l%16][4(l/16)+e], B[4(l/16)+e][l%16]; both D[4(l/16)+r][l%16].
+#include "common.hpp"
+
+#include <cmath>
+
+namespace rkv {
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) short bf16x4_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kBS = 16;  // tokens per block = keys per staged block
+
+// hi = bf16(x), lo = bf16(x - hi), packed in pairs (element 2i in the low half).
+__device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t ha = bf16_rne(a), hb = bf16_rne(b);
+  hi = ha | (hb << 16);
+  lo = bf16_rne(a - __uint_as_float(ha << 16)) | (bf16_rne(b - __uint_as_float(hb << 16)) << 16);
+}
+
+template <typename T, int D, int G, int QS, int KB>
+__global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
+    float* __restrict__ out, const float* __restrict__ q, const void* __restrict__ k_pool_,
+    const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
+    int max_blocks_per_seq, const int32_t* __restrict__ q_start,
+    const int32_t* __restrict__ ctx_lens, int num_kv_heads, int64_t num_blocks, int max_q_len,
+    float q_scale) {
+  constexpr bool F32 = sizeof(T) == 4;
+  constexpr int NT = 64 * G * QS;
+  constexpr int QT = 16 * QS;              // query tokens per workgroup
+  constexpr int NS = F32 ? 2 : 1;          // bf16 slices per staged element (hi, lo)
+  constexpr int KP = D + 8;                // padded K row in LDS (bf16 elements)
+  constexpr int VP = kBS + 4;              // padded V^T row (keys of one dim): spreads
+                                           // the transposing 2-byte stores over banks
+  constexpr int CE = 16 / sizeof(T);       // elements per 16-byte chunk
+  constexpr int CPR = D / CE;              // chunks per token row
+  constexpr int CH = kBS * CPR;            // chunks per (block, head) tile
+  constexpr int PT = (KB * CH + NT - 1) / NT;  // chunks per thread and iteration
+  constexpr int NC = D / 32;               // QK^T MFMAs per key block (per slice)
+  constexpr int NO = D / 16;               // PV MFMAs per key block (per slice)
+  __shared__ __align__(16) uint16_t s_k[2][NS][KB * kBS * KP];
+  __shared__ __align__(16) uint16_t s_vt[2][NS][KB * D * VP];
+
+  const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
+  const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
+  const int qt = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = w % G, rt = w / G;  // query head within the group, row sub-tile
+  const int num_q_heads = num_kv_heads * G, h = kh * G + g;
+
+  const int s0 = q_start[b];
+  const int n = q_start[b + 1] - s0;
+  const int nr = n < max_q_len ? n : max_q_len;  // rows computed (the first nr new tokens)
+  const int q0 = qt * QT;
+  if (q0 >= nr) return;
+  const int cap = max_blocks_per_seq * kBS;
+  const int pos0 = ctx_lens[b] - n;  // position of the first new token (may be < 0)
+  int last = pos0 + (q0 + QT < nr ? q0 + QT : nr) - 1;  // the workgroup's last query position
+  last = last < cap - 1 ? last : cap - 1;
+  const int nblk = last < 0 ? 0 : last / kBS + 1;
+  const int nit = (nblk + KB - 1) / KB;
+
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int qr0 = q0 + 16 * rt;      // this wave's first query row
+  const bool active = qr0 < nr;      // wave-uniform: the sub-tile holds a query
+  const int qi = qr0 + r16;          // this lane's query row
+  const bool row_ok = qi < nr;
+  const int qpos = pos0 + qi;
+  const int wlast = pos0 + (qr0 + 16 < nr ? qr0 + 16 : nr) - 1;  // this wave's last query position
+
+  const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
+  // Block ids come from a 64-entry window held one per lane (one vector load
+  // per 64 blocks) and are read with readlane, so issuing a block's K/V loads
+  // never waits on a table read.
+  int win = 0;
+  int32_t idv = lane < max_blocks_per_seq ? tab[lane] : -1;
+  auto block_id = [&](int j) __attribute__((always_inline)) {
+    if ((j >> 6) != win) {  // wave-uniform
+      win = j >> 6;
+      const int jj = (win << 6) + lane;
+      idv = jj < max_blocks_per_seq ? tab[jj] : -1;
+    }
+    return __builtin_amdgcn_readlane(idv, j & 63);
+  };
+  uint4 kr[PT], vr[PT];
+  // Issues iteration it's K/V loads (KB blocks) into registers; returns a
+  // bit per block whose id is valid.
+  auto fetch = [&](int it) __attribute__((always_inline)) {
+    uint32_t okm = 0;
+    int64_t base[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int j = it * KB + kb;
+      int32_t blk = j < nblk ? block_id(j) : -1;
+      const bool ok = blk >= 0 && blk < num_blocks;
+      okm |= ok ? 1u << kb : 0u;
+      base[kb] = ((int64_t)(ok ? blk : 0) * num_kv_heads + kh) * kBS * D;
+    }
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int ci = tid + i * NT;
+      if ((KB * CH) % NT == 0 || ci < KB * CH) {
+        const int kb = ci / CH, cc = ci % CH;
+        int64_t bb = base[0];  // base[kb] by selects (kb is not a compile-time index)
+#pragma unroll
+        for (int x = 1; x < KB; ++x) bb = kb == x ? base[x] : bb;
+        kr[i] = *reinterpret_cast<const uint4*>(k_pool + bb + cc * CE);
+        vr[i] = *reinterpret_cast<const uint4*>(v_pool + bb + cc * CE);
+      }
+    }
+    return okm;
+  };
+  // Writes the registers into LDS buffer buf: K row-major, V transposed.
+  auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int ci = tid + i * NT;
+      if ((KB * CH) % NT == 0 || ci < KB * CH) {
+        const int kb = ci / CH, cc = ci % CH;
+        const int key = cc / CPR, col = (cc % CPR) * CE;
+        uint16_t* kd = &s_k[buf][0][(kb * kBS + key) * KP + col];
+        uint16_t* vd = &s_vt[buf][0][(kb * D + col) * VP + key];
+        if constexpr (!F32) {
+          *reinterpret_cast<uint4*>(kd) = kr[i];
+          const uint32_t wv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vd[e * VP] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+        } else {
+          constexpr int KS = KB * kBS * KP, VS = KB * D * VP;  // slice strides
+          const float kf[4] = {__uint_as_float(kr[i].x), __uint_as_float(kr[i].y),
+                               __uint_as_float(kr[i].z), __uint_as_float(kr[i].w)};
+          const float vf[4] = {__uint_as_float(vr[i].x), __uint_as_float(vr[i].y),
+                               __uint_as_float(vr[i].z), __uint_as_float(vr[i].w)};
+          uint2 kh2, kl2;
+          split2(kf[0], kf[1], kh2.x, kl2.x);
+          split2(kf[2], kf[3], kh2.y, kl2.y);
+          *reinterpret_cast<uint2*>(kd) = kh2;
+          *reinterpret_cast<uint2*>(kd + KS) = kl2;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t hv = bf16_rne(vf[e]);
+            vd[e * VP] = (uint16_t)hv;
+            vd[e * VP + VS] = (uint16_t)bf16_rne(vf[e] - __uint_as_float(hv << 16));
+          }
+        }
+      }
+    }
+  };
+
+  uint32_t ok_next = nit > 0 ? fetch(0) : 0u;
+
+  // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8], hi and lo.
+  uint4 qhi[NC], qlo[NC];
+  {
+    const float* qp = q + ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h) * D + 8 * grp;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float4 x = reinterpret_cast<const float4*>(qp + 32 * c)[0];
+      float4 y = reinterpret_cast<const float4*>(qp + 32 * c)[1];
+      if (!row_ok) x = y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      split2(x.x, x.y, qhi[c].x, qlo[c].x);
+      split2(x.z, x.w, qhi[c].y, qlo[c].y);
+      split2(y.x, y.y, qhi[c].z, qlo[c].z);
+      split2(y.z, y.w, qhi[c].w, qlo[c].w);
+    }
+  }
+
+  f32x4_t o[NO];
+#pragma unroll
+  for (int c = 0; c < NO; ++c) o[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+
+  for (int it = 0; it < nit; ++it) {
+    const int buf = it & 1;
+    stage(buf);
+    const uint32_t okm = ok_next;
+    __syncthreads();
+    if (it + 1 < nit) ok_next = fetch(it + 1);
+    // keys of this iteration that some row of this wave may attend to
+    const int kfirst = it * KB * kBS;
+    if (!active || kfirst > wlast) continue;
+
+    // ---- S^T = K Q^T for the KB * 16 keys ----
+    float s[KB][4];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      f32x4_t st = {0.0f, 0.0f, 0.0f, 0.0f};
+      const uint16_t* kr0 = &s_k[buf][0][(kb * kBS + r16) * KP + 8 * grp];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 ka = *reinterpret_cast<const uint4*>(kr0 + 32 * c);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka),
+                                                     __builtin_bit_cast(bf16x8_t, qhi[c]), st,
+                                                     0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka),
+                                                     __builtin_bit_cast(bf16x8_t, qlo[c]), st,
+                                                     0, 0, 0);
+        if constexpr (F32) {
+          const uint4 kl =
+              *reinterpret_cast<const uint4*>(kr0 + KB * kBS * KP + 32 * c);
+          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kl),
+                                                       __builtin_bit_cast(bf16x8_t, qhi[c]), st,
+                                                       0, 0, 0);
+        }
+      }
+      // causal mask: key position > query position is excluded
+      const int kp0 = kfirst + kb * kBS + 4 * grp;
+      const bool bok = (okm >> kb) & 1u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        s[kb][r] = (bok && row_ok && kp0 + r <= qpos) ? st[r] * q_scale : -INFINITY;
+    }
+    // ---- online softmax of row r16 ----
+    float mb = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+      mb = fmaxf(mb, fmaxf(fmaxf(s[kb][0], s[kb][1]), fmaxf(s[kb][2], s[kb][3])));
+    mb = fmaxf(mb, __shfl_xor(mb, 16));
+    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    const float mn = fmaxf(m, mb);
+    const float mref = mn == -INFINITY ? 0.0f : mn;
+    const float alpha = exp2f(m - mref);
+    float ls = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[kb][r] = exp2f(s[kb][r] - mref);
+        ls += s[kb][r];
+      }
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    l = l * alpha + ls;
+    m = mn;
+#pragma unroll
+    for (int c = 0; c < NO; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[c][r] *= alpha;
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      uint2 ph, pl;
+      split2(s[kb][0], s[kb][1], ph.x, pl.x);
+      split2(s[kb][2], s[kb][3], ph.y, pl.y);
+      const uint16_t* vr0 = &s_vt[buf][0][(kb * D + r16) * VP + 4 * grp];
+#pragma unroll
+      for (int c = 0; c < NO; ++c) {
+        const uint2 va = *reinterpret_cast<const uint2*>(vr0 + 16 * c * VP);
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
+                                                        __builtin_bit_cast(bf16x4_t, ph), o[c],
+                                                        0, 0, 0);
+        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
+                                                        __builtin_bit_cast(bf16x4_t, pl), o[c],
+                                                        0, 0, 0);
+        if constexpr (F32) {
+          const uint2 vl =
+              *reinterpret_cast<const uint2*>(vr0 + KB * D * VP + 16 * c * VP);
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, vl),
+                                                          __builtin_bit_cast(bf16x4_t, ph), o[c],
+                                                          0, 0, 0);
+        }
+      }
+    }
+  }
+
+  if (!row_ok) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  float* op = out + ((int64_t)(s0 + qi) * num_q_heads + h) * D + 4 * grp;
+#pragma unroll
+  for (int c = 0; c < NO; ++c)
+    *reinterpret_cast<float4*>(op + 16 * c) =
+        make_float4(o[c][0] * inv, o[c][1] * inv, o[c][2] * inv, o[c][3] * inv);
+}
+
+using PrefillFn = void (*)(float*, const float*, const void*, const void*, const int32_t*, int,
+                           const int32_t*, const int32_t*, int, int64_t, int, float);
+
+// Query row sub-tiles per KV-head group (waves per query head) and key blocks
+// per staged iteration.
+#ifndef RKV_PREFILL_QS
+#define RKV_PREFILL_QS 4
+#endif
+#ifndef RKV_PREFILL_KB
+#define RKV_PREFILL_KB 2
+#endif
+constexpr int kQS = RKV_PREFILL_QS;
+constexpr int kKB = RKV_PREFILL_KB;
+
+template <typename T, int D>
+PrefillFn pick_g(int G) {
+  switch (G) {
+    case 1: return &prefill_kernel<T, D, 1, kQS, kKB>;
+    case 2: return &prefill_kernel<T, D, 2, kQS, kKB>;
+    case 4: return &prefill_kernel<T, D, 4, kQS, kKB>;
+    case 8: return &prefill_kernel<T, D, 8, kQS * 8 <= 16 ? kQS : 2, kKB>;
+    default: return nullptr;
+  }
+}
+
+template <typename T>
+PrefillFn pick_d(int D, int G) {
+  switch (D) {
+    case 32: return pick_g<T, 32>(G);
+    case 64: return pick_g<T, 64>(G);
+    case 128: return pick_g<T, 128>(G);
+    default: return nullptr;
+  }
+}
+
+}  // namespace
+}  // namespace rkv
+
+using namespace rkv;
+
+extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_pool,
+                                     const void* v_pool, const int32_t* block_tables,
+                                     int max_blocks_per_seq, const int32_t* q_start,
+                                     const int32_t* ctx_lens, int num_seqs, int num_q_heads,
+                                     int num_kv_heads, int head_dim, int block_size,
+                                     int64_t num_blocks, int max_q_len, float scale, int dtype,
+                                     void* stream) {
+  clear_error();
+  if (num_seqs < 0 || max_blocks_per_seq < 0 || num_blocks < 0 || max_q_len < 0)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_prefill_attention: negative size argument");
+  if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads)
+    return fail(RKV_ERR_INVALID_ARG,
+                "rkv_prefill_attention: num_q_heads must be a positive multiple of num_kv_heads");
+  if (dtype != RKV_F32 && dtype != RKV_BF16)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_prefill_attention: dtype must be RKV_F32 or RKV_BF16");
+  if (block_size != kBS)
+    return fail(RKV_ERR_UNSUPPORTED, "rkv_prefill_attention: block_size must be 16");
+  const int G = num_q_heads / num_kv_heads;
+  PrefillFn fn = dtype == RKV_BF16 ? pick_d<uint16_t>(head_dim, G) : pick_d<float>(head_dim, G);
+  if (!fn)
+    return fail(RKV_ERR_UNSUPPORTED,
+                "rkv_prefill_attention: head_dim must be 32, 64 or 128 and num_q_heads / "
+                "num_kv_heads 1, 2, 4 or 8");
+  if (num_seqs > 65535 || num_kv_heads > 65535)
+    return fail(RKV_ERR_INVALID_ARG,
+                "rkv_prefill_attention: num_seqs and num_kv_heads must be <= 65535");
+  if (num_seqs == 0 || max_q_len == 0 || max_blocks_per_seq == 0) return RKV_OK;
+  if ((int64_t)max_blocks_per_seq * kBS > 0x7fffffff)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_prefill_attention: max_blocks_per_seq too large");
+  if (num_blocks < 1) return fail(RKV_ERR_INVALID_ARG, "rkv_prefill_attention: num_blocks < 1");
+  if (!out || !q || !k_pool || !v_pool || !block_tables || !q_start || !ctx_lens)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_prefill_attention: null pointer argument");
+  if (!aligned16(out) || !aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool))
+    return fail(RKV_ERR_INVALID_ARG,
+                "rkv_prefill_attention: out, q and pools must be 16-byte aligned");
+  const int qs = G == 8 && kQS * 8 > 16 ? 2 : kQS;  // at most 16 waves per workgroup
+  const int qt = 16 * qs;
+  const dim3 grid((unsigned)((max_q_len + qt - 1) / qt), (unsigned)num_kv_heads,
+                  (unsigned)num_seqs);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * G * qs), 0, static_cast<hipStream_t>(stream), out, q, k_pool,
+                     v_pool, block_tables, max_blocks_per_seq, q_start, ctx_lens, num_kv_heads,
+                     num_blocks, max_q_len, scale * kLog2e);
+  return check_launch("rkv_prefill_attention");
+}

@@ -168,4 +168,40 @@ def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     return out
 
 
-__all__ = ["append", "gather", "copy_blocks", "decode_attention", "workspace_bytes", "_lib"]
+def prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                      block_tables: torch.Tensor, q_start: torch.Tensor, ctx_lens: torch.Tensor,
+                      scale: float | None = None, *, max_q_len: int | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal prefill attention: q [total, Hq, D] fp32 -> out [total, Hq, D].
+
+    Sequence b owns rows q_start[b] .. q_start[b+1]-1 (int32 [B+1]); its new
+    tokens are the last ones of its ctx_lens[b] cached tokens (appended
+    beforehand).  max_q_len bounds every sequence's new-token count (computed
+    from q_start, with a device sync, when not given).
+    """
+    _dev(q, "q", torch.float32), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
+    _dev(q_start, "q_start", torch.int32)
+    nb, hkv, bs, d = k_pool.shape
+    total, hq, dq = q.shape
+    B = ctx_lens.shape[0]
+    if dq != d:
+        raise ValueError("q head_dim does not match the pool")
+    if q_start.shape != (B + 1,) or block_tables.shape[0] != B:
+        raise ValueError("q_start must be [B+1] and block_tables [B, max_blocks]")
+    if max_q_len is None:
+        max_q_len = int((q_start[1:] - q_start[:-1]).max().item()) if B else 0
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.zeros_like(q)
+    check(lib().rkv_prefill_attention(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(),
+                                      v_pool.data_ptr(), block_tables.data_ptr(),
+                                      block_tables.shape[1], q_start.data_ptr(),
+                                      ctx_lens.data_ptr(), B, hq, hkv, d, bs, nb, max_q_len,
+                                      float(scale), _dtype_code(k_pool), _stream(q)))
+    return out
+
+
+__all__ = ["append", "gather", "copy_blocks", "decode_attention", "prefill_attention",
+           "workspace_bytes", "_lib"]

@@ -75,3 +75,40 @@ def assert_allclose_ref(got, want, rtol, atol, name=""):
         i = np.unravel_index(np.argmax(np.where(ok, 0, diff)), diff.shape)
         raise AssertionError(f"{name}: mismatch at {i}: got {got[i]} want {want[i]} "
                              f"(max abs diff {diff.max():.3e}, rtol {rtol}, atol {atol})")
+
+
+def ref_prefill_f64(q, k_pool_f32, v_pool_f32, tables, q_start, ctx_lens, scale):
+    """Independent float64 formulation of causal prefill: per sequence, the
+    full score matrix Q K^T * scale plus the reference's additive -1e9 mask
+    above the diagonal (causal_mask_tape), a row softmax, then W V.  Rows
+    whose position is negative are zero."""
+    total, hq, d = q.shape
+    nb, hkv, bs, _ = k_pool_f32.shape
+    g = hq // hkv
+    out = np.zeros((total, hq, d), np.float64)
+    for b in range(len(ctx_lens)):
+        s0, n, L = int(q_start[b]), int(q_start[b + 1] - q_start[b]), int(ctx_lens[b])
+        if n <= 0 or L <= 0:
+            continue
+        pos = np.arange(L)
+        blk = tables[b, pos // bs]
+        K = k_pool_f32[blk, :, pos % bs, :].astype(np.float64)  # [L, Hkv, D]
+        V = v_pool_f32[blk, :, pos % bs, :].astype(np.float64)
+        qpos = L - n + np.arange(n)                              # position of each new token
+        mask = np.where(pos[None, :] > qpos[:, None], -1e9, 0.0)  # [n, L]
+        Q = q[s0:s0 + n].astype(np.float64).reshape(n, hkv, g, d)
+        s = np.einsum("nkgd,lkd->nkgl", Q, K) * scale + mask[:, None, None, :]
+        s -= s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        o = np.einsum("nkgl,lkd->nkgd", p, V).reshape(n, hq, d)
+        o[qpos < 0] = 0.0
+        out[s0:s0 + n] = o
+    return out
+
+
+def make_prefill(rng, n_new, ctx_lens):
+    """q_start offsets for sequences with n_new[b] new tokens."""
+    q_start = np.zeros(len(n_new) + 1, np.int32)
+    q_start[1:] = np.cumsum(n_new)
+    return q_start

@@ -87,3 +87,21 @@ def test_copy_kernels_reject_bad_arguments():
                         None) == RKV_ERR_INVALID_ARG  # f32 -> bf16 not offered
     assert L.rkv_copy_blocks(16, 16, 0, 1, 16, 3, 100, 10, None) == RKV_ERR_INVALID_ARG
     assert L.rkv_copy_blocks(16, 16, 0, 1, 16, 0, 4096, 10, None) == 0
+
+
+def test_prefill_rejects_bad_arguments():
+    """Argument checks of rkv_prefill_attention run before any launch."""
+    L = _lib.lib()
+
+    def call(hq=8, hkv=2, d=128, bs=16, dt=RKV_BF16, B=2, mq=16, mbs=4):
+        return L.rkv_prefill_attention(16, 16, 16, 16, 16, mbs, 16, 16, B, hq, hkv, d, bs, 10, mq,
+                                       0.1, dt, None)
+    assert call(bs=8) == RKV_ERR_UNSUPPORTED
+    assert call(d=48) == RKV_ERR_UNSUPPORTED
+    assert call(hq=6, hkv=2) == RKV_ERR_UNSUPPORTED
+    assert call(hq=7, hkv=2) == RKV_ERR_INVALID_ARG
+    assert call(dt=7) == RKV_ERR_INVALID_ARG
+    assert call(B=-1) == RKV_ERR_INVALID_ARG
+    assert call(B=0) == 0 and call(mq=0) == 0          # nothing to do: no launch
+    assert L.rkv_prefill_attention(None, 16, 16, 16, 16, 4, 16, 16, 2, 8, 2, 128, 16, 10, 16,
+                                   0.1, RKV_BF16, None) == RKV_ERR_INVALID_ARG

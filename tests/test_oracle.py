@@ -318,3 +318,69 @@ def test_multithreaded_oracle_is_identical():
     a = oracle.decode_attention(q, kp, vp, tables, ctx, 0.1)
     b = oracle.decode_attention(q, kp, vp, tables, ctx, 0.1, n_threads=5)
     assert np.array_equal(a, b)
+
+
+# ---- causal prefill over the paged pool -------------------------------------
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 64), (4, 4, 32), (32, 8, 128)])
+def test_prefill_vs_independent_f64(dtype, hq, hkv, d):
+    from tests.helpers import make_prefill, ref_prefill_f64
+    rng = np.random.default_rng(hq * 10 + d)
+    bs = 16
+    n_new = np.array([1, 17, 40, 0, 5], np.int32)
+    ctx = n_new + np.array([0, 0, 100, 7, 33], np.int32)   # square prefills and chunked ones
+    nb = int(sum((c + bs - 1) // bs for c in ctx)) + 5
+    kp, vp, kf, vf = make_pool(rng, nb, hkv, bs, d, dtype)
+    if dtype == "bf16":
+        kf, vf = oracle.pool_as_f32(kp), oracle.pool_as_f32(vp)
+    tables = make_tables(rng, ctx, bs, nb)
+    qs = make_prefill(rng, n_new, ctx)
+    q = rng.standard_normal((int(qs[-1]), hq, d)).astype(np.float32)
+    scale = 1 / math.sqrt(d)
+    got = oracle.prefill_attention(q, kp, vp, tables, qs, ctx, scale)
+    want = ref_prefill_f64(q, kf, vf, tables, qs, ctx, scale)
+    assert np.abs(got - want).max() < 2e-5
+
+
+def test_prefill_square_case_vs_torch_causal_sdpa():
+    """ctx == n (the reference's square causal prefill) against torch's
+    is_causal scaled_dot_product_attention in float64."""
+    from tests.helpers import make_prefill
+    rng = np.random.default_rng(3)
+    hq, hkv, d, bs, n = 8, 2, 64, 16, 70
+    nb = 8
+    kp, vp, kf, vf = make_pool(rng, nb, hkv, bs, d, "f32")
+    tables = make_tables(rng, [n], bs, nb)
+    qs = make_prefill(rng, [n], [n])
+    q = rng.standard_normal((n, hq, d)).astype(np.float32)
+    got = oracle.prefill_attention(q, kp, vp, tables, qs, [n], 0.125)
+    pos = np.arange(n)
+    K = torch.from_numpy(kf[tables[0, pos // bs], :, pos % bs, :]).double()  # [n, Hkv, D]
+    V = torch.from_numpy(vf[tables[0, pos // bs], :, pos % bs, :]).double()
+    Q = torch.from_numpy(q).double().transpose(0, 1)                          # [Hq, n, D]
+    K = K.transpose(0, 1).repeat_interleave(hq // hkv, dim=0).contiguous()
+    V = V.transpose(0, 1).repeat_interleave(hq // hkv, dim=0).contiguous()
+    ref = torch.nn.functional.scaled_dot_product_attention(Q, K, V, is_causal=True, scale=0.125)
+    assert np.abs(got - ref.transpose(0, 1).numpy()).max() < 2e-5
+
+
+def test_prefill_last_token_is_decode_and_negative_positions_are_zero():
+    from tests.helpers import make_prefill
+    rng = np.random.default_rng(4)
+    hq, hkv, d, bs = 4, 2, 32, 16
+    n_new = np.array([9, 3, 1], np.int32)
+    ctx = np.array([40, 3, 2], np.int32)
+    nb = 10
+    kp, vp, _, _ = make_pool(rng, nb, hkv, bs, d, "bf16")
+    tables = make_tables(rng, ctx, bs, nb)
+    qs = make_prefill(rng, n_new, ctx)
+    q = rng.standard_normal((int(qs[-1]), hq, d)).astype(np.float32)
+    got = oracle.prefill_attention(q, kp, vp, tables, qs, ctx, 0.2)
+    # the last new token of each sequence attends to its whole context: a decode row
+    last = qs[1:] - 1
+    dec = oracle.decode_attention(q[last], kp, vp, tables, ctx, 0.2)
+    assert np.array_equal(got[last], dec)
+    # more new tokens than context: the rows before position 0 are zero
+    bad = oracle.prefill_attention(q, kp, vp, tables, qs, np.array([40, 1, 2], np.int32), 0.2)
+    assert np.all(bad[qs[1]:qs[1] + 2] == 0.0) and np.any(bad[qs[1] + 2] != 0.0)
