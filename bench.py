@@ -12,9 +12,14 @@ KV pool (32 x ~604 MB, far beyond the 256 MB Infinity Cache, so every call
 streams from HBM).  GEMMs of the model are not part of this path.
 
 Prints one JSON line.  value = algorithmic bytes / time over the whole step
-(both split-K passes and launch gaps); roofline.achieved = algorithmic
-bytes / the partition kernel's own average duration, from HIP events
-recorded on the launch stream around every launch in the timed region.
+(both split-K passes and the gaps between launches), the 32 calls of a step
+captured once in a HIP graph and replayed K times, as a serving loop replays
+its step; roofline.achieved = algorithmic bytes / the partition kernel's own
+average duration, from HIP events recorded on the launch stream around every
+launch of a second, eagerly launched timed region of K steps.
+
+Other workloads (--workload config0|config1|config3|config4|prefill) print
+their own line.
 """
 from __future__ import annotations
 
@@ -101,7 +106,8 @@ def copy_bandwidth(torch, dev, nbytes=2 << 30, reps=10):
 def cpu_baseline(torch, layers, ctx, threads):
     """The C oracle (a restatement of the reference's CPU semantics) on a
     bounded sample: layer 0 of the workload, all 64 sequences, timed with
-    `threads` POSIX threads, plus one single-thread pass over 4 sequences."""
+    `threads` POSIX threads, repeated for about 10 s, plus one single-thread
+    pass over 4 sequences."""
     import numpy as np
     import oracle
     q, k, v, tables = layers[0]
@@ -112,7 +118,7 @@ def cpu_baseline(torch, layers, ctx, threads):
     scale = 1.0 / math.sqrt(D)
     oracle.decode_attention(qh[:1], kh, vh, th[:1], ctx[:1], scale)  # load + warm
     reps, t_mt = 0, 0.0
-    while reps < 3 and t_mt < 10.0:
+    while t_mt < 10.0 and reps < 500:  # about 10 s of CPU work
         t0 = time.perf_counter()
         oracle.decode_attention(qh, kh, vh, th, ctx, scale, n_threads=threads)
         t_mt += time.perf_counter() - t0
@@ -616,16 +622,39 @@ def main():
         kv.decode_attention(q, k, v, t, ctx_d, scale, max_context=max_ctx, out=outs[i],
                             workspace=ws, passes=passes)
 
-    for _ in range(args.warmup):
-        for i in range(n_layers):
-            call(i, "both")
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(args.warmup):
+            for i in range(n_layers):
+                call(i, "both")
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
 
+    # (1) value: the step as a serving loop runs it -- the 32 calls (both
+    # passes each) captured once in a HIP graph; K steps = K replays.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n_layers):
+            call(i, "both")
+    graph.replay()
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    marks = [[(ev(), ev(), ev()) for _ in range(n_layers)] for _ in range(args.steps)]
     start, stop = ev(), ev()
     torch.cuda.synchronize()
     start.record()
+    for s in range(args.steps):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_step = start.elapsed_time(stop) / args.steps
+    del graph
+
+    # (2) roofline: the same steps launched eagerly, HIP events on the launch
+    # stream around every partition and merge launch.
+    marks = [[(ev(), ev(), ev()) for _ in range(n_layers)] for _ in range(args.steps)]
+    e0, e1 = ev(), ev()
+    torch.cuda.synchronize()
+    e0.record()
     for s in range(args.steps):
         for i in range(n_layers):
             a, m, e = marks[s][i]
@@ -634,11 +663,9 @@ def main():
             m.record()
             call(i, "merge")
             e.record()
-    stop.record()
+    e1.record()
     torch.cuda.synchronize()
-
-    total_ms = start.elapsed_time(stop)
-    ms_step = total_ms / args.steps
+    ms_step_eager = e0.elapsed_time(e1) / args.steps
     part_ms = [a.elapsed_time(m) for row in marks for (a, m, e) in row]
     merge_ms = [m.elapsed_time(e) for row in marks for (a, m, e) in row]
     avg_part_us = 1e3 * sum(part_ms) / len(part_ms)
@@ -673,10 +700,12 @@ def main():
                    "batch": B, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
                    "block_size": BS, "kv_dtype": "bf16", "accumulate": "fp32",
                    "context": [CTX_LO, CTX_HI], "mean_context": float(ctx.mean()),
-                   "layers_per_step": n_layers, "step": "one decode token: 32 attention calls"},
+                   "layers_per_step": n_layers,
+                   "step": "one decode token: 32 attention calls, replayed from a HIP graph"},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
         "decode_tokens_per_s_b64": round(tokens_per_s, 1),
         "us_per_call": round(call_us, 2),
+        "step_ms_eager_with_events": round(ms_step_eager, 4),
         "partition_kernel_us": round(avg_part_us, 2),
         "merge_kernel_us": round(avg_merge_us, 2),
         "algorithmic_bytes_per_call": bytes_call,

@@ -199,3 +199,49 @@ def test_decode_is_deterministic(dev):
     a = run_gpu(dev, q, kp, vp, tables, ctx, 0.09)
     b = run_gpu(dev, q, kp, vp, tables, ctx, 0.09)
     assert np.array_equal(a, b)
+
+
+def test_decode_graph_replay_matches_eager(dev):
+    """Decode calls of several layers (partition + merge passes) captured in
+    one HIP graph, as the bench and a serving step replay them: every replay,
+    with new queries written eagerly between replays, equals the eager calls
+    bit for bit."""
+    say("decode graph replay")
+    rng = np.random.default_rng(12)
+    ctx = contexts(rng, 24, 1, 3000)
+    layers = []
+    for i in range(3):
+        q, kp, vp, _, _, tables = case(20 + i, 24, 32, 8, 128, ctx, "bf16")
+        layers.append([to_dev(q, dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(tables, dev)])
+    ctx_d = to_dev(ctx, dev)
+    mc = 3008
+    ws = torch.zeros(kv.workspace_bytes(24, 32, 128, mc), dtype=torch.uint8, device=dev)
+    outs = [torch.zeros_like(l[0]) for l in layers]
+
+    def step(dst):
+        for (q, k, v, t), o in zip(layers, dst):
+            kv.decode_attention(q, k, v, t, ctx_d, 0.09, max_context=mc, out=o, workspace=ws)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(outs)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(outs)
+    g = torch.Generator(device=dev).manual_seed(3)
+    for rep in range(4):
+        for l in layers:
+            l[0].normal_(generator=g)
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = [torch.zeros_like(o) for o in outs]
+        step(eager)
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep}"
