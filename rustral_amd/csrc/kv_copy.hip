@@ -7,8 +7,21 @@
 // bytes per instruction.  No LDS: there is no reuse to stage.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace rkv {
 namespace {
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte store of the bits of v (any 16-byte trivially copyable type).
+// (Non-temporal stores were measured: +3% on the bf16 gather, -34% on the
+// fp32-output gather; plain stores are kept.)
+template <typename V>
+__device__ __forceinline__ void store16(void* p, const V& v) {
+  static_assert(sizeof(V) == 16, "16-byte store");
+  *static_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
+}
 
 struct alignas(16) F8 {  // 8 floats = 32 bytes
   float4 a, b;
@@ -20,9 +33,8 @@ __device__ __forceinline__ F8 load_f8(const float* p) {
 }
 
 __device__ __forceinline__ void store_f8(float* p, const F8& x) {
-  float4* v = reinterpret_cast<float4*>(p);
-  v[0] = x.a;
-  v[1] = x.b;
+  store16(p, x.a);
+  store16(p + 4, x.b);
 }
 
 __device__ __forceinline__ uint4 f8_to_bf16x8(const F8& x) {
@@ -99,14 +111,15 @@ __global__ __launch_bounds__(256) void gather_kernel(
     int64_t num_blocks, int max_ctx) {
   const int j = blockIdx.x, b = blockIdx.y;
   const bool is_v = blockIdx.z != 0;
+  // the three per-sequence reads are independent: issued together
   int L = ctx_lens[b];
+  const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + j];
+  int64_t seq_base = out_offsets ? out_offsets[b] : 0;
   L = L < 0 ? 0 : L;
   const int cap = max_blocks_per_seq * block_size;
   L = L > cap ? cap : L;
-  int64_t seq_base;
   int row_stride;  // output rows per head
   if (out_offsets) {
-    seq_base = out_offsets[b];
     if (seq_base < 0 || (seq_base & 7)) return;  // 16-byte vector stores need 8-element alignment
     row_stride = L;
   } else {
@@ -116,23 +129,43 @@ __global__ __launch_bounds__(256) void gather_kernel(
   }
   const int p0 = j * block_size;
   if (p0 >= L) return;
-  const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + j];
   if (blk < 0 || blk >= num_blocks) return;
   const int nt = (L - p0) < block_size ? (L - p0) : block_size;
   const TIn* src_pool = is_v ? v_pool : k_pool;
   TOut* dst_all = is_v ? v_out : k_out;
   const int per_head = (nt * head_dim) >> 3;  // 8-element units per head
   const int units = num_kv_heads * per_head;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const int h = u / per_head, r = u - h * per_head;
-    const TIn* s = src_pool + ((int64_t)blk * num_kv_heads + h) * block_size * head_dim + r * 8;
-    TOut* d = dst_all + seq_base + ((int64_t)h * row_stride + p0) * head_dim + r * 8;
-    if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 2) {
-      *reinterpret_cast<uint4*>(d) = *reinterpret_cast<const uint4*>(s);
-    } else if constexpr (sizeof(TIn) == 2) {
-      store_f8(reinterpret_cast<float*>(d), bf16x8_to_f8(*reinterpret_cast<const uint4*>(s)));
-    } else {
-      store_f8(reinterpret_cast<float*>(d), load_f8(reinterpret_cast<const float*>(s)));
+  // Up to UNR units per thread per round: every load of the round is issued
+  // before the first store, so a thread keeps UNR loads in flight.
+  constexpr int UNR = 8;
+  using In = typename std::conditional<sizeof(TIn) == 2, uint4, F8>::type;
+  for (int u0 = threadIdx.x; u0 < units; u0 += UNR * blockDim.x) {
+    In x[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * blockDim.x;
+      if (u < units) {
+        const int h = u / per_head, r = u - h * per_head;
+        const TIn* s = src_pool + ((int64_t)blk * num_kv_heads + h) * block_size * head_dim + r * 8;
+        if constexpr (sizeof(TIn) == 2)
+          x[k] = *reinterpret_cast<const uint4*>(s);
+        else
+          x[k] = load_f8(reinterpret_cast<const float*>(s));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * blockDim.x;
+      if (u < units) {
+        const int h = u / per_head, r = u - h * per_head;
+        TOut* d = dst_all + seq_base + ((int64_t)h * row_stride + p0) * head_dim + r * 8;
+        if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 2)
+          store16(d, x[k]);
+        else if constexpr (sizeof(TIn) == 2)
+          store_f8(reinterpret_cast<float*>(d), bf16x8_to_f8(x[k]));
+        else
+          store_f8(reinterpret_cast<float*>(d), x[k]);
+      }
     }
   }
 }
@@ -149,7 +182,20 @@ __global__ __launch_bounds__(256) void copy_blocks_kernel(
   const uint4* s = reinterpret_cast<const uint4*>(base + src * block_bytes);
   uint4* d = reinterpret_cast<uint4*>(base + dst * block_bytes);
   const int64_t n = block_bytes >> 4;
-  for (int64_t u = threadIdx.x; u < n; u += blockDim.x) d[u] = s[u];
+  constexpr int UNR = 8;  // loads in flight per thread before the stores
+  for (int64_t u0 = threadIdx.x; u0 < n; u0 += UNR * blockDim.x) {
+    uint4 x[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int64_t u = u0 + k * blockDim.x;
+      if (u < n) x[k] = s[u];
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int64_t u = u0 + k * blockDim.x;
+      if (u < n) store16(d + u, x[k]);
+    }
+  }
 }
 
 int check_common(int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, int dtype) {
