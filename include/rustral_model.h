@@ -107,6 +107,46 @@ void rkv_decoder_destroy(rkv_decoder* dec);
 int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int n_prompt, int n_new,
                          int32_t* out_tokens, float* out_logits);
 
+/* ---- serving engine (continuous batching over the decoder) ----------------------
+ * Replaces ServingEngine (crates/nn/src/continuous_batching.rs:493-537).  The
+ * reference's step emits a dummy token for every scheduled request
+ * (:516-524); here a step runs the decoder above over the scheduler's batch
+ * (include/rustral_serving.h, which owns the block manager): all input tokens
+ * of the batch as rows -- a prompt in prefill, the last generated token
+ * otherwise, prompt + generated when resuming after a preemption -- their K/V
+ * appended into paged fp32 pools of num_blocks 16-token blocks per layer, one
+ * rkv_prefill_attention call per layer for the whole batch (a decode row is
+ * its single-token case), and one greedy token per request from its last
+ * row, handed to rkv_sched_update.  Every call synchronizes the stream once
+ * (the tokens come back to the host for the scheduler). */
+typedef struct rkv_engine rkv_engine;
+struct rkv_scheduler;
+
+/* Uploads the parameters and allocates the pools on the current device; the
+ * engine's scheduler admits at most max_batch_size running requests and
+ * bounds prompt + max_tokens by cfg->max_seq.  NULL on failure. */
+rkv_engine* rkv_engine_create(const rkv_decoder_config* cfg, const float* host_params,
+                              int64_t n_params, int64_t num_blocks, int max_batch_size,
+                              void* stream);
+void rkv_engine_destroy(rkv_engine* e);
+
+/* ServingEngine::submit (:507-510): queues a request, returns its id. */
+int64_t rkv_engine_submit(rkv_engine* e, const int32_t* prompt, int n_prompt, int max_tokens,
+                          int priority);
+
+/* ServingEngine::step (:513-535): returns the number of requests run (0 when
+ * nothing is running) or a negative code (RKV_ERR_OOM when the pool cannot
+ * hold a request's next token, as Scheduler::update reports it). */
+int rkv_engine_step(rkv_engine* e);
+
+/* ServingEngine::run_to_completion (:538-543), bounded by max_steps; returns
+ * the number of steps run or a negative code. */
+int rkv_engine_run(rkv_engine* e, int max_steps);
+
+/* The engine's scheduler: rkv_sched_generated / rkv_sched_stats read the
+ * results.  Owned by the engine. */
+struct rkv_scheduler* rkv_engine_scheduler(rkv_engine* e);
+
 /* ---- seeded generator (host) -------------------------------------------------
  * PCG64 (XSL-RR 128/64; state' = state * 0x2360ED051FC65DA44385DF649FCCF645
  * + inc, output from state') with state = seed and inc = 0xDA3E39CB94B95BDB *

@@ -69,6 +69,12 @@ SIGNATURES = {
     "rkv_decoder_create": (_p, [_p, _p, _i64, _p]),
     "rkv_decoder_destroy": (None, [_p]),
     "rkv_decoder_generate": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rkv_engine_create": (_p, [_p, _p, _i64, _i64, _i, _p]),
+    "rkv_engine_destroy": (None, [_p]),
+    "rkv_engine_submit": (_i64, [_p, _p, _i, _i, _i]),
+    "rkv_engine_step": (_i, [_p]),
+    "rkv_engine_run": (_i, [_p, _i]),
+    "rkv_engine_scheduler": (_p, [_p]),
     "rkv_rng_raw": (_i, [C.c_uint64, _p, _i64]),
     "rkv_fill_normal": (_i, [_p, _i64, C.c_uint64, _f]),
 }

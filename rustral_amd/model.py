@@ -91,6 +91,53 @@ class Decoder:
         return (toks, lg[:n_new]) if logits else toks
 
 
+class Engine:
+    """Continuous-batching serving engine on the current device (rkv_engine_*):
+    the scheduler's batch runs through the decoder each step."""
+
+    def __init__(self, cfg: DecoderConfig, params: np.ndarray, num_blocks: int,
+                 max_batch_size: int = 8, device=None):
+        from .serving import Scheduler
+        params = np.ascontiguousarray(params, np.float32)
+        dev = torch.device("cuda:0") if device is None else torch.device(device)
+        self._stream = torch.cuda.current_stream(dev).cuda_stream
+        self.cfg = cfg
+        h = lib().rkv_engine_create(C.byref(cfg), _p(params), params.size, num_blocks,
+                                    max_batch_size, self._stream)
+        if not h:
+            raise RkvError(-1, lib().rkv_last_error().decode())
+        self._h = h
+        self.scheduler = Scheduler._borrow(lib().rkv_engine_scheduler(h), self)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self.scheduler = None
+            lib().rkv_engine_destroy(self._h)
+            self._h = None
+
+    def submit(self, prompt, max_tokens: int, priority: int = 1) -> int:
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        rid = lib().rkv_engine_submit(self._h, _p(prompt), len(prompt), max_tokens, priority)
+        if rid < 0:
+            check(int(rid))
+        return int(rid)
+
+    def step(self) -> int:
+        n = lib().rkv_engine_step(self._h)
+        if n < 0:
+            check(n)
+        return n
+
+    def run(self, max_steps: int = 1 << 30) -> int:
+        n = lib().rkv_engine_run(self._h, max_steps)
+        if n < 0:
+            check(n)
+        return n
+
+    def generated(self, request_id: int) -> list[int]:
+        return self.scheduler.generated(request_id)
+
+
 # ---- device ops on torch tensors ---------------------------------------------------
 
 def linear(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:

@@ -129,8 +129,16 @@ class Scheduler:
         self.cache = PagedCache(block_size, num_blocks,
                                 _handle=lib().rkv_sched_block_manager(h), _owner=self)
 
+    @classmethod
+    def _borrow(cls, handle, owner):
+        """A view of a scheduler owned by another object (the serving engine)."""
+        s = cls.__new__(cls)
+        s._h, s._borrowed, s._owner = handle, True, owner
+        s.cache = PagedCache(0, 0, _handle=lib().rkv_sched_block_manager(handle), _owner=s)
+        return s
+
     def __del__(self):
-        if getattr(self, "_h", None):
+        if getattr(self, "_h", None) and not getattr(self, "_borrowed", False):
             lib().rkv_sched_destroy(self._h)
             self._h = None
 

@@ -1,0 +1,94 @@
+"""The continuous-batching engine (rkv_engine_*) on the GPU: every request's
+tokens equal what the CPU oracle decoder generates for that request alone,
+however the scheduler batches, pauses and resumes it.
+
+The engine runs a request's prompt through causal prefill attention in one
+step and then decodes inside mixed batches; the oracle feeds the prompt one
+token at a time.  Both are within the fp32 attention tolerance of each other,
+so the greedy tokens agree unless two logits tie within ~1e-5 (the test
+prints the smallest top-1 / top-2 margin it relies on).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from rustral_amd import model
+from rustral_amd._lib import RKV_ERR_OOM, RkvError
+from rustral_amd.serving import LOW, NORMAL
+from tests.gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+EOS = 2
+
+
+def expected(params, prompt, max_tokens):
+    """Oracle tokens for one request, cut after the first EOS as the
+    scheduler completes a request (Request::should_complete)."""
+    toks, lg = oracle.decoder_generate(oracle.decoder_config(), params, prompt, max_tokens,
+                                       logits=True)
+    toks = toks.tolist()
+    if EOS in toks:
+        toks = toks[:toks.index(EOS) + 1]
+    srt = np.sort(lg[:len(toks)], axis=1)
+    return toks, float((srt[:, -1] - srt[:, -2]).min())
+
+
+def requests(seed, lens, max_tokens):
+    rng = np.random.default_rng(seed)
+    return [(rng.integers(0, 1000, n).astype(np.int32), m) for n, m in zip(lens, max_tokens)]
+
+
+def test_engine_requests_match_oracle(dev):
+    say("engine: 8 requests, max batch 4")
+    cfg = model.config()
+    params = model.init_params(cfg, seed=0, std=0.02)
+    reqs = requests(1, [5, 20, 33, 1, 12, 40, 7, 64], [10, 25, 8, 30, 16, 12, 20, 9])
+    eng = model.Engine(cfg, params, num_blocks=64, max_batch_size=4)
+    ids = [eng.submit(p, m) for p, m in reqs]
+    steps = eng.run()
+    assert steps > 0
+    st = eng.scheduler.stats()
+    assert st["completed"] == len(reqs) and st["running"] == 0 and st["pending"] == 0
+    margins = []
+    for rid, (p, m) in zip(ids, reqs):
+        want, margin = expected(params, p, m)
+        margins.append(margin)
+        assert eng.generated(rid) == want, f"request {rid}"
+    say(f"smallest top-1/top-2 logit margin {min(margins):.3e}")
+
+
+def test_engine_preempted_requests_recompute_to_the_same_tokens(dev):
+    """Low-priority requests are paused under batch pressure and resumed by
+    recomputing prompt + generated tokens; their tokens do not change."""
+    say("engine: preemption and recompute")
+    cfg = model.config()
+    params = model.init_params(cfg, seed=0, std=0.02)
+    reqs = requests(2, [9, 30, 14, 22, 6], [20, 12, 18, 15, 24])
+    prio = [NORMAL, LOW, NORMAL, LOW, NORMAL]
+    eng = model.Engine(cfg, params, num_blocks=64, max_batch_size=4)
+    ids = [eng.submit(p, m, pr) for (p, m), pr in zip(reqs, prio)]
+    paused_seen = 0
+    for _ in range(500):
+        if eng.step() == 0:
+            break
+        paused_seen = max(paused_seen, eng.scheduler.stats()["paused"])
+    assert eng.scheduler.stats()["completed"] == len(reqs)
+    assert paused_seen > 0, "the scenario is meant to preempt"
+    for rid, (p, m) in zip(ids, reqs):
+        want, _ = expected(params, p, m)
+        assert eng.generated(rid) == want, f"request {rid}"
+
+
+def test_engine_reports_pool_exhaustion(dev):
+    say("engine: KV pool exhaustion")
+    cfg = model.config()
+    params = model.init_params(cfg, seed=0, std=0.02)
+    eng = model.Engine(cfg, params, num_blocks=3, max_batch_size=2)
+    (p, _), = requests(3, [40], [1])
+    eng.submit(p, 20)
+    with pytest.raises(RkvError) as e:
+        for _ in range(30):
+            if eng.step() == 0:
+                break
+    assert e.value.code == RKV_ERR_OOM
