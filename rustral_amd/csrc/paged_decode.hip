@@ -1,23 +1,18 @@
 // paged_decode.hip -- single-token paged decode attention with GQA, split-K,
 // for gfx950 (CDNA4, wave64).
 //
-// Pass 1 splits every sequence into partitions of P tokens and produces, per
-// (partition, query head), the partial softmax state (m, l, acc); the G =
-// Hq/Hkv query heads that share a KV head are served together, so every K/V
-// byte is read from HBM once.  Two implementations of pass 1 share the lane
-// mapping and the arithmetic:
-//   * decode_stream_kernel (the default): SPLIT waves per (partition, KV
-//     head, sequence), each streaming a slice of the partition's K and V
-//     tiles through a register ring, QK^T on the matrix cores for bf16
-//     pools; the waves combine their states in LDS.
-//   * decode_partition_kernel (RKV_DECODE_STREAM=0): NW waves that issue all
-//     their K and V loads before any arithmetic.
-// Common to both:
+// Pass 1 (decode_stream_kernel) splits every sequence into partitions of P
+// tokens and produces, per (partition, query head), the partial softmax state
+// (m, l, acc); the G = Hq/Hkv query heads that share a KV head are served by
+// the same workgroup, so every K/V byte is read from HBM once.  SPLIT waves
+// per (partition, KV head, sequence) each stream a slice of the partition's
+// K and V tiles through a register ring and combine their states in LDS.
 //   * Lane mapping: a wave reads one (block, head) tile [BS][D] as NL
 //     coalesced 1 KiB loads: lane l takes 16 bytes of token row l / LPT at
 //     dims (l % LPT) * E ... + E, where E = 16 / sizeof(elem) and
 //     LPT = D / E lanes cover one row.
-//   * QK^T (VALU form): each lane multiplies its E key elements with the
+//   * QK^T: on the matrix cores for bf16 pools (below); for fp32 pools each
+//     lane multiplies its E key elements with the
 //     matching E elements of the G (pre-scaled) queries held in registers,
 //     then a DPP sum over the LPT lanes of the row gives the G scores.
 //   * Scores go to LDS; the max and the sum of exp2(s - max) are taken over
@@ -89,245 +84,6 @@ __device__ __forceinline__ void to_float(const uint4& w, float (&f)[4]) {
   f[3] = __uint_as_float(w.w);
 }
 
-template <typename T, int D, int G, int BS, int NW, int TPW>
-__global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
-    float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
-    const float* __restrict__ q, const void* __restrict__ k_pool_,
-    const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
-    int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens, int ctx_cap, int num_kv_heads,
-    int64_t num_blocks, float q_scale, int max_parts) {
-  const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
-  const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
-  constexpr int E = Traits<T>::E;
-  constexpr int LPT = D / E;     // lanes per token row
-  constexpr int TPL = 64 / LPT;  // token rows per wave-load
-  constexpr int NL = BS / TPL;   // wave-loads per (block, head) tile
-  constexpr int P = TPW * NW * BS;
-  constexpr int NT = NW * 64;
-  static_assert(D % E == 0 && 64 % LPT == 0 && BS % TPL == 0, "unsupported tile shape");
-
-  __shared__ __align__(16) float s_p[P * G];  // scores, then probabilities [token][g]
-  __shared__ float s_red[NW][G];
-  __shared__ float s_m[G], s_l[G];
-  __shared__ __align__(16) float s_acc[NW][G * D];
-
-  const int part = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
-  const int num_q_heads = num_kv_heads * G;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int slot = lane / LPT, dl = lane % LPT;
-
-  const int64_t head0 = (int64_t)b * num_q_heads + kh * G;  // first query head row
-
-  // Everything whose address does not depend on the context length is
-  // requested before the length arrives: the context length, this wave's
-  // block ids (index clamped into the table), the partition's first block id
-  // and the queries.  The KV loads then wait on one round trip instead of a
-  // chain of them.
-  int L = ctx_lens[b];
-  int32_t pbs[TPW];
-  const int lb0 = part * (P / BS);
-  const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int lb = lb0 + w + NW * i;
-    const int lbc = lb < max_blocks_per_seq ? lb : max_blocks_per_seq - 1;
-    pbs[i] = lbc >= 0 ? tab[lbc] : -1;
-  }
-  int32_t pb_first = lb0 < max_blocks_per_seq ? tab[lb0] : -1;
-  float qf[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* qp = q + (head0 + g) * D + dl * E;
-#pragma unroll
-    for (int e = 0; e < E; e += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(qp + e);
-      qf[g][e + 0] = v.x;
-      qf[g][e + 1] = v.y;
-      qf[g][e + 2] = v.z;
-      qf[g][e + 3] = v.w;
-    }
-  }
-  L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
-  const int nparts = (L + P - 1) / P;
-  if (L == 0) {
-    if (part == 0)
-      for (int o = tid; o < G * D; o += NT) out[head0 * D + o] = 0.0f;
-    return;
-  }
-  if (part >= nparts) return;
-
-  // ---- issue every K load, then every V load, of this wave ----
-  // Loads are unconditional so the compiler keeps them back to back.  A tile
-  // past the context or with an invalid block id re-reads the partition's
-  // first tile (already requested by wave 0, so the L2 serves it), or block 0
-  // when that id is invalid too; its scores are masked and its V is zeroed.
-  if (pb_first < 0 || pb_first >= num_blocks) pb_first = 0;
-  int64_t base[TPW];
-  bool tile_ok[TPW], tile_full[TPW];
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int tbase = (lb0 + w + NW * i) * BS;
-    const int32_t pb = pbs[i];
-    const bool ok = (tbase < L) && pb >= 0 && pb < num_blocks;
-    tile_ok[i] = ok;
-    tile_full[i] = ok && tbase + BS <= L;
-    base[i] = ((int64_t)(ok ? pb : pb_first) * num_kv_heads + kh) * BS * D + dl * E;
-  }
-  uint4 kr[TPW][NL], vr[TPW][NL];
-#pragma unroll
-  for (int i = 0; i < TPW; ++i)
-#pragma unroll
-    for (int n = 0; n < NL; ++n)
-      kr[i][n] = *reinterpret_cast<const uint4*>(k_pool + base[i] + (n * TPL + slot) * D);
-#pragma unroll
-  for (int i = 0; i < TPW; ++i)
-#pragma unroll
-    for (int n = 0; n < NL; ++n)
-      vr[i][n] = *reinterpret_cast<const uint4*>(v_pool + base[i] + (n * TPL + slot) * D);
-
-  // ---- phase 1: scores ----
-  const int tok0 = part * P;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-#pragma unroll
-    for (int n = 0; n < NL; ++n) {
-      float kf[E];
-      to_float(kr[i][n], kf);
-      float s[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float a = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) a = fmaf(qf[g][e], kf[e], a);
-        s[g] = group_sum<LPT>(a) * q_scale;  // scale after the dot
-      }
-      const int tp = (w + NW * i) * BS + n * TPL + slot;  // token within the partition
-      const bool valid = tile_ok[i] && (tok0 + tp < L);
-      if (dl == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) s_p[tp * G + g] = valid ? s[g] : -INFINITY;
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- softmax statistics over the partition ----
-  {
-    float mloc[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) mloc[g] = -INFINITY;
-    for (int t = tid; t < P; t += NT)
-#pragma unroll
-      for (int g = 0; g < G; ++g) mloc[g] = fmaxf(mloc[g], s_p[t * G + g]);
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      mloc[g] = wave_max(mloc[g]);
-      if (lane == 0) s_red[w][g] = mloc[g];
-    }
-    __syncthreads();
-    float m[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      m[g] = s_red[0][g];
-#pragma unroll
-      for (int x = 1; x < NW; ++x) m[g] = fmaxf(m[g], s_red[x][g]);
-    }
-    __syncthreads();
-    float lloc[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) lloc[g] = 0.0f;
-    for (int t = tid; t < P; t += NT)
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float s = s_p[t * G + g];
-        const float p = (s == -INFINITY) ? 0.0f : exp2f(s - m[g]);
-        s_p[t * G + g] = p;
-        lloc[g] += p;
-      }
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      lloc[g] = wave_sum(lloc[g]);
-      if (lane == 0) s_red[w][g] = lloc[g];
-    }
-    __syncthreads();
-    if (tid == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float l = 0.0f;
-#pragma unroll
-        for (int x = 0; x < NW; ++x) l += s_red[x][g];
-        s_m[g] = m[g];
-        s_l[g] = l;
-      }
-    }
-  }
-
-  // ---- phase 2: PV ----
-  float acc[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[g][e] = 0.0f;
-#pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    if (!tile_full[i]) {  // wave-uniform: only the last tile of a sequence, or a bad id
-      const int tbase = (lb0 + w + NW * i) * BS;
-#pragma unroll
-      for (int n = 0; n < NL; ++n)
-        if (!tile_ok[i] || tbase + n * TPL + slot >= L) vr[i][n] = make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int n = 0; n < NL; ++n) {
-      float vf[E];
-      to_float(vr[i][n], vf);
-      const int tp = (w + NW * i) * BS + n * TPL + slot;
-      float p[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) p[g] = s_p[tp * G + g];
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p[g], vf[e], acc[g][e]);
-    }
-  }
-  // sum over the TPL token rows of the wave
-#pragma unroll
-  for (int o = LPT; o < 64; o <<= 1)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
-  if (slot == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < E; e += 4)
-        *reinterpret_cast<float4*>(&s_acc[w][g * D + dl * E + e]) =
-            make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
-  }
-  __syncthreads();
-
-  // ---- sum over waves, then finish or emit a partial ----
-  for (int o = tid; o < G * D; o += NT) {
-    float v = 0.0f;
-#pragma unroll
-    for (int x = 0; x < NW; ++x) v += s_acc[x][o];
-    const int g = o / D, d = o - g * D;
-    const float l = s_l[g];
-    if (nparts == 1) {
-      out[(head0 + g) * D + d] = l > 0.0f ? v / l : 0.0f;
-    } else {
-      const int64_t row = (head0 + g) * max_parts + part;
-      part_acc[row * D + d] = v;
-      if (d == 0) {
-        part_ml[row * 2 + 0] = s_m[g];
-        part_ml[row * 2 + 1] = l;
-      }
-    }
-  }
-}
-
 // ---- streaming variant ---------------------------------------------------------
 // SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
 // item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
@@ -335,11 +91,8 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
 // tile t + R are issued as soon as tile t has been consumed, so a wave always
 // has R tiles (R KiB x 4 for bf16 D=128) in flight and its arithmetic overlaps
 // its own loads.  Scores live in wave-private LDS; the only barrier is the
-// final combine of the SPLIT softmax states (m, l, acc) through LDS.  (KHW > 1
-// instead puts KHW adjacent KV heads of one partition in a workgroup, one wave
-// each, with SPLIT = 1.)
-// Lane mapping and arithmetic are those of decode_partition_kernel, except
-// that for bf16 pools QK^T runs on the matrix cores (MFMA = true): one
+// final combine of the SPLIT softmax states (m, l, acc) through LDS.
+// For bf16 pools QK^T runs on the matrix cores (MFMA = true): one
 // v_mfma_f32_16x16x32_bf16 per 32 dims of a 16-token tile with
 //   A (16 x 32) = queries: rows 0..G-1 = bf16(q) of the G heads, rows
 //                 G..2G-1 = bf16(q - bf16(q)), other rows zero.  hi + lo keeps
@@ -349,8 +102,8 @@ __global__ __launch_bounds__(NW * 64) void decode_partition_kernel(
 //   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
 // (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
 // D[4(l/16)+r][l%16].)  PV stays on the VALU.
-template <typename T, int D, int G, int BS, int NTILE, int R, int KHW, int SPLIT>
-__global__ __launch_bounds__(64 * KHW * SPLIT) void decode_stream_kernel(
+template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
     float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
     const float* __restrict__ q, const void* __restrict__ k_pool_,
     const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
@@ -367,18 +120,16 @@ __global__ __launch_bounds__(64 * KHW * SPLIT) void decode_stream_kernel(
   constexpr int NT = 2 * NTW;    // tiles streamed: K then V
   static_assert(D % E == 0 && 64 % LPT == 0 && BS % TPL == 0 && R >= 1 && R <= NT,
                 "unsupported tile shape");
-  static_assert(NTILE % SPLIT == 0 && (SPLIT == 1 || KHW == 1), "SPLIT waves share one KV head");
+  static_assert(NTILE % SPLIT == 0, "the partition splits evenly over the waves");
 
-  __shared__ __align__(16) float s_pw[KHW * SPLIT][NTW * BS * G];  // per wave: scores, then probabilities
+  __shared__ __align__(16) float s_pw[SPLIT][NTW * BS * G];  // per wave: scores, then probabilities
 
-  // KHW waves = KHW consecutive KV heads of one (partition, sequence): the
-  // waves stay co-scheduled and read the adjacent head tiles of each block
-  // (KHW * 4 KiB contiguous for bf16 D=128) at the same time.
+  // The SPLIT waves stream consecutive NTW-tile slices of one partition and
+  // combine their softmax states in LDS at the end.  The grid is KV-head
+  // major: the Hkv workgroups of one (partition, sequence) are consecutive.
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // SPLIT > 1: the SPLIT waves stream consecutive NTW-tile slices of one
-  // partition and combine their softmax states in LDS at the end.
-  const int kh = blockIdx.x * KHW + (SPLIT > 1 ? 0 : w), part = blockIdx.y, b = blockIdx.z;
-  const int sub = SPLIT > 1 ? w : 0;
+  const int kh = blockIdx.x, part = blockIdx.y, b = blockIdx.z;
+  const int sub = w;
   float* __restrict__ s_p = s_pw[w];
   const int num_q_heads = num_kv_heads * G;
   const int lane = threadIdx.x & 63;
@@ -773,39 +524,28 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge_kernel(
 // ---- dispatch ----------------------------------------------------------------
 
 constexpr int kBS = 16;
-// Tokens per partition and waves per workgroup (bf16 pools; fp32 D=128 uses
-// twice the waves so a wave holds at most 16 16-byte K+V loads per lane).
+// Tokens per partition, waves per partition (each streams a slice) and the
+// register ring depth in 16-byte loads per lane.
 #ifndef RKV_DECODE_P
 #define RKV_DECODE_P 512
 #endif
-#ifndef RKV_DECODE_NW
-#define RKV_DECODE_NW 4
-#endif
-constexpr int kP = RKV_DECODE_P;
-#ifndef RKV_DECODE_STREAM
-#define RKV_DECODE_STREAM 1
+#ifndef RKV_DECODE_SPLIT
+#define RKV_DECODE_SPLIT 4
 #endif
 #ifndef RKV_DECODE_RING_LOADS
 #define RKV_DECODE_RING_LOADS 16
 #endif
-constexpr bool kStream = RKV_DECODE_STREAM != 0;
-
+constexpr int kP = RKV_DECODE_P;
+constexpr int kSplit = RKV_DECODE_SPLIT;
 
 struct Launch {
   int nw = 0;
-  int khw = 0;  // streaming kernel: KV heads (waves) per workgroup
   void (*kernel)(float*, float*, float*, const float*, const void*, const void*, const int32_t*,
                  int, const int32_t*, int, int, int64_t, float, int) = nullptr;
 };
 
-#ifndef RKV_DECODE_SPLIT
-#define RKV_DECODE_SPLIT 4
-#endif
-// Waves per partition of the streaming kernel (each streams a slice).
-constexpr int kSplit = RKV_DECODE_SPLIT;
-
-// Ring depth of the streaming kernel: RKV_DECODE_RING_LOADS 16-byte loads per
-// lane in flight, at most every tile of the wave's slice.
+// Ring depth: RKV_DECODE_RING_LOADS 16-byte loads per lane in flight, at most
+// every tile of the wave's slice.
 template <typename T, int D>
 constexpr int ring_for() {
   constexpr int nl = kBS / (64 / (D / Traits<T>::E));
@@ -814,63 +554,31 @@ constexpr int ring_for() {
   return r < 1 ? 1 : (r > nt ? nt : r);
 }
 
-template <typename T, int D, int G, int NW, int KHW>
+template <typename T, int D, int G>
 Launch make_launch() {
   Launch l;
-  if constexpr (kStream) {
-    constexpr int S = KHW == 1 ? kSplit : 1;
-    l.nw = KHW * S;
-    l.khw = KHW;
-    l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), KHW, S>;
-  } else {
-    constexpr int TPW = kP / (NW * kBS);
-    static_assert(TPW >= 1 && TPW * NW * kBS == kP, "partition must split evenly over waves");
-    l.nw = NW;
-    l.kernel = &decode_partition_kernel<T, D, G, kBS, NW, TPW>;
-  }
+  l.nw = kSplit;
+  l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), kSplit>;
   return l;
 }
 
 template <typename T, int D>
-constexpr int waves_for() {
-  constexpr int nw = RKV_DECODE_NW;
-  return (sizeof(T) == 4 && D == 128 && kP / (nw * kBS) > 2) ? nw * 2 : nw;
-}
-
-#ifndef RKV_DECODE_KHW
-#define RKV_DECODE_KHW 1
-#endif
-
-template <typename T, int D, int G>
-Launch pick_khw(int hkv) {
-  constexpr int NW = waves_for<T, D>();
-  // largest KV-head group <= RKV_DECODE_KHW that divides num_kv_heads
-  if constexpr (RKV_DECODE_KHW >= 8)
-    if (hkv % 8 == 0) return make_launch<T, D, G, NW, 8>();
-  if constexpr (RKV_DECODE_KHW >= 4)
-    if (hkv % 4 == 0) return make_launch<T, D, G, NW, 4>();
-  if constexpr (RKV_DECODE_KHW >= 2)
-    if (hkv % 2 == 0) return make_launch<T, D, G, NW, 2>();
-  return make_launch<T, D, G, NW, 1>();
-}
-
-template <typename T, int D>
-Launch pick_g(int G, int hkv) {
+Launch pick_g(int G) {
   switch (G) {
-    case 1: return pick_khw<T, D, 1>(hkv);
-    case 2: return pick_khw<T, D, 2>(hkv);
-    case 4: return pick_khw<T, D, 4>(hkv);
-    case 8: return pick_khw<T, D, 8>(hkv);
+    case 1: return make_launch<T, D, 1>();
+    case 2: return make_launch<T, D, 2>();
+    case 4: return make_launch<T, D, 4>();
+    case 8: return make_launch<T, D, 8>();
     default: return Launch{};
   }
 }
 
 template <typename T>
-Launch pick_d(int D, int G, int hkv) {
+Launch pick_d(int D, int G) {
   switch (D) {
-    case 32: return pick_g<T, 32>(G, hkv);
-    case 64: return pick_g<T, 64>(G, hkv);
-    case 128: return pick_g<T, 128>(G, hkv);
+    case 32: return pick_g<T, 32>(G);
+    case 64: return pick_g<T, 64>(G);
+    case 128: return pick_g<T, 128>(G);
     default: return Launch{};
   }
 }
@@ -952,19 +660,17 @@ void split_ws(void* ws, int B, int Hq, int D, int max_parts, float*& acc, float*
 int launch_partitions(const DecodeArgs& a, int max_parts) {
   const int G = a.num_q_heads / a.num_kv_heads;
 
-  Launch l = a.dtype == RKV_BF16 ? pick_d<uint16_t>(a.head_dim, G, a.num_kv_heads)
-                                  : pick_d<float>(a.head_dim, G, a.num_kv_heads);
+  Launch l = a.dtype == RKV_BF16 ? pick_d<uint16_t>(a.head_dim, G) : pick_d<float>(a.head_dim, G);
   if (!l.kernel) return fail(RKV_ERR_UNSUPPORTED, "no decode kernel for this shape");
   float *acc = nullptr, *ml = nullptr;
   if (max_parts > 1) split_ws(a.workspace, a.num_seqs, a.num_q_heads, a.head_dim, max_parts, acc, ml);
   const int cap = ctx_cap_of(a.max_context, a.max_blocks_per_seq, a.block_size);
-  dim3 grid = l.khw ? dim3((unsigned)(a.num_kv_heads / l.khw), (unsigned)max_parts,
-                           (unsigned)a.num_seqs)
-                    : dim3((unsigned)max_parts, (unsigned)a.num_kv_heads, (unsigned)a.num_seqs);
+  // KV-head major: the Hkv workgroups of one (partition, sequence) are adjacent
+  const dim3 grid((unsigned)a.num_kv_heads, (unsigned)max_parts, (unsigned)a.num_seqs);
   hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), 0, a.stream, a.out, acc, ml, a.q, a.k_pool,
                      a.v_pool, a.block_tables, a.max_blocks_per_seq, a.ctx_lens, cap,
                      a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts);
-  return check_launch("decode_partition_kernel");
+  return check_launch("decode_stream_kernel");
 }
 
 int launch_merge(float* out, const int32_t* ctx_lens, int num_seqs, int num_q_heads, int head_dim,
