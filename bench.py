@@ -49,7 +49,8 @@ def parse():
     p.add_argument("--copy-only", action="store_true",
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
-                   choices=["config0", "config1", "config2", "config3", "config4", "prefill"],
+                   choices=["config0", "config1", "config2", "config3", "config4", "prefill",
+                            "decode_q"],
                    help="config2 (default): the headline decode line; the others print "
                         "their own line (BASELINE.json configs[0], [1], [3], [4])")
     return p.parse_args()
@@ -487,6 +488,81 @@ def run_prefill(torch, dev, args):
                                          "tflops": round(f_chk / (us_chk * 1e-6) / 1e12, 2)})
 
 
+def run_decode_q(torch, dev, args):
+    """configs[2]'s decode (B64, Hq32, Hkv8, D128, contexts U[512, 4096], seed
+    2, 32 layer pools) over 1-byte pools: int8 and OCP fp8 e4m3 with one fp32
+    scale per (token, KV head) row, filled by the quantizing append from
+    N(0, 1) rows.  A step (32 calls) is replayed from a HIP graph as in the
+    headline line.  Bytes per call: the bytes and scales of K and V once, q
+    in, out, block ids, lengths."""
+    import numpy as np
+    from rustral_amd import kv
+    rng = np.random.default_rng(SEED)
+    ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B).astype(np.int32)
+    need = (ctx.astype(np.int64) + BS - 1) // BS
+    nb = int(need.sum())
+    mbs = CTX_HI // BS
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    ctx_d = torch.from_numpy(ctx).to(dev)
+    slots = torch.arange(nb * BS, dtype=torch.int64, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    res = {}
+    for fmt in ("int8", "fp8"):
+        layers = []
+        for _ in range(32):
+            kp = torch.empty((nb, HKV, BS, D), dtype=torch.uint8, device=dev)
+            vp = torch.empty_like(kp)
+            ks = torch.empty((nb, HKV, BS), dtype=torch.float32, device=dev)
+            vs = torch.empty_like(ks)
+            kn = torch.randn((nb * BS, HKV, D), generator=g, device=dev)
+            vn = torch.randn((nb * BS, HKV, D), generator=g, device=dev)
+            kv.append_q(kp, vp, ks, vs, kn, vn, slots, fmt)
+            del kn, vn
+            q = torch.randn((B, HQ, D), generator=g, device=dev)
+            perm = torch.randperm(nb, generator=g, device=dev).to(torch.int32)
+            t = torch.full((B, mbs), -1, dtype=torch.int32, device=dev)
+            o = 0
+            for b in range(B):
+                t[b, :int(need[b])] = perm[o:o + int(need[b])]
+                o += int(need[b])
+            layers.append((q, kp, vp, ks, vs, t, torch.empty_like(q)))
+        ws = torch.empty(kv.workspace_bytes(B, HQ, D, CTX_HI), dtype=torch.uint8, device=dev)
+
+        def step():
+            for (q, kp, vp, ks, vs, t, o) in layers:
+                kv.decode_attention_q(q, kp, vp, ks, vs, t, ctx_d, scale, fmt,
+                                      max_context=CTX_HI, out=o, workspace=ws)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(max(args.warmup, 1)):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        ms = _timed(torch, graph.replay, args.steps)
+        del graph
+        nbytes = (int(ctx.astype(np.int64).sum()) * HKV * (D + 4) * 2 + B * HQ * D * 4 * 2
+                  + int(need.sum()) * 4 + B * 4)
+        us = 1e3 * ms / 32
+        res[fmt] = {"us_per_call": round(us, 2), "bytes_per_call": nbytes,
+                    "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "decode_tokens_per_s_b64": round(B / (ms * 1e-3), 1)}
+        del layers, ws
+        torch.cuda.empty_cache()
+    r = res["int8"]
+    return _line("paged-KV decode over int8 pools GB/s (configs[2] shape); tokens/s at batch 64",
+                 r["GBps"], "GB/s", 32 * r["us_per_call"] / 1e3, args, "int8",
+                 {"workload": "configs[2] decode shape over 1-byte KV pools (int8, fp8 e4m3) "
+                              "with per-row fp32 scales", "batch": B, "num_q_heads": HQ,
+                  "num_kv_heads": HKV, "head_dim": D, "block_size": BS,
+                  "context": [CTX_LO, CTX_HI], "layers_per_step": 32},
+                 results=res)
+
+
 def run_config4(torch, dev, args):
     """continuous-batching step mix.  256 running sequences with
     contexts U[1, 8192] (seed 4) in 32 layer pools of 80,000 blocks (bf16,
@@ -624,7 +700,7 @@ def main():
     dev = torch.device("cuda:0")
     if args.workload != "config2":
         line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
-                "prefill": run_prefill,
+                "prefill": run_prefill, "decode_q": run_decode_q,
                 "config4": run_config4}[args.workload](torch, dev, args)
         print(json.dumps(line), flush=True)
         return

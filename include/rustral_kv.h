@@ -39,6 +39,8 @@ extern "C" {
 
 #define RKV_F32 0
 #define RKV_BF16 1
+#define RKV_I8 2  /* int8 bytes + one fp32 scale per (token, KV head) row   */
+#define RKV_FP8 3 /* OCP fp8 e4m3 bytes + one fp32 scale per row            */
 
 #define RKV_OK 0
 #define RKV_ERR_INVALID_ARG (-1) /* maps to CoreError::InvalidArgument / Shape */
@@ -149,6 +151,54 @@ int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens, int max_bloc
                                int num_seqs, int num_q_heads, int head_dim, int block_size,
                                int max_context, int dtype, int partition_size,
                                const void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- 1-byte pools (CacheQuantization::Int8 / Fp8) ---------------------------
+ * The reference lists these modes (crates/nn/src/kv_cache.rs:38-63) but its
+ * quantize_kv (:266-296) scales twice (x / s * 127, then clamped) and its
+ * dequantize_kv (:299-314) is never called, so the format is this library's:
+ * each row -- the head_dim values of one token of one KV head -- is stored as
+ * head_dim bytes in a pool laid out like the others ([num_blocks][Hkv]
+ * [block_size][head_dim] uint8) plus one fp32 scale in a scale pool
+ * [num_blocks][Hkv][block_size]:
+ *   RKV_I8:  s = max|x| / 127, byte = rint(x * (127 / max|x|)) clamped to
+ *            [-127, 127] (int8; max|x| = 0 or NaN input: 0); value = byte * s.
+ *   RKV_FP8: s = max|x| / 448, byte = OCP e4m3 of x * (448 / max|x|), round to
+ *            nearest even, magnitudes >= 448 saturating to 448; value =
+ *            e4m3(byte) * s.
+ * Compaction of 1-byte pools calls rkv_copy_blocks twice: on the byte pools
+ * (block_bytes = Hkv*block_size*head_dim) and on the scale pools (block_bytes
+ * = Hkv*block_size*4). */
+
+/* rkv_append for 1-byte pools: quantizes each appended (token, head) row and
+ * writes its bytes and scale.  Same arguments as rkv_append plus the scale
+ * pools; pool_layer_stride is in bytes (= elements) of the byte pools, the
+ * scale pools' layer stride is pool_layer_stride / head_dim.  head_dim 32, 64
+ * or 128. */
+int rkv_append_q(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                 int64_t pool_layer_stride, const float* k_new, const float* v_new,
+                 int64_t src_layer_stride, int64_t src_tok_stride, int64_t src_head_stride,
+                 const int64_t* slot_mapping, int64_t n_tokens, int n_layers, int num_kv_heads,
+                 int head_dim, int block_size, int64_t num_blocks, int dtype, void* stream);
+
+/* rkv_gather for 1-byte pools: dequantized fp32 output (byte value * row
+ * scale) in the same padded or packed layouts. */
+int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, const void* v_pool,
+                 const float* k_scale, const float* v_scale, const int32_t* block_tables,
+                 int max_blocks_per_seq, const int32_t* ctx_lens, const int64_t* out_offsets,
+                 int num_seqs, int num_kv_heads, int head_dim, int block_size,
+                 int64_t num_blocks, int max_ctx, int dtype, void* stream);
+
+/* rkv_decode_attention over 1-byte pools: the same result as decode on the
+ * dequantized values (scores = (q . bytes) * scale * row scale; the V row
+ * scale multiplies the softmax weight).  head_dim 64 or 128; workspace as
+ * rkv_decode_workspace_bytes. */
+int rkv_decode_attention_q(float* out, const float* q, const void* k_pool, const void* v_pool,
+                           const float* k_scale, const float* v_scale,
+                           const int32_t* block_tables, int max_blocks_per_seq,
+                           const int32_t* ctx_lens, int num_seqs, int num_q_heads,
+                           int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                           int max_context, float scale, int dtype, int partition_size,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* Causal prefill attention over the paged pool (many new query tokens per
  * sequence).  Sequence b owns query rows q_start[b] .. q_start[b+1]-1 of q

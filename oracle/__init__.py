@@ -63,6 +63,15 @@ def _declare(L):
     L.orc_decode_partials.argtypes = [_p, _p] + dec + [C.c_int, C.c_int]
     L.orc_splitk_merge.argtypes = [_p, _p, _p, _p, _p, C.c_int, C.c_int, C.c_int, C.c_int,
                                    C.c_int, C.c_int, C.c_int]
+    L.orc_e4m3_from_f32.restype = C.c_uint8
+    L.orc_e4m3_from_f32.argtypes = [_f32]
+    L.orc_f32_from_e4m3.restype = _f32
+    L.orc_f32_from_e4m3.argtypes = [C.c_uint8]
+    L.orc_quantize_row.argtypes = [_p, C.c_int, C.c_int, _p, _p]
+    L.orc_append_q.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, C.c_int, C.c_int, C.c_int, _i64,
+                               _i64, _i64, C.c_int]
+    L.orc_append_q.restype = C.c_int
+    L.orc_dequantize_pool.argtypes = [_p, _p, _i64, C.c_int, C.c_int, _p]
     L.orc_prefill_attention.argtypes = [_p, _p, _p, _p, _p, C.c_int, _p, _p, C.c_int, C.c_int,
                                         C.c_int, C.c_int, C.c_int, _i64, _f32, C.c_int]
     L.orc_decoder_param_count.restype = _i64
@@ -229,6 +238,52 @@ def decode_splitk(q, k_pool, v_pool, block_tables, ctx_lens, scale, partition_si
     _check(lib().orc_splitk_merge(_ptr(out), _ptr(m), _ptr(l), _ptr(acc), _ptr(keep[2]), mbs, bs,
                                   B, hq, d, partition_size, max_parts), "orc_splitk_merge")
     return out, (m, l, acc)
+
+
+I8, FP8 = 2, 3
+
+
+def e4m3_from_f32(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    return np.array([lib().orc_e4m3_from_f32(float(v)) for v in x], np.uint8)
+
+
+def f32_from_e4m3(b) -> np.ndarray:
+    b = np.ascontiguousarray(b, np.uint8).ravel()
+    return np.array([lib().orc_f32_from_e4m3(int(v)) for v in b], np.float32)
+
+
+def quantize_rows(x, dtype):
+    """Quantizes each row of x [rows, n] -> (bytes [rows, n] uint8, scales [rows] fp32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    q = np.zeros((rows, n), np.uint8)
+    s = np.zeros(rows, np.float32)
+    for r in range(rows):
+        lib().orc_quantize_row(_ptr(x[r]), n, dtype, q[r].ctypes.data_as(C.c_void_p),
+                               s[r:].ctypes.data_as(C.c_void_p))
+    return q, s
+
+
+def append_q(k_pool, v_pool, k_scale, v_scale, k_new, v_new, slot_mapping, dtype):
+    """Quantizing append into uint8 pools [nb, Hkv, BS, D] and scales [nb, Hkv, BS]."""
+    nb, hkv, bs, d = k_pool.shape
+    k_new = np.ascontiguousarray(k_new, np.float32)
+    v_new = np.ascontiguousarray(v_new, np.float32)
+    sm = np.ascontiguousarray(slot_mapping, np.int64)
+    _check(lib().orc_append_q(_ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale),
+                              _ptr(k_new), _ptr(v_new), _ptr(sm), len(sm), hkv, d, bs, nb,
+                              hkv * d, d, dtype), "orc_append_q")
+
+
+def dequantize_pool(pool, scales, dtype):
+    """fp32 values of a 1-byte pool: byte value * its row's scale."""
+    pool = np.ascontiguousarray(pool, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    d = pool.shape[-1]
+    out = np.zeros(pool.shape, np.float32)
+    lib().orc_dequantize_pool(_ptr(pool), _ptr(scales), pool.size // d, d, dtype, _ptr(out))
+    return out
 
 
 def prefill_attention(q, k_pool, v_pool, block_tables, q_start, ctx_lens, scale):

@@ -78,6 +78,89 @@ int orc_append(void* k_pool, void* v_pool, const float* k_new, const float* v_ne
   return 0;
 }
 
+/* ---- 1-byte storage ------------------------------------------------------ */
+
+uint8_t orc_e4m3_from_f32(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  const uint32_t sign = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7fu); /* NaN */
+  if (a >= 0x43e00000u) return (uint8_t)(sign | 0x7eu); /* >= 448 saturates */
+  if (a < 0x3c800000u) { /* below 2^-6: subnormal m * 2^-9 */
+    float f;
+    memcpy(&f, &a, 4);
+    return (uint8_t)(sign | (uint32_t)(int)rintf(f * 512.0f));
+  }
+  uint32_t e = (a >> 23) - 120u, m = (a >> 20) & 7u;
+  const uint32_t rem = a & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) ++m; /* nearest, ties to even */
+  if (m == 8u) {
+    m = 0;
+    ++e;
+  }
+  return (uint8_t)(sign | (e << 3) | m);
+}
+
+float orc_f32_from_e4m3(uint8_t b) {
+  const int e = (b >> 3) & 15, m = b & 7;
+  float v;
+  if (e == 15 && m == 7)
+    v = NAN;
+  else if (e == 0)
+    v = (float)m * 0.001953125f; /* m * 2^-9 */
+  else
+    v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return (b & 0x80) ? -v : v;
+}
+
+static uint8_t i8_quant(float x, float inv) {
+  const float r = rintf(x * inv);
+  if (r != r) return 0;
+  const float c = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+  return (uint8_t)(int8_t)(int)c;
+}
+
+void orc_quantize_row(const float* x, int n, int dtype, uint8_t* q, float* scale) {
+  float amax = 0.0f;
+  for (int i = 0; i < n; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  const float top = dtype == ORC_I8 ? 127.0f : 448.0f;
+  const float inv = amax > 0.0f ? top / amax : 0.0f;
+  *scale = amax / top;
+  for (int i = 0; i < n; ++i)
+    q[i] = dtype == ORC_I8 ? i8_quant(x[i], inv) : orc_e4m3_from_f32(x[i] * inv);
+}
+
+int orc_append_q(uint8_t* k_pool, uint8_t* v_pool, float* k_scale, float* v_scale,
+                 const float* k_new, const float* v_new, const int64_t* slot_mapping,
+                 int64_t n_tokens, int num_kv_heads, int head_dim, int block_size,
+                 int64_t num_blocks, int64_t src_tok_stride, int64_t src_head_stride, int dtype) {
+  if (!k_pool || !v_pool || !k_scale || !v_scale || !k_new || !v_new || !slot_mapping) return -1;
+  if (dtype != ORC_I8 && dtype != ORC_FP8) return -1;
+  const int64_t n_slots = num_blocks * block_size;
+  for (int64_t t = 0; t < n_tokens; ++t) {
+    const int64_t slot = slot_mapping[t];
+    if (slot < 0 || slot >= n_slots) continue;
+    const int64_t blk = slot / block_size, row = slot % block_size;
+    for (int h = 0; h < num_kv_heads; ++h) {
+      const int64_t r = (blk * num_kv_heads + h) * block_size + row;
+      const int64_t src = t * src_tok_stride + (int64_t)h * src_head_stride;
+      orc_quantize_row(k_new + src, head_dim, dtype, k_pool + r * head_dim, k_scale + r);
+      orc_quantize_row(v_new + src, head_dim, dtype, v_pool + r * head_dim, v_scale + r);
+    }
+  }
+  return 0;
+}
+
+void orc_dequantize_pool(const uint8_t* pool, const float* scales, int64_t n_rows, int head_dim,
+                         int dtype, float* out) {
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int d = 0; d < head_dim; ++d) {
+      const uint8_t b = pool[r * head_dim + d];
+      const float v = dtype == ORC_I8 ? (float)(int8_t)b : orc_f32_from_e4m3(b);
+      out[r * head_dim + d] = v * scales[r];
+    }
+}
+
 /* ---- gather ------------------------------------------------------------ */
 
 static inline int clamp_ctx(int L, int max_blocks_per_seq, int block_size) {

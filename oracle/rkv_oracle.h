@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-enum { ORC_F32 = 0, ORC_BF16 = 1 };
+enum { ORC_F32 = 0, ORC_BF16 = 1, ORC_I8 = 2, ORC_FP8 = 3 };
 
 /* fp32 -> bf16 round-to-nearest-even, NaN kept as a quiet NaN of the same
  * sign.  Deviation from the reference's only converter, which truncates
@@ -122,6 +122,33 @@ int orc_splitk_merge(float* out, const float* m, const float* l, const float* ac
                      const int32_t* ctx_lens, int max_blocks_per_seq, int block_size,
                      int num_seqs, int num_q_heads, int head_dim, int partition_size,
                      int max_parts);
+
+/* ---- 1-byte KV storage (CacheQuantization::Int8 / Fp8) ------------------
+ * The reference declares the modes (crates/nn/src/kv_cache.rs:38-63) but its
+ * quantize_kv (:266-296) divides by the scale and multiplies by 127 again
+ * (off by a factor 127, then clamped) and its dequantize_kv (:299-314) is
+ * never called, so this is the build's own specification, per row (the
+ * head_dim values of one token of one KV head) with an fp32 scale:
+ *   int8: amax = max |x|, s = amax / 127, q = rint(x * (127 / amax)) clamped
+ *         to [-127, 127] (amax = 0 or NaN input: 0); value = q * s.
+ *   fp8 (OCP e4m3, the Fp8 mode): s = amax / 448, q = e4m3(x * (448 / amax))
+ *         rounded to nearest even, |.| >= 448 saturating to 448, NaN kept;
+ *         value = f32(q) * s.
+ * Rows are stored in pools of bytes with the same layout as the fp32/bf16
+ * pools and scales in [num_blocks][num_kv_heads][block_size] fp32. */
+uint8_t orc_e4m3_from_f32(float x);
+float orc_f32_from_e4m3(uint8_t b);
+/* Quantizes one row of n values: bytes into q, the scale into *scale. */
+void orc_quantize_row(const float* x, int n, int dtype, uint8_t* q, float* scale);
+/* orc_append for 1-byte pools: quantizes each (token, head) row into the
+ * pool and its scale into the scale pool. */
+int orc_append_q(uint8_t* k_pool, uint8_t* v_pool, float* k_scale, float* v_scale,
+                 const float* k_new, const float* v_new, const int64_t* slot_mapping,
+                 int64_t n_tokens, int num_kv_heads, int head_dim, int block_size,
+                 int64_t num_blocks, int64_t src_tok_stride, int64_t src_head_stride, int dtype);
+/* value = dequantized byte * its row's scale, for n_rows rows of head_dim. */
+void orc_dequantize_pool(const uint8_t* pool, const float* scales, int64_t n_rows, int head_dim,
+                         int dtype, float* out);
 
 /* Causal prefill attention over the paged pool.  Sequence b has n_b =
  * q_start[b+1] - q_start[b] new query tokens (rows q_start[b] .. of q/out,

@@ -10,7 +10,7 @@ import os
 
 from .build import LIB_PATH
 
-RKV_F32, RKV_BF16 = 0, 1
+RKV_F32, RKV_BF16, RKV_I8, RKV_FP8 = 0, 1, 2, 3
 RKV_OK = 0
 RKV_ERR_INVALID_ARG, RKV_ERR_UNSUPPORTED, RKV_ERR_WORKSPACE, RKV_ERR_HIP = -1, -2, -3, -4
 RKV_ERR_OOM = -5
@@ -33,6 +33,12 @@ SIGNATURES = {
     "rkv_decode_attention_merge": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "rkv_prefill_attention": (_i, [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i64, _i,
                                    _f, _i, _p]),
+    "rkv_append_q": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i, _i, _i,
+                          _i, _i64, _i, _p]),
+    "rkv_gather_q": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i64, _i, _i,
+                          _p]),
+    "rkv_decode_attention_q": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,
+                                    _i, _f, _i, _i, _p, _sz, _p]),
     # include/rustral_serving.h (host memory)
     "rkv_bm_create": (_p, [_i64, _i]),
     "rkv_bm_destroy": (None, [_p]),

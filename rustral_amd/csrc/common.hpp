@@ -52,6 +52,62 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// ---- 1-byte KV storage: int8 and OCP fp8 e4m3 with a per-row scale ---------
+// A row (the D elements of one token of one KV head) is stored as D bytes
+// plus one fp32 scale s:
+//   int8: amax = max |x|; s = amax / 127; q = rint(x * (127 / amax)) clamped
+//         to [-127, 127] (amax = 0 or x NaN: q = 0); value = q * s.
+//   fp8:  s = amax / 448; q = e4m3(x * (448 / amax)), round to nearest even,
+//         magnitudes >= 448 saturate to 448, NaN stays NaN; value = f(q) * s.
+// The oracle uses the same bit routines (oracle/rkv_oracle.c), so the stored
+// bytes and scales match exactly.
+
+__host__ __device__ __forceinline__ uint8_t i8_quant(float x, float inv) {
+  const float r = rintf(x * inv);
+  if (!(r == r)) return 0;  // NaN
+  const float c = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+  return (uint8_t)(int8_t)(int)c;
+}
+
+__host__ __device__ __forceinline__ uint8_t e4m3_from_f32(float x) {
+  uint32_t u;
+  __builtin_memcpy(&u, &x, 4);
+  const uint32_t sign = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7fu);     // NaN
+  if (a >= 0x43e00000u) return (uint8_t)(sign | 0x7eu);    // >= 448: saturate
+  if (a < 0x3c800000u) {                                   // below 2^-6: subnormal
+    float f;
+    __builtin_memcpy(&f, &a, 4);
+    return (uint8_t)(sign | (uint32_t)(int)rintf(f * 512.0f));  // m * 2^-9, m <= 8
+  }
+  uint32_t e = (a >> 23) - 120u;  // biased e4m3 exponent, 1..15
+  uint32_t m = (a >> 20) & 7u;
+  const uint32_t rem = a & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) ++m;  // round to nearest even
+  if (m == 8u) {
+    m = 0;
+    ++e;
+  }
+  return (uint8_t)(sign | (e << 3) | m);
+}
+
+// Exact: the 7 exponent + mantissa bits placed at f32 bit 20 form a float
+// 2^(e-127) (1 + m/8) -- or the subnormal m 2^-129 when e = 0 -- and the
+// power-of-two factor 2^120 moves the bias from 127 to e4m3's 7.  (Relies on
+// fp32 denormals being kept, the default float mode of these kernels.)
+__host__ __device__ __forceinline__ float f32_from_e4m3(uint8_t b) {
+  const uint32_t mag = b & 0x7fu;
+  uint32_t u = mag << 20;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  f *= 1.329227995784916e36f;  // 2^120
+  __builtin_memcpy(&u, &f, 4);
+  if (mag == 0x7fu) u = 0x7fc00000u;  // NaN
+  u |= (uint32_t)(b & 0x80u) << 24;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
 // ---- cross-lane sums (wave64) --------------------------------------------
 
 template <int CTRL>
@@ -73,6 +129,17 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (N >= 16) x += dpp<0x140>(x);
   if constexpr (N >= 32) x += __shfl_xor(x, 16);
   if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+
+// Maximum over aligned groups of N consecutive lanes (N in {4, 8, 16}); every
+// lane of the group receives it.
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  if constexpr (N >= 2) x = fmaxf(x, dpp<0xB1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp<0x4E>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp<0x141>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp<0x140>(x));
   return x;
 }
 

@@ -198,6 +198,128 @@ __global__ __launch_bounds__(256) void copy_blocks_kernel(
   }
 }
 
+// ---- 1-byte storage (int8 / fp8 e4m3, one fp32 scale per row) ---------------
+// append_q: grid = (n_tokens, n_layers).  Thread u quantizes 8 elements of one
+// K row and one V row (row = a KV head of the token); the D/8 threads of a row
+// are consecutive lanes of one wave (D/8 in {4, 8, 16}), so the row maximum is
+// a DPP group maximum.  Every thread of the workgroup runs the same number of
+// rounds, so all lanes of a group take part in each reduction.
+template <int D, int FMT>
+__global__ __launch_bounds__(256) void append_q_kernel(
+    uint8_t* __restrict__ k_pool, uint8_t* __restrict__ v_pool, float* __restrict__ k_scale,
+    float* __restrict__ v_scale, int64_t pool_layer_stride, int64_t scale_layer_stride,
+    const float* __restrict__ k_new, const float* __restrict__ v_new, int64_t src_layer_stride,
+    int64_t src_tok_stride, int64_t src_head_stride, const int64_t* __restrict__ slot_mapping,
+    int num_kv_heads, int block_size, int bs_log2, int64_t num_slots) {
+  constexpr int CH = D / 8;  // threads per row
+  constexpr float kTop = FMT == RKV_I8 ? 127.0f : 448.0f;
+  const int t = blockIdx.x, layer = blockIdx.y;
+  const int units = num_kv_heads * CH;
+  const int64_t slot = slot_mapping[t];
+  const bool valid = slot >= 0 && slot < num_slots;
+  const int64_t blk = valid ? (bs_log2 >= 0 ? slot >> bs_log2 : slot / block_size) : 0;
+  const int64_t row = slot - blk * block_size;
+  for (int u0 = 0; u0 < units; u0 += blockDim.x) {
+    const int u = u0 + threadIdx.x;
+    const bool act = u < units;
+    const int h = u / CH, c = u - h * CH;
+    const int64_t src = layer * src_layer_stride + t * src_tok_stride + h * src_head_stride + c * 8;
+    float kx[8], vx[8];
+    if (act) {
+      const F8 k = load_f8(k_new + src), v = load_f8(v_new + src);
+      kx[0] = k.a.x, kx[1] = k.a.y, kx[2] = k.a.z, kx[3] = k.a.w;
+      kx[4] = k.b.x, kx[5] = k.b.y, kx[6] = k.b.z, kx[7] = k.b.w;
+      vx[0] = v.a.x, vx[1] = v.a.y, vx[2] = v.a.z, vx[3] = v.a.w;
+      vx[4] = v.b.x, vx[5] = v.b.y, vx[6] = v.b.z, vx[7] = v.b.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kx[e] = vx[e] = 0.0f;
+    }
+    float ka = 0.0f, va = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ka = fmaxf(ka, fabsf(kx[e]));
+      va = fmaxf(va, fabsf(vx[e]));
+    }
+    ka = group_max<CH>(ka);
+    va = group_max<CH>(va);
+    if (!act || !valid) continue;
+    const float kinv = ka > 0.0f ? kTop / ka : 0.0f, vinv = va > 0.0f ? kTop / va : 0.0f;
+    uint32_t kw[2] = {0u, 0u}, vw[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t kb = FMT == RKV_I8 ? i8_quant(kx[e], kinv) : e4m3_from_f32(kx[e] * kinv);
+      const uint32_t vb = FMT == RKV_I8 ? i8_quant(vx[e], vinv) : e4m3_from_f32(vx[e] * vinv);
+      kw[e >> 2] |= kb << (8 * (e & 3));
+      vw[e >> 2] |= vb << (8 * (e & 3));
+    }
+    const int64_t r = (blk * num_kv_heads + h) * block_size + row;  // row index in the layer
+    const int64_t dst = layer * pool_layer_stride + r * D + c * 8;
+    *reinterpret_cast<uint2*>(k_pool + dst) = make_uint2(kw[0], kw[1]);
+    *reinterpret_cast<uint2*>(v_pool + dst) = make_uint2(vw[0], vw[1]);
+    if (c == 0) {
+      k_scale[layer * scale_layer_stride + r] = ka / kTop;
+      v_scale[layer * scale_layer_stride + r] = va / kTop;
+    }
+  }
+}
+
+// gather_q: grid = (max_blocks_per_seq, num_seqs, 2 [K,V]); like gather_kernel,
+// one workgroup per logical block; each thread turns 16 stored bytes of a row
+// into 16 fp32 values (byte value * row scale).
+template <int FMT>
+__global__ __launch_bounds__(256) void gather_q_kernel(
+    float* __restrict__ k_out, float* __restrict__ v_out, const uint8_t* __restrict__ k_pool,
+    const uint8_t* __restrict__ v_pool, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
+    int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
+    const int64_t* __restrict__ out_offsets, int num_kv_heads, int head_dim, int block_size,
+    int64_t num_blocks, int max_ctx) {
+  const int j = blockIdx.x, b = blockIdx.y;
+  const bool is_v = blockIdx.z != 0;
+  int L = ctx_lens[b];
+  const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + j];
+  int64_t seq_base = out_offsets ? out_offsets[b] : 0;
+  L = L < 0 ? 0 : L;
+  const int cap = max_blocks_per_seq * block_size;
+  L = L > cap ? cap : L;
+  int row_stride;
+  if (out_offsets) {
+    if (seq_base < 0 || (seq_base & 3)) return;  // 16-byte vector stores need 4-float alignment
+    row_stride = L;
+  } else {
+    L = L > max_ctx ? max_ctx : L;
+    seq_base = (int64_t)b * num_kv_heads * max_ctx * head_dim;
+    row_stride = max_ctx;
+  }
+  const int p0 = j * block_size;
+  if (p0 >= L) return;
+  if (blk < 0 || blk >= num_blocks) return;
+  const int nt = (L - p0) < block_size ? (L - p0) : block_size;
+  const uint8_t* src_pool = is_v ? v_pool : k_pool;
+  const float* scales = is_v ? v_scale : k_scale;
+  float* dst_all = is_v ? v_out : k_out;
+  const int per_row = head_dim >> 4;  // 16-byte units per row
+  const int units = num_kv_heads * nt * per_row;
+  for (int u = threadIdx.x; u < units; u += blockDim.x) {
+    const int hr = u / per_row, c = u - hr * per_row;  // hr = head * nt + token row
+    const int h = hr / nt, rr = hr - h * nt;
+    const int64_t r = ((int64_t)blk * num_kv_heads + h) * block_size + rr;
+    const uint4 w = *reinterpret_cast<const uint4*>(src_pool + r * head_dim + c * 16);
+    const float s = scales[r];
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    float f[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const uint8_t byte = (uint8_t)(ws[e >> 2] >> (8 * (e & 3)));
+      f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3(byte)) * s;
+    }
+    float* d = dst_all + seq_base + ((int64_t)h * row_stride + p0 + rr) * head_dim + c * 16;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) store16(d + e, make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]));
+  }
+}
+
 int check_common(int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, int dtype) {
   if (num_kv_heads <= 0 || head_dim <= 0 || block_size <= 0 || num_blocks < 0)
     return fail(RKV_ERR_INVALID_ARG, "num_kv_heads, head_dim, block_size must be > 0");
@@ -285,6 +407,98 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
     RKV_GATHER(uint16_t, uint16_t);
 #undef RKV_GATHER
   return check_launch("rkv_gather");
+}
+
+namespace {
+int check_q(int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, int dtype) {
+  if (num_kv_heads <= 0 || block_size <= 0 || num_blocks < 0)
+    return fail(RKV_ERR_INVALID_ARG, "num_kv_heads and block_size must be > 0");
+  if (dtype != RKV_I8 && dtype != RKV_FP8)
+    return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_I8 or RKV_FP8");
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return fail(RKV_ERR_UNSUPPORTED, "1-byte pools: head_dim must be 32, 64 or 128");
+  return RKV_OK;
+}
+}  // namespace
+
+extern "C" int rkv_append_q(void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                            int64_t pool_layer_stride, const float* k_new, const float* v_new,
+                            int64_t src_layer_stride, int64_t src_tok_stride,
+                            int64_t src_head_stride, const int64_t* slot_mapping,
+                            int64_t n_tokens, int n_layers, int num_kv_heads, int head_dim,
+                            int block_size, int64_t num_blocks, int dtype, void* stream) {
+  clear_error();
+  if (int rc = check_q(num_kv_heads, head_dim, block_size, num_blocks, dtype)) return rc;
+  if (n_tokens < 0 || n_layers < 0) return fail(RKV_ERR_INVALID_ARG, "negative n_tokens/n_layers");
+  if (n_tokens == 0 || n_layers == 0) return RKV_OK;
+  if (!k_pool || !v_pool || !k_scale || !v_scale || !k_new || !v_new || !slot_mapping)
+    return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (n_tokens > 0x7fffffff || n_layers > 65535)
+    return fail(RKV_ERR_INVALID_ARG, "n_tokens or n_layers too large for one launch");
+  if ((src_layer_stride | src_tok_stride | src_head_stride) & 3)
+    return fail(RKV_ERR_INVALID_ARG, "source strides must be multiples of 4 elements");
+  if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(k_pool) || !aligned16(v_pool))
+    return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
+  if (n_layers > 1 && (pool_layer_stride % 16))
+    return fail(RKV_ERR_INVALID_ARG, "pool_layer_stride must be a multiple of 16 bytes");
+  const int units = num_kv_heads * (head_dim / 8);
+  const int threads = units >= 256 ? 256 : ((units + 63) / 64) * 64;
+  const dim3 grid((unsigned)n_tokens, (unsigned)n_layers);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n_slots = num_blocks * block_size;
+  const int bs_log2 = (block_size & (block_size - 1)) ? -1 : __builtin_ctz((unsigned)block_size);
+  // scales: one per row; a layer of the scale pool holds num_blocks * Hkv * block_size
+  const int64_t scale_ls = n_layers > 1 ? pool_layer_stride / head_dim : 0;
+#define RKV_APPEND_Q(D, F)                                                                      \
+  append_q_kernel<D, F><<<grid, threads, 0, s>>>(                                               \
+      static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scale, v_scale,           \
+      pool_layer_stride, scale_ls, k_new, v_new, src_layer_stride, src_tok_stride,              \
+      src_head_stride, slot_mapping, num_kv_heads, block_size, bs_log2, n_slots)
+  if (dtype == RKV_I8) {
+    if (head_dim == 32) RKV_APPEND_Q(32, RKV_I8);
+    else if (head_dim == 64) RKV_APPEND_Q(64, RKV_I8);
+    else RKV_APPEND_Q(128, RKV_I8);
+  } else {
+    if (head_dim == 32) RKV_APPEND_Q(32, RKV_FP8);
+    else if (head_dim == 64) RKV_APPEND_Q(64, RKV_FP8);
+    else RKV_APPEND_Q(128, RKV_FP8);
+  }
+#undef RKV_APPEND_Q
+  return check_launch("rkv_append_q");
+}
+
+extern "C" int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, const void* v_pool,
+                            const float* k_scale, const float* v_scale,
+                            const int32_t* block_tables, int max_blocks_per_seq,
+                            const int32_t* ctx_lens, const int64_t* out_offsets, int num_seqs,
+                            int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                            int max_ctx, int dtype, void* stream) {
+  clear_error();
+  if (int rc = check_q(num_kv_heads, head_dim, block_size, num_blocks, dtype)) return rc;
+  if (num_seqs < 0 || max_blocks_per_seq < 0)
+    return fail(RKV_ERR_INVALID_ARG, "negative num_seqs/max_blocks_per_seq");
+  if (num_seqs == 0 || max_blocks_per_seq == 0) return RKV_OK;
+  if (num_seqs > 65535) return fail(RKV_ERR_INVALID_ARG, "num_seqs > 65535");
+  if (!k_out || !v_out || !k_pool || !v_pool || !k_scale || !v_scale || !block_tables ||
+      !ctx_lens)
+    return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (!out_offsets && max_ctx <= 0)
+    return fail(RKV_ERR_INVALID_ARG, "padded output needs max_ctx > 0");
+  if (!aligned16(k_out) || !aligned16(v_out) || !aligned16(k_pool) || !aligned16(v_pool))
+    return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
+  const dim3 grid((unsigned)max_blocks_per_seq, (unsigned)num_seqs, 2);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == RKV_I8)
+    gather_q_kernel<RKV_I8><<<grid, 256, 0, s>>>(
+        k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),
+        k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,
+        head_dim, block_size, num_blocks, max_ctx);
+  else
+    gather_q_kernel<RKV_FP8><<<grid, 256, 0, s>>>(
+        k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),
+        k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,
+        head_dim, block_size, num_blocks, max_ctx);
+  return check_launch("rkv_gather_q");
 }
 
 extern "C" int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes,

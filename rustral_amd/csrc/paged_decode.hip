@@ -52,6 +52,10 @@ template <>
 struct Traits<uint16_t> {
   static constexpr int E = 8;
 };
+template <>
+struct Traits<uint8_t> {  // int8 / fp8 pools
+  static constexpr int E = 16;
+};
 
 // Calls f(std::integral_constant<int, I>) for I = B .. E-1 in order.
 template <int B, int E, class F>
@@ -84,6 +88,48 @@ __device__ __forceinline__ void to_float(const uint4& w, float (&f)[4]) {
   f[3] = __uint_as_float(w.w);
 }
 
+// The 4 stored bytes of a dword of a 1-byte pool as floats (before the row
+// scale).  fp8: v_cvt_pk_f32_fp8, which decodes OCP e4m3 on gfx950 (checked
+// against the exact bit decode for all 256 codes); int8: sign-extend + convert.
+template <int FMT>
+__device__ __forceinline__ void dword_values(uint32_t w, float (&f)[4]) {
+  if constexpr (FMT == RKV_I8) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = (float)((int32_t)(w << (24 - 8 * e)) >> 24);
+  } else {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);  // bytes 0, 1
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);   // bytes 2, 3
+    f[0] = lo[0], f[1] = lo[1], f[2] = hi[0], f[3] = hi[1];
+  }
+}
+
+// 16 stored bytes as floats (before the row scale).
+template <int FMT>
+__device__ __forceinline__ void to_float_q(const uint4& w, float (&f)[16]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float t[4];
+    dword_values<FMT>(ws[k], t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[4 * k + e] = t[e];
+  }
+}
+
+// 8 stored bytes (two dwords) as 8 bf16 values packed in a uint4; exact, since
+// int8 integers and e4m3 values have at most 8 significant bits (the bf16 is
+// the high half of the float).
+template <int FMT>
+__device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
+  float a[4], b[4];
+  dword_values<FMT>(lo, a);
+  dword_values<FMT>(hi, b);
+  auto pack = [](float x, float y) {
+    return (__float_as_uint(x) >> 16) | (__float_as_uint(y) & 0xffff0000u);
+  };
+  return make_uint4(pack(a[0], a[1]), pack(a[2], a[3]), pack(b[0], b[1]), pack(b[2], b[3]));
+}
+
 // ---- streaming variant ---------------------------------------------------------
 // SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
 // item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
@@ -102,11 +148,12 @@ __device__ __forceinline__ void to_float(const uint4& w, float (&f)[4]) {
 //   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
 // (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
 // D[4(l/16)+r][l%16].)  PV stays on the VALU.
-template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT>
+template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT>
 __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
     float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
     const float* __restrict__ q, const void* __restrict__ k_pool_,
-    const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
+    const void* __restrict__ v_pool_, const float* __restrict__ k_scale,
+    const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens, int ctx_cap, int num_kv_heads,
     int64_t num_blocks, float q_scale, int max_parts) {
   const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
@@ -147,18 +194,26 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
     const int lbc = lb < max_blocks_per_seq ? lb : max_blocks_per_seq - 1;
     pb[i] = lbc >= 0 ? tab[lbc] : -1;
   }
-  constexpr bool MFMA = sizeof(T) == 2 && 2 * G <= 16;
-  constexpr int NC = D / 32;                     // MFMAs per tile (bf16: == NL)
+  // 1-byte pools (QNT): bytes plus one fp32 scale per (token, KV head) row.
+  constexpr bool QNT = FMT == RKV_I8 || FMT == RKV_FP8;
+  static_assert(QNT == (sizeof(T) == 1), "1-byte element type iff a 1-byte format");
+  constexpr bool MFMA = (sizeof(T) == 2 || QNT) && 2 * G <= 16;
+  constexpr int NC = D / 32;                     // MFMAs per tile
   const int kt = lane & 15, kq = lane >> 4;      // MFMA lanes: token row, k-quarter
   // VALU path: this lane's E dims of each head.  MFMA path: the A operand
-  // row kt (hi rows 0..G-1, lo rows G..2G-1) at dims 32c + 8 kq .. + 8.
+  // row kt (hi rows 0..G-1, lo rows G..2G-1), chunk c at dims 32c + 8 kq .. + 8
+  // for bf16; for 1-byte pools a lane loads the contiguous quarter
+  // [D/4 kq, D/4 (kq+1)) of its key row, so chunk c holds dims D/4 kq + 8c ..
+  // + 8 (any assignment of dims to k-slots gives the same dot product, as long
+  // as q and K use the same one).
   constexpr int QN = MFMA ? NC * 8 : G * E;
   float qv[QN];
   if constexpr (MFMA) {
     const int qrow = kt < G ? kt : (kt < 2 * G ? kt - G : 0);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const float4* qp = reinterpret_cast<const float4*>(q + (head0 + qrow) * D + 32 * c + 8 * kq);
+      const int d0 = QNT ? (D / 4) * kq + 8 * c : 32 * c + 8 * kq;
+      const float4* qp = reinterpret_cast<const float4*>(q + (head0 + qrow) * D + d0);
       const float4 x = qp[0], y = qp[1];
       qv[c * 8 + 0] = x.x; qv[c * 8 + 1] = x.y; qv[c * 8 + 2] = x.z; qv[c * 8 + 3] = x.w;
       qv[c * 8 + 4] = y.x; qv[c * 8 + 5] = y.y; qv[c * 8 + 6] = y.z; qv[c * 8 + 7] = y.w;
@@ -200,9 +255,10 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
     base[i] = ((int64_t)(ok[i] ? pb[i] : pb0) * num_kv_heads + kh) * BS * D;
   }
   // this lane's first element in a tile, and the stride between its loads
-  const T* __restrict__ kl = MFMA ? k_pool + kt * D + 8 * kq : k_pool + slot * D + dl * E;
+  const T* __restrict__ kl = MFMA ? k_pool + kt * D + (QNT ? (D / 4) * kq : 8 * kq)
+                                  : k_pool + slot * D + dl * E;
   const T* __restrict__ vl = v_pool + slot * D + dl * E;
-  constexpr int KSTEP = MFMA ? 32 : TPL * D;
+  constexpr int KSTEP = MFMA ? (QNT ? 16 : 32) : TPL * D;
   constexpr int VSTEP = TPL * D;
 
   uint4 ring[R][NL];
@@ -213,6 +269,24 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
 #pragma unroll
     for (int n = 0; n < NL; ++n)
       ring[t][n] = *reinterpret_cast<const uint4*>(pool + base[t % NTW] + n * step);
+  }
+
+  // 1-byte pools: the K scale of this lane's token in each K tile (MFMA column
+  // kt), and the V scale of the tokens this lane folds into the
+  // probabilities (x = lane + 64 j of the slice).  Issued with the ring loads.
+  constexpr int NX = QNT ? (NTW * BS + 63) / 64 : 1;
+  float ksc[QNT ? NTW : 1], vsc[NX];
+  if constexpr (QNT) {
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) ksc[i] = k_scale[base[i] / D + kt];
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      const int x = lane + 64 * j, ix = x / BS;
+      int64_t rb = base[0];  // base[ix] by selects (ix differs between lanes)
+#pragma unroll
+      for (int i = 1; i < NTW; ++i) rb = ix == i ? base[i] : rb;
+      vsc[j] = x < NTW * BS ? v_scale[rb / D + x % BS] : 0.0f;
+    }
   }
 
   // MFMA A operands: q split into bf16 hi + lo rows (after the ring loads
@@ -246,25 +320,41 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
       // ---- QK^T for the 16 tokens of tile i ----
       if constexpr (MFMA) {
         f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (QNT) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[c]),
-                                                        __builtin_bit_cast(bf16x8_t, tile[c]),
-                                                        sacc, 0, 0, 0);
+          for (int n = 0; n < NL; ++n) {
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, qa[2 * n]),
+                __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(tile[n].x, tile[n].y)), sacc, 0, 0,
+                0);
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, qa[2 * n + 1]),
+                __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(tile[n].z, tile[n].w)), sacc, 0, 0,
+                0);
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[c]),
+                                                          __builtin_bit_cast(bf16x8_t, tile[c]),
+                                                          sacc, 0, 0, 0);
+        }
+        // dot * scale (the reference's order), then the token's K row scale
+        const float qs = QNT ? q_scale * ksc[i] : q_scale;
         const int tp = i * BS + kt;  // token of this lane's column
         const bool valid = ok[i] && (tok0 + tp < L);
         if constexpr (G == 1) {
-          if (kq == 0) s_p[tp] = valid ? (sacc[0] + sacc[1]) * q_scale : -INFINITY;
+          if (kq == 0) s_p[tp] = valid ? (sacc[0] + sacc[1]) * qs : -INFINITY;
         } else if constexpr (G == 2) {
           if (kq == 0) {
-            s_p[tp * 2 + 0] = valid ? (sacc[0] + sacc[2]) * q_scale : -INFINITY;
-            s_p[tp * 2 + 1] = valid ? (sacc[1] + sacc[3]) * q_scale : -INFINITY;
+            s_p[tp * 2 + 0] = valid ? (sacc[0] + sacc[2]) * qs : -INFINITY;
+            s_p[tp * 2 + 1] = valid ? (sacc[1] + sacc[3]) * qs : -INFINITY;
           }
         } else {
           constexpr int XOR = G == 4 ? 16 : 32;  // lanes between hi and lo rows
           float sc[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[r] = (sacc[r] + __shfl_xor(sacc[r], XOR)) * q_scale;
+          for (int r = 0; r < 4; ++r) sc[r] = (sacc[r] + __shfl_xor(sacc[r], XOR)) * qs;
           if (lane < XOR) {  // lanes kq * 16 + kt hold heads 4 kq .. 4 kq + 3
             *reinterpret_cast<float4*>(&s_p[tp * G + 4 * kq]) =
                 valid ? make_float4(sc[0], sc[1], sc[2], sc[3])
@@ -309,14 +399,23 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
           l[g] = 0.0f;
         }
 #pragma unroll
-        for (int x = lane; x < NTW * BS; x += 64)
+        for (int j = 0; j < (NTW * BS + 63) / 64; ++j) {
+          const int x = lane + 64 * j;
+          if (x < NTW * BS) {
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float sv = s_p[x * G + g];
-            const float pv = (sv == -INFINITY) ? 0.0f : exp2f(sv - m[g]);
-            s_p[x * G + g] = pv;
-            l[g] += pv;
+            for (int g = 0; g < G; ++g) {
+              const float sv = s_p[x * G + g];
+              const float pv = (sv == -INFINITY) ? 0.0f : exp2f(sv - m[g]);
+              l[g] += pv;
+              // 1-byte pools: the V row scale goes into the weight (selected,
+              // so the unwritten scale of a masked token never enters)
+              if constexpr (QNT)
+                s_p[x * G + g] = pv > 0.0f ? pv * vsc[j] : 0.0f;
+              else
+                s_p[x * G + g] = pv;
+            }
           }
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           l[g] = wave_sum(l[g]);
@@ -342,7 +441,10 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
         vv.z = keep ? vv.z : 0u;
         vv.w = keep ? vv.w : 0u;
         float vf[E];
-        to_float(vv, vf);
+        if constexpr (QNT)
+          to_float_q<FMT>(vv, vf);
+        else
+          to_float(vv, vf);
         const int tp = i * BS + n * TPL + slot;
         float pr[G];
 #pragma unroll
@@ -525,7 +627,8 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge_kernel(
 
 constexpr int kBS = 16;
 // Tokens per partition, waves per partition (each streams a slice) and the
-// register ring depth in 16-byte loads per lane.
+// register ring depth in 16-byte loads per lane (16-bit / fp32 pools, 1-byte
+// pools).
 #ifndef RKV_DECODE_P
 #define RKV_DECODE_P 512
 #endif
@@ -535,13 +638,17 @@ constexpr int kBS = 16;
 #ifndef RKV_DECODE_RING_LOADS
 #define RKV_DECODE_RING_LOADS 16
 #endif
+#ifndef RKV_DECODE_RING_LOADS_Q  // 1-byte pools (more registers per tile)
+#define RKV_DECODE_RING_LOADS_Q 8
+#endif
 constexpr int kP = RKV_DECODE_P;
 constexpr int kSplit = RKV_DECODE_SPLIT;
 
 struct Launch {
   int nw = 0;
-  void (*kernel)(float*, float*, float*, const float*, const void*, const void*, const int32_t*,
-                 int, const int32_t*, int, int, int64_t, float, int) = nullptr;
+  void (*kernel)(float*, float*, float*, const float*, const void*, const void*, const float*,
+                 const float*, const int32_t*, int, const int32_t*, int, int, int64_t, float,
+                 int) = nullptr;
 };
 
 // Ring depth: RKV_DECODE_RING_LOADS 16-byte loads per lane in flight, at most
@@ -549,36 +656,49 @@ struct Launch {
 template <typename T, int D>
 constexpr int ring_for() {
   constexpr int nl = kBS / (64 / (D / Traits<T>::E));
-  constexpr int r = RKV_DECODE_RING_LOADS / nl;
+  constexpr int r = (sizeof(T) == 1 ? RKV_DECODE_RING_LOADS_Q : RKV_DECODE_RING_LOADS) / nl;
   constexpr int nt = 2 * (kP / kBS) / kSplit;
   return r < 1 ? 1 : (r > nt ? nt : r);
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int FMT>
 Launch make_launch() {
   Launch l;
   l.nw = kSplit;
-  l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), kSplit>;
+  l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), kSplit, FMT>;
   return l;
 }
 
-template <typename T, int D>
+template <typename T, int D, int FMT>
 Launch pick_g(int G) {
   switch (G) {
-    case 1: return make_launch<T, D, 1>();
-    case 2: return make_launch<T, D, 2>();
-    case 4: return make_launch<T, D, 4>();
-    case 8: return make_launch<T, D, 8>();
+    case 1: return make_launch<T, D, 1, FMT>();
+    case 2: return make_launch<T, D, 2, FMT>();
+    case 4: return make_launch<T, D, 4, FMT>();
+    case 8: return make_launch<T, D, 8, FMT>();
     default: return Launch{};
   }
 }
 
-template <typename T>
+// 16-bit and fp32 pools: head_dim 32, 64, 128; 1-byte pools: 64, 128.
+template <typename T, int FMT>
 Launch pick_d(int D, int G) {
   switch (D) {
-    case 32: return pick_g<T, 32>(G);
-    case 64: return pick_g<T, 64>(G);
-    case 128: return pick_g<T, 128>(G);
+    case 32:
+      if constexpr (sizeof(T) == 1) return Launch{};
+      else return pick_g<T, 32, FMT>(G);
+    case 64: return pick_g<T, 64, FMT>(G);
+    case 128: return pick_g<T, 128, FMT>(G);
+    default: return Launch{};
+  }
+}
+
+Launch pick(int dtype, int D, int G) {
+  switch (dtype) {
+    case RKV_F32: return pick_d<float, RKV_F32>(D, G);
+    case RKV_BF16: return pick_d<uint16_t, RKV_BF16>(D, G);
+    case RKV_I8: return pick_d<uint8_t, RKV_I8>(D, G);
+    case RKV_FP8: return pick_d<uint8_t, RKV_FP8>(D, G);
     default: return Launch{};
   }
 }
@@ -599,6 +719,8 @@ struct DecodeArgs {
   void* workspace;
   size_t workspace_bytes;
   hipStream_t stream;
+  const float* k_scale = nullptr;  // 1-byte pools: [num_blocks][Hkv][block_size] fp32
+  const float* v_scale = nullptr;
 };
 
 size_t ws_bytes(int B, int Hq, int D, int max_parts) {
@@ -619,8 +741,11 @@ int validate(const DecodeArgs& a, int& max_parts) {
     return fail(RKV_ERR_INVALID_ARG, "negative size argument");
   if (a.num_q_heads <= 0 || a.num_kv_heads <= 0 || a.num_q_heads % a.num_kv_heads)
     return fail(RKV_ERR_INVALID_ARG, "num_q_heads must be a positive multiple of num_kv_heads");
-  if (a.dtype != RKV_F32 && a.dtype != RKV_BF16)
-    return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_F32 or RKV_BF16");
+  const bool q8 = a.dtype == RKV_I8 || a.dtype == RKV_FP8;
+  if (a.dtype != RKV_F32 && a.dtype != RKV_BF16 && !q8)
+    return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_F32, RKV_BF16, RKV_I8 or RKV_FP8");
+  if (q8 && a.head_dim == 32)
+    return fail(RKV_ERR_UNSUPPORTED, "1-byte pools: head_dim must be 64 or 128");
   if (a.block_size != kBS) return fail(RKV_ERR_UNSUPPORTED, "block_size must be 16");
   if (a.head_dim != 32 && a.head_dim != 64 && a.head_dim != 128)
     return fail(RKV_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128");
@@ -640,6 +765,9 @@ int validate(const DecodeArgs& a, int& max_parts) {
   if (a.num_seqs == 0) return RKV_OK;
   if (!a.out || !a.q || !a.k_pool || !a.v_pool || !a.block_tables || !a.ctx_lens)
     return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (q8 && (!a.k_scale || !a.v_scale))
+    return fail(RKV_ERR_INVALID_ARG,
+                "1-byte pools need their scale pools (rkv_decode_attention_q)");
   if (!aligned16(a.out) || !aligned16(a.q) || !aligned16(a.k_pool) || !aligned16(a.v_pool))
     return fail(RKV_ERR_INVALID_ARG, "out, q and pools must be 16-byte aligned");
   const size_t need = ws_bytes(a.num_seqs, a.num_q_heads, a.head_dim, max_parts);
@@ -660,7 +788,7 @@ void split_ws(void* ws, int B, int Hq, int D, int max_parts, float*& acc, float*
 int launch_partitions(const DecodeArgs& a, int max_parts) {
   const int G = a.num_q_heads / a.num_kv_heads;
 
-  Launch l = a.dtype == RKV_BF16 ? pick_d<uint16_t>(a.head_dim, G) : pick_d<float>(a.head_dim, G);
+  Launch l = pick(a.dtype, a.head_dim, G);
   if (!l.kernel) return fail(RKV_ERR_UNSUPPORTED, "no decode kernel for this shape");
   float *acc = nullptr, *ml = nullptr;
   if (max_parts > 1) split_ws(a.workspace, a.num_seqs, a.num_q_heads, a.head_dim, max_parts, acc, ml);
@@ -668,7 +796,8 @@ int launch_partitions(const DecodeArgs& a, int max_parts) {
   // KV-head major: the Hkv workgroups of one (partition, sequence) are adjacent
   const dim3 grid((unsigned)a.num_kv_heads, (unsigned)max_parts, (unsigned)a.num_seqs);
   hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), 0, a.stream, a.out, acc, ml, a.q, a.k_pool,
-                     a.v_pool, a.block_tables, a.max_blocks_per_seq, a.ctx_lens, cap,
+                     a.v_pool, a.k_scale, a.v_scale, a.block_tables, a.max_blocks_per_seq,
+                     a.ctx_lens, cap,
                      a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts);
   return check_launch("decode_stream_kernel");
 }
@@ -779,4 +908,29 @@ extern "C" int rkv_decode_attention(float* out, const float* q, const void* k_po
   return rkv_decode_attention_merge(out, ctx_lens, max_blocks_per_seq, num_seqs, num_q_heads,
                                     head_dim, block_size, max_context, dtype, partition_size,
                                     workspace, workspace_bytes, stream);
+}
+
+extern "C" int rkv_decode_attention_q(float* out, const float* q, const void* k_pool,
+                                      const void* v_pool, const float* k_scale,
+                                      const float* v_scale, const int32_t* block_tables,
+                                      int max_blocks_per_seq, const int32_t* ctx_lens,
+                                      int num_seqs, int num_q_heads, int num_kv_heads,
+                                      int head_dim, int block_size, int64_t num_blocks,
+                                      int max_context, float scale, int dtype,
+                                      int partition_size, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (dtype != RKV_I8 && dtype != RKV_FP8)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_decode_attention_q: dtype must be RKV_I8 or RKV_FP8");
+  DecodeArgs a{out, q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens, num_seqs,
+               num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context, scale,
+               dtype, partition_size, workspace, workspace_bytes,
+               static_cast<hipStream_t>(stream), k_scale, v_scale};
+  int max_parts = 1;
+  if (int rc = validate(a, max_parts)) return rc;
+  if (num_seqs == 0) return RKV_OK;
+  if (int rc = launch_partitions(a, max_parts)) return rc;
+  const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
+  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, max_parts, workspace,
+                      a.stream);
 }

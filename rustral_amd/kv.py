@@ -168,6 +168,90 @@ def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     return out
 
 
+_QFMT = {"int8": _lib.RKV_I8, "fp8": _lib.RKV_FP8, _lib.RKV_I8: _lib.RKV_I8,
+         _lib.RKV_FP8: _lib.RKV_FP8}
+
+
+def _qcode(fmt) -> int:
+    if fmt not in _QFMT:
+        raise ValueError(f"1-byte format {fmt!r}: want 'int8' or 'fp8'")
+    return _QFMT[fmt]
+
+
+def append_q(k_pool: torch.Tensor, v_pool: torch.Tensor, k_scale: torch.Tensor,
+             v_scale: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+             slot_mapping: torch.Tensor, fmt: str = "int8") -> None:
+    """Quantizing append into 1-byte pools (uint8 [.., nb, Hkv, BS, D]) with
+    per-row fp32 scales ([.., nb, Hkv, BS]); fmt 'int8' or 'fp8' (OCP e4m3)."""
+    _dev(k_pool, "k_pool", torch.uint8), _dev(v_pool, "v_pool", torch.uint8)
+    _dev(k_scale, "k_scale", torch.float32), _dev(v_scale, "v_scale", torch.float32)
+    _dev(k_new, "k_new", torch.float32), _dev(v_new, "v_new", torch.float32)
+    _dev(slot_mapping, "slot_mapping", torch.int64)
+    multi = k_pool.dim() == 5
+    n_layers = k_pool.shape[0] if multi else 1
+    nb, hkv, bs, d = k_pool.shape[-4:]
+    if k_scale.shape != k_pool.shape[:-1] or v_scale.shape != v_pool.shape[:-1]:
+        raise ValueError("scale pools must be the byte pools' shape without head_dim")
+    n_tok = k_new.shape[-3]
+    if slot_mapping.shape != (n_tok,) or k_new.shape[-2:] != (hkv, d):
+        raise ValueError("k_new / slot_mapping shapes do not match the pool")
+    pool_ls = nb * hkv * bs * d if multi else 0
+    src_ls = n_tok * hkv * d if multi else 0
+    check(lib().rkv_append_q(k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(),
+                             v_scale.data_ptr(), pool_ls, k_new.data_ptr(), v_new.data_ptr(),
+                             src_ls, hkv * d, d, slot_mapping.data_ptr(), n_tok, n_layers, hkv,
+                             d, bs, nb, _qcode(fmt), _stream(k_pool)))
+
+
+def gather_q(k_pool: torch.Tensor, v_pool: torch.Tensor, k_scale: torch.Tensor,
+             v_scale: torch.Tensor, block_tables: torch.Tensor, ctx_lens: torch.Tensor,
+             fmt: str = "int8", *, max_ctx: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dequantized K/V per sequence, padded fp32 [B, Hkv, max_ctx, D]."""
+    nb, hkv, bs, d = k_pool.shape
+    B, mbs = block_tables.shape
+    if max_ctx is None:
+        max_ctx = mbs * bs
+    k_out = torch.zeros((B, hkv, max_ctx, d), dtype=torch.float32, device=k_pool.device)
+    v_out = torch.zeros_like(k_out)
+    check(lib().rkv_gather_q(k_out.data_ptr(), v_out.data_ptr(), k_pool.data_ptr(),
+                             v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+                             block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), None, B, hkv, d,
+                             bs, nb, max_ctx, _qcode(fmt), _stream(k_pool)))
+    return k_out, v_out
+
+
+def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                       k_scale: torch.Tensor, v_scale: torch.Tensor, block_tables: torch.Tensor,
+                       ctx_lens: torch.Tensor, scale: float | None = None, fmt: str = "int8", *,
+                       max_context: int | None = None, out: torch.Tensor | None = None,
+                       workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """decode_attention over 1-byte pools with per-row scales."""
+    _dev(q, "q", torch.float32), _dev(k_pool, "k_pool", torch.uint8)
+    _dev(v_pool, "v_pool", torch.uint8), _dev(k_scale, "k_scale", torch.float32)
+    _dev(v_scale, "v_scale", torch.float32)
+    _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
+    nb, hkv, bs, d = k_pool.shape
+    B, hq, _ = q.shape
+    mbs = block_tables.shape[1]
+    if max_context is None:
+        max_context = mbs * bs
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    need = workspace_bytes(B, hq, d, max_context)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_len = workspace.numel() if workspace is not None else 0
+    check(lib().rkv_decode_attention_q(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(),
+                                       v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
+                                       block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), B, hq,
+                                       hkv, d, bs, nb, max_context, float(scale), _qcode(fmt), 0,
+                                       ws_ptr, ws_len, _stream(q)))
+    return out
+
+
 def prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                       block_tables: torch.Tensor, q_start: torch.Tensor, ctx_lens: torch.Tensor,
                       scale: float | None = None, *, max_q_len: int | None = None,
@@ -204,4 +288,4 @@ def prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tenso
 
 
 __all__ = ["append", "gather", "copy_blocks", "decode_attention", "prefill_attention",
-           "workspace_bytes", "_lib"]
+           "append_q", "gather_q", "decode_attention_q", "workspace_bytes", "_lib"]

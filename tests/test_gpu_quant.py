@@ -1,0 +1,168 @@
+"""GPU parity of the 1-byte KV pools (int8 and OCP fp8 e4m3, one fp32 scale
+per (token, KV head) row) against the oracle.
+
+  * append_q: bytes and scales bit-exact (the oracle quantizes with the same
+    rules: tests/test_oracle.py pins them against torch's e4m3 cast and an
+    independent numpy int8 formulation);
+  * gather_q: dequantized values bit-exact (byte value * row scale);
+  * decode_attention_q: within max-abs 1e-4 / rel 1e-3 of the oracle's decode
+    on the dequantized fp32 pool (the decode tolerance).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from rustral_amd import kv
+from tests.gpu_util import say, to_dev, to_np
+from tests.helpers import assert_allclose_ref, contexts, make_tables
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+CODE = {"int8": oracle.I8, "fp8": oracle.FP8}
+
+
+def quant_case(seed, nb, hkv, bs, d, fmt, fill_slots=None):
+    """Pools filled through the oracle's quantizing append: every slot (or the
+    given ones) holds a quantized N(0,1) row; other rows keep canary bytes and
+    scale 1e30 (never read for valid tokens)."""
+    rng = np.random.default_rng(seed)
+    kp = rng.integers(0, 256, (nb, hkv, bs, d), dtype=np.uint8)
+    vp = rng.integers(0, 256, (nb, hkv, bs, d), dtype=np.uint8)
+    ks = np.full((nb, hkv, bs), 1e30, np.float32)
+    vs = ks.copy()
+    slots = np.arange(nb * bs, dtype=np.int64) if fill_slots is None else fill_slots
+    kn = (rng.standard_normal((len(slots), hkv, d)) * rng.random((len(slots), hkv, 1)) * 3)
+    vn = rng.standard_normal((len(slots), hkv, d))
+    oracle.append_q(kp, vp, ks, vs, kn.astype(np.float32), vn.astype(np.float32), slots,
+                    CODE[fmt])
+    return kp, vp, ks, vs
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+@pytest.mark.parametrize("hkv,d,nl", [(8, 128, 1), (4, 64, 3), (2, 32, 2), (32, 128, 1)])
+def test_append_q_bitexact(dev, fmt, hkv, d, nl):
+    say(f"append_q fmt={fmt} hkv={hkv} d={d} layers={nl}")
+    rng = np.random.default_rng(hkv * 100 + d + nl)
+    nb, bs, n = 40, 16, 300
+    kp = rng.integers(0, 256, (nl, nb, hkv, bs, d), dtype=np.uint8)
+    vp = rng.integers(0, 256, (nl, nb, hkv, bs, d), dtype=np.uint8)
+    ks = rng.standard_normal((nl, nb, hkv, bs)).astype(np.float32)
+    vs = rng.standard_normal((nl, nb, hkv, bs)).astype(np.float32)
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[::29] = -1
+    kn = (rng.standard_normal((nl, n, hkv, d)) * 4).astype(np.float32)
+    vn = rng.standard_normal((nl, n, hkv, d)).astype(np.float32)
+    kn[0, 3] = 0.0                     # an all-zero row: scale 0, bytes 0
+    kn[0, 4, 0, 5] = 1e4               # one dominating element
+    g = [to_dev(a, dev) for a in (kp, vp, ks, vs)]
+    if nl == 1:
+        kv.append_q(g[0][0], g[1][0], g[2][0], g[3][0], to_dev(kn[0], dev), to_dev(vn[0], dev),
+                    to_dev(slots, dev), fmt)
+    else:
+        kv.append_q(*g, to_dev(kn, dev), to_dev(vn, dev), to_dev(slots, dev), fmt)
+    for l in range(nl):
+        oracle.append_q(kp[l], vp[l], ks[l], vs[l], kn[l], vn[l], slots, CODE[fmt])
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(g[0]), kp) and np.array_equal(to_np(g[1]), vp)
+    assert np.array_equal(to_np(g[2]).view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(to_np(g[3]).view(np.uint32), vs.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_gather_q_dequantizes_bitexact(dev, fmt):
+    say(f"gather_q fmt={fmt}")
+    rng = np.random.default_rng(21)
+    nb, hkv, bs, d = 120, 8, 16, 128
+    ctx = np.array([0, 1, 15, 16, 17, 300, 999], np.int32)
+    kp, vp, ks, vs = quant_case(21, nb, hkv, bs, d, fmt)
+    tables = make_tables(rng, ctx, bs, nb)
+    k_out, v_out = kv.gather_q(to_dev(kp, dev), to_dev(vp, dev), to_dev(ks, dev),
+                               to_dev(vs, dev), to_dev(tables, dev), to_dev(ctx, dev), fmt,
+                               max_ctx=1008)
+    torch.cuda.synchronize()
+    kf = oracle.dequantize_pool(kp, ks, CODE[fmt])
+    vf = oracle.dequantize_pool(vp, vs, CODE[fmt])
+    wk, wv = oracle.gather(kf, vf, tables, ctx, max_ctx=1008)
+    assert np.array_equal(to_np(k_out), wk) and np.array_equal(to_np(v_out), wv)
+
+
+def run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, fmt, max_context=None):
+    out = kv.decode_attention_q(to_dev(q, dev), to_dev(kp, dev), to_dev(vp, dev),
+                                to_dev(ks, dev), to_dev(vs, dev), to_dev(tables, dev),
+                                to_dev(ctx, dev), scale, fmt, max_context=max_context)
+    torch.cuda.synchronize()
+    return to_np(out)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64), (16, 2, 128), (8, 1, 128),
+                                      (4, 4, 64), (2, 1, 64)])
+def test_decode_q_matches_oracle_on_dequantized_pool(dev, fmt, hq, hkv, d):
+    say(f"decode_q fmt={fmt} hq={hq} hkv={hkv} d={d}")
+    rng = np.random.default_rng(hq * 7 + d)
+    ctx = np.array([1, 2, 15, 16, 17, 255, 512, 513, 1000, 2100], np.int32)
+    bs = 16
+    nb = int(sum((c + bs - 1) // bs for c in ctx)) + 4
+    kp, vp, ks, vs = quant_case(hq + d, nb, hkv, bs, d, fmt)
+    tables = make_tables(rng, ctx, bs, nb)
+    q = rng.standard_normal((len(ctx), hq, d)).astype(np.float32)
+    scale = float(np.float32(1 / math.sqrt(d)))
+    got = run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, fmt)
+    kf = oracle.dequantize_pool(kp, ks, CODE[fmt])
+    vf = oracle.dequantize_pool(vp, vs, CODE[fmt])
+    want = oracle.decode_attention(q, kf, vf, tables, ctx, scale)
+    assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle (dequantized pool)")
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_decode_q_config2_shape_and_partial_blocks(dev, fmt):
+    """configs[2] shape (B64, Hq32, Hkv8, D128, L in U[512, 4096]); only the
+    context's slots are written, so the unwritten rows of each sequence's last
+    block keep canary bytes and a 1e30 scale and must not leak in."""
+    say(f"decode_q configs[2] shape fmt={fmt}")
+    rng = np.random.default_rng(30)
+    ctx = contexts(rng, 64, 512, 4096)
+    bs, hkv, d = 16, 8, 128
+    nb = int(sum((c + bs - 1) // bs for c in ctx))
+    tables = make_tables(rng, ctx, bs, nb)
+    slots = np.concatenate([tables[b, np.arange(L) // bs].astype(np.int64) * bs + np.arange(L) % bs
+                            for b, L in enumerate(ctx)])
+    kp, vp, ks, vs = quant_case(31, nb, hkv, bs, d, fmt, fill_slots=slots)
+    q = rng.standard_normal((64, 32, d)).astype(np.float32)
+    got = run_q(dev, q, kp, vp, ks, vs, tables, ctx, 1 / math.sqrt(d), fmt, max_context=4096)
+    kf = oracle.dequantize_pool(kp, ks, CODE[fmt])
+    vf = oracle.dequantize_pool(vp, vs, CODE[fmt])
+    want = oracle.decode_attention(q, kf, vf, tables, ctx, 1 / math.sqrt(d), n_threads=8)
+    assert np.isfinite(got).all()
+    assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle")
+
+
+def test_decode_q_quantization_error_is_small(dev):
+    """Against fp32 attention on the unquantized values: the int8 / fp8
+    storage error stays within a few 1e-2 (max-abs) on N(0,1) data."""
+    say("decode_q vs unquantized fp32")
+    rng = np.random.default_rng(40)
+    ctx = np.array([300, 1000, 2000], np.int32)
+    bs, hkv, d, hq = 16, 2, 128, 8
+    nb = int(sum((c + bs - 1) // bs for c in ctx))
+    tables = make_tables(rng, ctx, bs, nb)
+    kf = rng.standard_normal((nb, hkv, bs, d)).astype(np.float32)
+    vf = rng.standard_normal((nb, hkv, bs, d)).astype(np.float32)
+    q = rng.standard_normal((3, hq, d)).astype(np.float32)
+    want = oracle.decode_attention(q, kf, vf, tables, ctx, 1 / math.sqrt(d))
+    slots = np.arange(nb * bs, dtype=np.int64)
+    for fmt, tol in (("int8", 2e-2), ("fp8", 6e-2)):
+        kp = np.zeros((nb, hkv, bs, d), np.uint8)
+        vp = np.zeros_like(kp)
+        ks = np.zeros((nb, hkv, bs), np.float32)
+        vs = np.zeros_like(ks)
+        oracle.append_q(kp, vp, ks, vs, kf.transpose(0, 2, 1, 3).reshape(-1, hkv, d),
+                        vf.transpose(0, 2, 1, 3).reshape(-1, hkv, d), slots, CODE[fmt])
+        got = run_q(dev, q, kp, vp, ks, vs, tables, ctx, 1 / math.sqrt(d), fmt)
+        err = np.abs(got - want).max()
+        say(f"{fmt}: max |decode_q - fp32 decode| = {err:.3e}")
+        assert err < tol

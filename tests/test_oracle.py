@@ -384,3 +384,90 @@ def test_prefill_last_token_is_decode_and_negative_positions_are_zero():
     # more new tokens than context: the rows before position 0 are zero
     bad = oracle.prefill_attention(q, kp, vp, tables, qs, np.array([40, 1, 2], np.int32), 0.2)
     assert np.all(bad[qs[1]:qs[1] + 2] == 0.0) and np.any(bad[qs[1] + 2] != 0.0)
+
+
+# ---- 1-byte KV storage (int8 / OCP fp8 e4m3 with per-row scales) ------------
+
+def test_e4m3_decode_matches_torch_for_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    ours = oracle.f32_from_e4m3(codes)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(torch.float32).numpy()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan) and nan.sum() == 2       # 0x7f, 0xff
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_e4m3_encode_matches_torch_round_to_nearest_even():
+    """Within the format's range torch's cast is round-to-nearest-even; the
+    encoder must give the same byte.  Sample: every representable value, every
+    midpoint between neighbours (the ties), and dense random magnitudes."""
+    vals = oracle.f32_from_e4m3(np.arange(256, dtype=np.uint8))
+    pos = np.unique(vals[(vals >= 0) & np.isfinite(vals)])
+    mids = ((pos[1:].astype(np.float64) + pos[:-1]) / 2).astype(np.float32)
+    rng = np.random.default_rng(5)
+    dense = (rng.random(20000) * 464).astype(np.float32) * rng.choice([-1, 1], 20000)
+    tiny = (rng.random(2000) * 2 ** -5).astype(np.float32)
+    x = np.concatenate([pos, -pos, mids, -mids, dense, tiny, [464.0, -464.0, 0.0]]).astype(np.float32)
+    ours = oracle.e4m3_from_f32(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ours, ref)
+
+
+def test_e4m3_encode_saturates_and_keeps_nan():
+    x = np.array([465.0, 480.0, 1e6, np.inf, -500.0, -np.inf, np.nan], np.float32)
+    assert oracle.e4m3_from_f32(x).tolist() == [0x7e, 0x7e, 0x7e, 0x7e, 0xfe, 0xfe, 0x7f]
+
+
+def test_int8_rows_match_independent_numpy_formulation():
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((300, 128)) * rng.random((300, 1)) * 10).astype(np.float32)
+    x[0] = 0.0                                   # all-zero row: scale 0, bytes 0
+    x[1, :] = np.float32(0.5) * np.arange(128) / 127.0   # exact ties of rint
+    q, s = oracle.quantize_rows(x, oracle.I8)
+    amax = np.abs(x).max(axis=1)
+    inv = np.where(amax > 0, np.float32(127.0) / np.where(amax > 0, amax, 1), 0).astype(np.float32)
+    want = np.clip(np.rint(x * inv[:, None]), -127, 127).astype(np.int8)
+    assert np.array_equal(q.view(np.int8), want)
+    assert np.array_equal(s, (amax / np.float32(127.0)).astype(np.float32))
+    deq = oracle.dequantize_pool(q, s, oracle.I8)
+    assert np.all(np.abs(deq - x) <= s[:, None] * 0.5 * (1 + 1e-5) + 1e-30)
+
+
+def test_fp8_rows_match_torch_cast_of_the_scaled_row():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((300, 64)) * 3).astype(np.float32)
+    q, s = oracle.quantize_rows(x, oracle.FP8)
+    amax = np.abs(x).max(axis=1)
+    inv = (np.float32(448.0) / amax).astype(np.float32)
+    ref = torch.from_numpy((x * inv[:, None]).astype(np.float32)).to(torch.float8_e4m3fn)
+    assert np.array_equal(q, ref.view(torch.uint8).numpy())
+    assert np.array_equal(s, (amax / np.float32(448.0)).astype(np.float32))
+    deq = oracle.dequantize_pool(q, s, oracle.FP8)
+    assert np.all(np.abs(deq - x) <= np.abs(x) * 2.0 ** -4 + s[:, None] * 2.0 ** -9 + 1e-30)
+
+
+@pytest.mark.parametrize("dtype", ["i8", "fp8"])
+def test_append_q_matches_fancy_indexing(dtype):
+    code = oracle.I8 if dtype == "i8" else oracle.FP8
+    rng = np.random.default_rng(8)
+    nb, hkv, bs, d, n = 20, 4, 16, 64, 150
+    kp = rng.integers(0, 256, (nb, hkv, bs, d), dtype=np.uint8)   # canary bytes
+    vp = kp.copy()
+    ks = np.full((nb, hkv, bs), 7.0, np.float32)
+    vs = ks.copy()
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[::13] = -1
+    kn = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    ek, ev, eks, evs = kp.copy(), vp.copy(), ks.copy(), vs.copy()
+    oracle.append_q(kp, vp, ks, vs, kn, vn, slots, code)
+    ok = slots >= 0
+    blk, row = slots[ok] // bs, slots[ok] % bs
+    qk, sk = oracle.quantize_rows(kn[ok].reshape(-1, d), code)
+    qv, sv = oracle.quantize_rows(vn[ok].reshape(-1, d), code)
+    ek[blk, :, row, :] = qk.reshape(-1, hkv, d)
+    ev[blk, :, row, :] = qv.reshape(-1, hkv, d)
+    eks[blk, :, row] = sk.reshape(-1, hkv)
+    evs[blk, :, row] = sv.reshape(-1, hkv)
+    assert np.array_equal(kp, ek) and np.array_equal(vp, ev)
+    assert np.array_equal(ks, eks) and np.array_equal(vs, evs)
