@@ -107,6 +107,28 @@ void rkv_decoder_destroy(rkv_decoder* dec);
 int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int n_prompt, int n_new,
                          int32_t* out_tokens, float* out_logits);
 
+/* ---- parameters in safetensors files (host) ---------------------------------------
+ * The reference saves and loads models as safetensors keyed by stable
+ * parameter names (crates/runtime/src/model_io.rs:12-33 save_model, :36-105
+ * load_model: strict -- missing keys, extra keys, a shape or element-count
+ * mismatch and a dtype other than F32 are errors; __metadata__ is ignored).
+ * Names, in parameter order (kvd = n_kv_heads * d_head):
+ *   token_embedding.weight [V, d]
+ *   layers.{i}.norm1.weight / .bias [d]
+ *   layers.{i}.self_attn.{q,out}_proj.weight [d, d], .bias [d]
+ *   layers.{i}.self_attn.{k,v}_proj.weight [kvd, d], .bias [kvd]
+ *   layers.{i}.norm2.weight / .bias [d]
+ *   layers.{i}.ff_linear1.weight [f, d], .bias [f]
+ *   layers.{i}.ff_linear2.weight [d, f], .bias [d]
+ *   final_norm.weight / .bias [d]
+ *   lm_head.weight [V, d]
+ * (the reference's TransformerDecoder names, transformer.rs:894-935, with a
+ * .weight/.bias pair for this decoder's biased projections). */
+int rkv_decoder_load_safetensors(const rkv_decoder_config* cfg, const char* path,
+                                 float* host_params, int64_t n_params);
+int rkv_decoder_save_safetensors(const rkv_decoder_config* cfg, const float* host_params,
+                                 int64_t n_params, const char* path);
+
 /* ---- serving engine (continuous batching over the decoder) ----------------------
  * Replaces ServingEngine (crates/nn/src/continuous_batching.rs:493-537).  The
  * reference's step emits a dummy token for every scheduled request

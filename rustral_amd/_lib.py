@@ -75,6 +75,8 @@ SIGNATURES = {
     "rkv_decoder_create": (_p, [_p, _p, _i64, _p]),
     "rkv_decoder_destroy": (None, [_p]),
     "rkv_decoder_generate": (_i, [_p, _p, _i, _i, _p, _p]),
+    "rkv_decoder_load_safetensors": (_i, [_p, C.c_char_p, _p, _i64]),
+    "rkv_decoder_save_safetensors": (_i, [_p, _p, _i64, C.c_char_p]),
     "rkv_engine_create": (_p, [_p, _p, _i64, _i64, _i, _p]),
     "rkv_engine_destroy": (None, [_p]),
     "rkv_engine_submit": (_i64, [_p, _p, _i, _i, _i]),

@@ -51,6 +51,20 @@ def init_params(cfg: DecoderConfig, seed: int = 0, std: float = 0.02) -> np.ndar
     return out
 
 
+def load_safetensors(cfg: DecoderConfig, path: str) -> np.ndarray:
+    """Parameters from a safetensors file (strict: exactly the decoder's names,
+    shapes and F32), in the packed order rkv_decoder_create takes."""
+    out = np.empty(param_count(cfg), np.float32)
+    check(lib().rkv_decoder_load_safetensors(C.byref(cfg), str(path).encode(), _p(out), out.size))
+    return out
+
+
+def save_safetensors(cfg: DecoderConfig, params: np.ndarray, path: str) -> None:
+    params = np.ascontiguousarray(params, np.float32)
+    check(lib().rkv_decoder_save_safetensors(C.byref(cfg), _p(params), params.size,
+                                             str(path).encode()))
+
+
 def rng_raw(seed: int, n: int) -> np.ndarray:
     out = np.empty(n, np.uint64)
     check(lib().rkv_rng_raw(seed, _p(out), n))
