@@ -34,7 +34,8 @@ int rkv_embed(float* out, const float* table, const int32_t* ids, const float* p
 
 /* y[r][o] = sum_i x[r][i] * w[o][i] + b[o], the sum serial in i.
  * Replaces TensorOps::linear (lib.rs:478-534) + add_row_vector (:318-341).
- * w is [out_dim][in_dim] (the reference's Linear layout); b may be NULL. */
+ * w is [out_dim][in_dim] (the reference's Linear layout); b may be NULL;
+ * in_dim <= 8192. */
 int rkv_linear(float* y, const float* x, const float* w, const float* b, int rows, int in_dim,
                int out_dim, void* stream);
 

@@ -17,6 +17,7 @@
 #include "../../include/rustral_model.h"
 #include "../../include/rustral_serving.h"
 #include "model_layout.hpp"
+#include "model_ops.hpp"
 
 // ---- generator -------------------------------------------------------------------
 
@@ -125,7 +126,7 @@ struct rkv_decoder {
   int32_t* table = nullptr;  // [max_blocks] block table of the sequence
   float* logits = nullptr;   // [max_seq][vocab]
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr,
-        *a = nullptr, *f1 = nullptr, *f2 = nullptr;
+        *f2 = nullptr;
   void* ws = nullptr;
   size_t ws_bytes = 0;
   rkv_block_manager* bm = nullptr;
@@ -142,8 +143,7 @@ void release(rkv_decoder* dec) {
   if (!dec) return;
   void* bufs[] = {dec->params, dec->pe,  dec->k_pool, dec->v_pool, dec->ids,   dec->pos,
                   dec->ctx,    dec->slots, dec->table, dec->logits, dec->x,     dec->h,
-                  dec->q,      dec->k,   dec->v,      dec->o,       dec->a,     dec->f1,
-                  dec->f2,     dec->ws};
+                  dec->q,      dec->k,   dec->v,      dec->o,       dec->f2,    dec->ws};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   if (dec->bm) rkv_bm_destroy(dec->bm);
@@ -192,8 +192,8 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
             dalloc(dec->table, (size_t)dec->num_blocks) &&
             dalloc(dec->logits, S * (size_t)c.vocab) && dalloc(dec->x, d) && dalloc(dec->h, d) &&
             dalloc(dec->q, d) && dalloc(dec->k, (size_t)dec->kvd) &&
-            dalloc(dec->v, (size_t)dec->kvd) && dalloc(dec->o, d) && dalloc(dec->a, d) &&
-            dalloc(dec->f1, (size_t)c.d_ff) && dalloc(dec->f2, (size_t)c.d_ff);
+            dalloc(dec->v, (size_t)dec->kvd) && dalloc(dec->o, d) &&
+            dalloc(dec->f2, (size_t)c.d_ff);
   dec->ws_bytes = rkv_decode_workspace_bytes(1, c.n_heads, dh, c.max_seq, 0);
   if (ok && dec->ws_bytes) ok = hipMalloc(&dec->ws, dec->ws_bytes) == hipSuccess;
   if (!ok) {
@@ -288,13 +288,11 @@ extern "C" int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int
       RKV_TRY(rkv_decode_attention(dec->o, dec->q, kp, vp, dec->table, dec->num_blocks,
                                    dec->ctx + p, 1, H, Hk, dh, 16, dec->num_blocks, c.max_seq,
                                    scale, RKV_F32, 0, dec->ws, dec->ws_bytes, s));
-      RKV_TRY(rkv_linear(dec->a, dec->o, P + o.wo, P + o.bo, 1, d, d, s));
-      RKV_TRY(rkv_add(dec->x, dec->x, dec->a, d, s));
+      // x += o W_o^T + b_o; x += gelu(LN2(x) W_1^T + b_1) W_2^T + b_2 (fused epilogues)
+      RKV_TRY(linear_launch(dec->x, dec->o, P + o.wo, P + o.bo, dec->x, 1, 1, d, d, s));
       RKV_TRY(rkv_layer_norm(dec->h, dec->x, P + o.ln2_g, P + o.ln2_b, 1, d, c.eps, s));
-      RKV_TRY(rkv_linear(dec->f1, dec->h, P + o.w1, P + o.b1, 1, d, f, s));
-      RKV_TRY(rkv_gelu(dec->f2, dec->f1, f, s));
-      RKV_TRY(rkv_linear(dec->a, dec->f2, P + o.w2, P + o.b2, 1, f, d, s));
-      RKV_TRY(rkv_add(dec->x, dec->x, dec->a, d, s));
+      RKV_TRY(linear_launch(dec->f2, dec->h, P + o.w1, P + o.b1, nullptr, 2, 1, d, f, s));
+      RKV_TRY(linear_launch(dec->x, dec->f2, P + o.w2, P + o.b2, dec->x, 1, 1, f, d, s));
     }
     if (p + 1 < n_prompt) continue;  // prompt ids are known
     float* lg = dec->logits + (int64_t)produced * V;

@@ -29,6 +29,7 @@
 #include "../../include/rustral_model.h"
 #include "../../include/rustral_serving.h"
 #include "model_layout.hpp"
+#include "model_ops.hpp"
 
 struct rkv_engine {
   rkv_decoder_config cfg{};
@@ -46,8 +47,7 @@ struct rkv_engine {
           *last = nullptr, *out_tok = nullptr;
   int64_t* slots = nullptr;
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr,
-        *a = nullptr, *f1 = nullptr, *f2 = nullptr, *xl = nullptr, *hl = nullptr,
-        *logits = nullptr;
+        *f2 = nullptr, *xl = nullptr, *hl = nullptr, *logits = nullptr;
 };
 
 namespace {
@@ -66,8 +66,8 @@ void dfree(T*& p) {
 void free_step_buffers(rkv_engine* e) {
   dfree(e->ids), dfree(e->pos), dfree(e->q_start), dfree(e->ctx), dfree(e->tables);
   dfree(e->last), dfree(e->out_tok), dfree(e->slots);
-  dfree(e->x), dfree(e->h), dfree(e->q), dfree(e->k), dfree(e->v), dfree(e->o), dfree(e->a);
-  dfree(e->f1), dfree(e->f2), dfree(e->xl), dfree(e->hl), dfree(e->logits);
+  dfree(e->x), dfree(e->h), dfree(e->q), dfree(e->k), dfree(e->v), dfree(e->o);
+  dfree(e->f2), dfree(e->xl), dfree(e->hl), dfree(e->logits);
   e->cap_tok = e->cap_req = e->cap_tab = 0;
 }
 
@@ -95,8 +95,8 @@ bool reserve(rkv_engine* e, int64_t n_tok, int64_t n_req, int64_t mb) {
                   dalloc(e->out_tok, cr) && dalloc(e->tables, cb) && dalloc(e->x, ct * d) &&
                   dalloc(e->h, ct * d) && dalloc(e->q, ct * d) &&
                   dalloc(e->k, ct * (size_t)e->kvd) && dalloc(e->v, ct * (size_t)e->kvd) &&
-                  dalloc(e->o, ct * d) && dalloc(e->a, ct * d) && dalloc(e->f1, ct * f) &&
-                  dalloc(e->f2, ct * f) && dalloc(e->xl, cr * d) && dalloc(e->hl, cr * d) &&
+                  dalloc(e->o, ct * d) && dalloc(e->f2, ct * f) && dalloc(e->xl, cr * d) &&
+                  dalloc(e->hl, cr * d) &&
                   dalloc(e->logits, cr * (size_t)c.vocab);
   if (!ok) {
     free_step_buffers(e);
@@ -244,13 +244,11 @@ extern "C" int rkv_engine_step(rkv_engine* e) {
                        e->num_blocks, RKV_F32, s));
     RKV_TRY(rkv_prefill_attention(e->o, e->q, kp, vp, e->tables, mb, e->q_start, e->ctx, n_req,
                                   H, Hk, dh, 16, e->num_blocks, max_q, scale, RKV_F32, s));
-    RKV_TRY(rkv_linear(e->a, e->o, P + o.wo, P + o.bo, T, d, d, s));
-    RKV_TRY(rkv_add(e->x, e->x, e->a, (int64_t)T * d, s));
+    // x += o W_o^T + b_o; x += gelu(LN2(x) W_1^T + b_1) W_2^T + b_2 (fused epilogues)
+    RKV_TRY(linear_launch(e->x, e->o, P + o.wo, P + o.bo, e->x, 1, T, d, d, s));
     RKV_TRY(rkv_layer_norm(e->h, e->x, P + o.ln2_g, P + o.ln2_b, T, d, c.eps, s));
-    RKV_TRY(rkv_linear(e->f1, e->h, P + o.w1, P + o.b1, T, d, f, s));
-    RKV_TRY(rkv_gelu(e->f2, e->f1, (int64_t)T * f, s));
-    RKV_TRY(rkv_linear(e->a, e->f2, P + o.w2, P + o.b2, T, f, d, s));
-    RKV_TRY(rkv_add(e->x, e->x, e->a, (int64_t)T * d, s));
+    RKV_TRY(linear_launch(e->f2, e->h, P + o.w1, P + o.b1, nullptr, 2, T, d, f, s));
+    RKV_TRY(linear_launch(e->x, e->f2, P + o.w2, P + o.b2, e->x, 1, T, f, d, s));
   }
   // each request's last row: final norm, lm_head (no bias, transformer.rs:789), greedy
   const int64_t fin = layer_offsets(c, c.n_layers - 1).end;

@@ -7,7 +7,7 @@
 // reference's summation order: one thread owns one output and adds its terms
 // serially, with floating-point contraction off, so the results are the bits
 // the ndarray backend computes (except gelu's tanh, from the device library).
-#include "common.hpp"
+#include "model_ops.hpp"
 
 #include <cmath>
 
@@ -37,24 +37,61 @@ __global__ __launch_bounds__(256) void embed_kernel(float* __restrict__ out,
   out[(int64_t)t * dim + i] = v;
 }
 
-// One thread per output; the dot product runs serially over in_dim.
-__global__ __launch_bounds__(64) void linear_kernel(float* __restrict__ y,
-                                                    const float* __restrict__ x,
-                                                    const float* __restrict__ w,
-                                                    const float* __restrict__ b, int rows,
-                                                    int in_dim, int out_dim) {
+// One thread per output; the dot product runs serially over in_dim (the
+// reference's order).  The input row is staged in LDS (coalesced) and each
+// thread reads its weight row four floats at a time, so the serial sum is not
+// waiting on scattered scalar loads.  EPI: 0 y = sum + b; 1 y = res + (sum + b)
+// (a fused residual add; y may be res); 2 y = gelu(sum + b).
+constexpr int kMaxStagedIn = 8192;  // floats of the input row kept in LDS
+
+__device__ __forceinline__ float gelu_f(float v) {
 #pragma clang fp contract(off)
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  const int r = blockIdx.y;
-  if (o >= out_dim || r >= rows) return;
-  const float* xr = x + (int64_t)r * in_dim;
-  const float* wo = w + (int64_t)o * in_dim;
-  float sum = 0.0f;
-  for (int i = 0; i < in_dim; ++i) sum += xr[i] * wo[i];
-  y[(int64_t)r * out_dim + o] = b ? sum + b[o] : sum;
+  const float k = sqrtf(2.0f / 3.14159265358979323846f);
+  const float x3 = v * v * v;
+  const float xp = v + 0.044715f * x3;
+  const float t = tanhf(k * xp);
+  return 0.5f * v * (1.0f + t);
 }
 
-// One wave per row: lane 0 forms the serial sums, every lane writes outputs.
+template <int EPI, bool VEC>
+__global__ __launch_bounds__(64) void linear_kernel(float* y, const float* __restrict__ x,
+                                                    const float* __restrict__ w,
+                                                    const float* __restrict__ b, const float* res,
+                                                    int rows, int in_dim, int out_dim) {
+#pragma clang fp contract(off)
+  __shared__ float s_x[kMaxStagedIn];
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  const int r = blockIdx.y;
+  const float* xr = x + (int64_t)r * in_dim;
+  for (int i = threadIdx.x; i < in_dim; i += 64) s_x[i] = xr[i];
+  __syncthreads();
+  if (o >= out_dim || r >= rows) return;
+  const float* wo = w + (int64_t)o * in_dim;
+  float sum = 0.0f;
+  if constexpr (VEC) {  // in_dim % 4 == 0 and w 16-byte aligned
+#pragma unroll 8
+    for (int i = 0; i < in_dim; i += 4) {
+      const float4 wv = *reinterpret_cast<const float4*>(wo + i);
+      sum += s_x[i] * wv.x;
+      sum += s_x[i + 1] * wv.y;
+      sum += s_x[i + 2] * wv.z;
+      sum += s_x[i + 3] * wv.w;
+    }
+  } else {
+    for (int i = 0; i < in_dim; ++i) sum += s_x[i] * wo[i];
+  }
+  const int64_t at = (int64_t)r * out_dim + o;
+  const float v = b ? sum + b[o] : sum;
+  if constexpr (EPI == 1)
+    y[at] = res[at] + v;
+  else if constexpr (EPI == 2)
+    y[at] = gelu_f(v);
+  else
+    y[at] = v;
+}
+
+// One wave per row: the row is staged in LDS, lane 0 forms the serial sums
+// from it, every lane writes outputs.
 __global__ __launch_bounds__(64) void layer_norm_kernel(float* __restrict__ y,
                                                         const float* __restrict__ x,
                                                         const float* __restrict__ g,
@@ -62,16 +99,19 @@ __global__ __launch_bounds__(64) void layer_norm_kernel(float* __restrict__ y,
                                                         int dim, float eps) {
 #pragma clang fp contract(off)
   __shared__ float s_stat[2];
+  __shared__ float s_row[8192];
   const int r = blockIdx.x, lane = threadIdx.x;
   if (r >= rows) return;
   const float* xr = x + (int64_t)r * dim;
+  for (int i = lane; i < dim; i += 64) s_row[i] = xr[i];
+  __syncthreads();
   if (lane == 0) {
     float sum = 0.0f;
-    for (int i = 0; i < dim; ++i) sum += xr[i];
+    for (int i = 0; i < dim; ++i) sum += s_row[i];
     const float mean = sum / (float)dim;
     float vs = 0.0f;
     for (int i = 0; i < dim; ++i) {
-      const float t = xr[i] - mean;
+      const float t = s_row[i] - mean;
       vs += t * t;
     }
     s_stat[0] = mean;
@@ -79,20 +119,14 @@ __global__ __launch_bounds__(64) void layer_norm_kernel(float* __restrict__ y,
   }
   __syncthreads();
   const float mean = s_stat[0], sd = s_stat[1];
-  for (int i = lane; i < dim; i += 64) y[(int64_t)r * dim + i] = (xr[i] - mean) / sd * g[i] + b[i];
+  for (int i = lane; i < dim; i += 64) y[(int64_t)r * dim + i] = (s_row[i] - mean) / sd * g[i] + b[i];
 }
 
 __global__ __launch_bounds__(256) void gelu_kernel(float* __restrict__ y,
                                                    const float* __restrict__ x, int64_t n) {
-#pragma clang fp contract(off)
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float k = sqrtf(2.0f / 3.14159265358979323846f);
-  const float v = x[i];
-  const float x3 = v * v * v;
-  const float xp = v + 0.044715f * x3;
-  const float t = tanhf(k * xp);
-  y[i] = 0.5f * v * (1.0f + t);
+  y[i] = gelu_f(x[i]);
 }
 
 // y may alias a or b (in-place residual add)
@@ -147,6 +181,31 @@ __global__ __launch_bounds__(64) void argmax_kernel(int32_t* __restrict__ out,
 unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
+
+// Shared by rkv_linear and the decoder / engine (fused epilogues).
+int linear_launch(float* y, const float* x, const float* w, const float* b, const float* res,
+                  int epi, int rows, int in_dim, int out_dim, hipStream_t s) {
+  if (rows < 0 || in_dim <= 0 || out_dim <= 0)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_linear: bad size argument");
+  if (rows == 0) return RKV_OK;
+  if (rows > 65535) return fail(RKV_ERR_INVALID_ARG, "rkv_linear: rows must be <= 65535");
+  if (in_dim > kMaxStagedIn) return fail(RKV_ERR_UNSUPPORTED, "rkv_linear: in_dim must be <= 8192");
+  if (!y || !x || !w || (epi == 1 && !res))
+    return fail(RKV_ERR_INVALID_ARG, "rkv_linear: null pointer argument");
+  const bool vec = in_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+  const dim3 grid(blocks_for(out_dim, 64), (unsigned)rows);
+#define RKV_LIN(E, V) linear_kernel<E, V><<<grid, 64, 0, s>>>(y, x, w, b, res, rows, in_dim, out_dim)
+  if (epi == 1) {
+    if (vec) RKV_LIN(1, true); else RKV_LIN(1, false);
+  } else if (epi == 2) {
+    if (vec) RKV_LIN(2, true); else RKV_LIN(2, false);
+  } else {
+    if (vec) RKV_LIN(0, true); else RKV_LIN(0, false);
+  }
+#undef RKV_LIN
+  return check_launch("rkv_linear");
+}
+
 }  // namespace rkv
 
 using namespace rkv;
@@ -170,14 +229,8 @@ extern "C" int rkv_embed(float* out, const float* table, const int32_t* ids, con
 extern "C" int rkv_linear(float* y, const float* x, const float* w, const float* b, int rows,
                           int in_dim, int out_dim, void* stream) {
   clear_error();
-  if (rows < 0 || in_dim <= 0 || out_dim <= 0)
-    return fail(RKV_ERR_INVALID_ARG, "rkv_linear: bad size argument");
-  if (rows == 0) return RKV_OK;
-  if (rows > 65535) return fail(RKV_ERR_INVALID_ARG, "rkv_linear: rows must be <= 65535");
-  if (!y || !x || !w) return fail(RKV_ERR_INVALID_ARG, "rkv_linear: null pointer argument");
-  linear_kernel<<<dim3(blocks_for(out_dim, 64), (unsigned)rows), 64, 0,
-                  static_cast<hipStream_t>(stream)>>>(y, x, w, b, rows, in_dim, out_dim);
-  return check_launch("rkv_linear");
+  return linear_launch(y, x, w, b, nullptr, 0, rows, in_dim, out_dim,
+                       static_cast<hipStream_t>(stream));
 }
 
 extern "C" int rkv_layer_norm(float* y, const float* x, const float* g, const float* b, int rows,

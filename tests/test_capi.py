@@ -105,3 +105,9 @@ def test_prefill_rejects_bad_arguments():
     assert call(B=0) == 0 and call(mq=0) == 0          # nothing to do: no launch
     assert L.rkv_prefill_attention(None, 16, 16, 16, 16, 4, 16, 16, 2, 8, 2, 128, 16, 10, 16,
                                    0.1, RKV_BF16, None) == RKV_ERR_INVALID_ARG
+
+
+def test_linear_rejects_rows_too_wide_for_staging():
+    L = _lib.lib()
+    assert L.rkv_linear(16, 16, 16, None, 1, 8193, 4, None) == RKV_ERR_UNSUPPORTED
+    assert "in_dim" in L.rkv_last_error().decode()

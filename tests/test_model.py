@@ -206,7 +206,7 @@ def torch_dev(dev):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,i,o", [(1, 128, 128), (1, 128, 512), (1, 512, 128), (3, 128, 1000),
-                                      (5, 33, 7)])
+                                      (5, 33, 7), (2, 8192, 70), (1, 4097, 65)])
 def test_gpu_linear_bit_exact(torch_dev, rows, i, o):
     torch, dev = torch_dev
     rng = np.random.default_rng(rows * 100 + i + o)
