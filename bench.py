@@ -571,9 +571,13 @@ def run_config4(torch, dev, args):
     sequences finish (blocks freed), the block manager plans a compaction of
     up to 25% of the live blocks and copy_blocks moves them (all layers, K and
     V, one launch), 10% new sequences are admitted with 128-token prefills
-    appended in bulk (one launch for all layers), then one decode token for
-    every running sequence: append (one launch) + 32 decode-attention calls.
-    Hq = 32 (GQA 4:1) is assumed; BASELINE does not state it."""
+    appended in bulk (one launch for all layers) and run through causal
+    prefill attention (one call per layer), then one decode token for every
+    running sequence: append (one launch) + 32 decode-attention calls.
+    Hq = 32 (GQA 4:1) is assumed; BASELINE does not state it.  One untimed
+    and four timed steps: every step replaces 10% of the sequences by
+    128-token ones, so a longer run drifts away from the configuration's
+    context distribution U[1, 8192]."""
     import numpy as np
     from rustral_amd import kv
     from rustral_amd.serving import PagedCache
@@ -601,11 +605,16 @@ def run_config4(torch, dev, args):
     vn_dec = torch.randn_like(kn_dec)
     q = torch.randn((B, HQ, D), generator=g, device=dev)
     out = torch.empty_like(q)
+    q_pre = torch.randn((n_turn * pre, HQ, D), generator=g, device=dev)
+    out_pre = torch.empty_like(q_pre)
+    d_qs = torch.arange(0, (n_turn + 1) * pre, pre, dtype=torch.int32, device=dev)
+    d_cpre = torch.full((n_turn,), pre, dtype=torch.int32, device=dev)
     ws = torch.empty(kv.workspace_bytes(B, HQ, D, 8192 + 64 * BS), dtype=torch.uint8, device=dev)
     scale = 1.0 / math.sqrt(D)
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     steps = []
-    for step in range(args.warmup + max(args.steps, 3)):
+    warmup, timed = 1, 4
+    for step in range(warmup + timed):
         t_host = time.perf_counter()
         ids = sorted(ctx)
         n_fin = n_turn
@@ -622,6 +631,7 @@ def run_config4(torch, dev, args):
             next_id += 1
         slots_pre = np.concatenate([np.asarray(cache.table(i), np.int64)[np.arange(pre) // BS] * BS
                                     + np.arange(pre) % BS for i in admitted])
+        tab_pre = cache.fill_tables(admitted, pre // BS)
         ids = sorted(ctx)
         for i in ids:                                  # room for the decode token
             cache.reserve(i, ctx[i] + 1)
@@ -635,19 +645,24 @@ def run_config4(torch, dev, args):
         cl_after = cl + 1
         d_pairs = torch.from_numpy(pairs.astype(np.int32)).to(dev)
         d_spre = torch.from_numpy(slots_pre).to(dev)
+        d_tpre = torch.from_numpy(tab_pre).to(dev)
         d_sdec = torch.from_numpy(slots_dec).to(dev)
         d_tab = torch.from_numpy(tables).to(dev)
         d_ctx = torch.from_numpy(cl_after).to(dev)
         n_pre = len(slots_pre)
         torch.cuda.synchronize()
         t_host = time.perf_counter() - t_host
-        e = [ev() for _ in range(5)]
+        e = [ev() for _ in range(6)]
         e[0].record()
         if len(pairs):
             kv.copy_blocks(kp, vp, d_pairs)
         e[1].record()
         kv.append(kp, vp, kn_pre, vn_pre, d_spre)
         e[2].record()
+        for l in range(n_layers):
+            kv.prefill_attention(q_pre, kp[l], vp[l], d_tpre, d_qs, d_cpre, scale, max_q_len=pre,
+                                 out=out_pre)
+        e[5].record()
         nb_ = len(ids)
         assert nb_ == B and n_pre == n_turn * pre
         kv.append(kp, vp, kn_dec, vn_dec, d_sdec)
@@ -657,26 +672,31 @@ def run_config4(torch, dev, args):
                                 max_context=mb * BS, out=out, workspace=ws)
         e[4].record()
         torch.cuda.synchronize()
-        if step < args.warmup:
+        if step < warmup:
             continue
-        ms = [e[i].elapsed_time(e[i + 1]) for i in range(4)]
+        ms = [e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2]), e[2].elapsed_time(e[5]),
+              e[5].elapsed_time(e[3]), e[3].elapsed_time(e[4])]
         copy_b = len(pairs) * n_layers * 2 * blk_bytes * 2
         pre_b = n_pre * n_layers * HKV * D * 2 * (4 + 2) + n_pre * 8
         dec_app_b = nb_ * n_layers * HKV * D * 2 * (4 + 2) + nb_ * 8
         attn_b = n_layers * (int(cl_after.astype(np.int64).sum()) * HKV * D * 2 * 2
                              + nb_ * HQ * D * 8 + int(sum(-(-c // BS) for c in cl_after)) * 4)
+        pa_b, pa_f = prefill_bytes_flops(np.full(n_turn, pre), np.full(n_turn, pre))
         steps.append(dict(pairs=len(pairs), live_blocks=live, prefill_tokens=n_pre,
                           running=nb_, ms=ms, host_ms=1e3 * t_host,
-                          bytes=[copy_b, pre_b, dec_app_b, attn_b]))
+                          bytes=[copy_b, pre_b, n_layers * pa_b, dec_app_b, attn_b]))
     n = len(steps)
     ms = np.array([s["ms"] for s in steps]).mean(0)
     by = np.array([s["bytes"] for s in steps], np.float64).mean(0)
     gbps = by / (ms * 1e-3) / 1e9
     total_ms = float(ms.sum())
     total_gbps = float(by.sum() / (total_ms * 1e-3) / 1e9)
-    comps = ["copy_blocks", "prefill_append", "decode_append", "decode_attention_32_layers"]
-    return _line("continuous-batching step GB/s (append + copy + decode attention)", total_gbps,
-                 "GB/s", total_ms, args, "bf16",
+    comps = ["copy_blocks", "prefill_append", "prefill_attention_32_layers", "decode_append",
+             "decode_attention_32_layers"]
+    import types
+    return _line("continuous-batching step GB/s (copy + prefill append/attention + decode "
+                 "append/attention)", total_gbps,
+                 "GB/s", total_ms, types.SimpleNamespace(steps=timed, warmup=warmup), "bf16",
                  {"workload": "configs[4] continuous-batching step mix", "running": B,
                   "layers": n_layers, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
                   "block_size": BS, "pool_blocks_per_layer": nblk, "prefill": pre},
