@@ -10,9 +10,9 @@
 // to the tile's last query position:
 //   * stage: the KB blocks' K tiles (row-major, rows padded) and V tiles
 //     (stored transposed, V^T[dim][key]) go through registers into LDS,
-//     double buffered: the next iteration's loads are in flight while this
-//     one is computed.  A wave skips the arithmetic of key blocks that lie
-//     entirely after its last query (causal).
+//     double buffered; the loads run two iterations ahead of the compute.
+//     A wave skips the arithmetic of key blocks that lie entirely after its
+//     last query (causal).
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = K rows from LDS, B = Q^T
 //     (queries of the 16 tokens, split hi + lo bf16 so the scores carry ~16
 //     significant bits of q).  Result: lane l holds S^T[key 4(l/16)+r][row
@@ -20,9 +20,10 @@
 //   * causal mask (key position > query position -> excluded), then an
 //     online softmax per row: running max m and sum l, the accumulator
 //     rescaled by 2^(m_old - m_new).  Scores carry scale * log2(e) (exp2).
-//   * O^T += V^T P^T on v_mfma_f32_16x16x16_bf16: A = V^T from LDS, B = P^T,
-//     which is exactly the S^T layout above (no cross-lane moves); P is split
-//     hi + lo like q.  Result: lane l holds O^T[dim 16c + 4(l/16)+r][row l%16].
+//   * O^T += V^T P^T on v_mfma_f32_16x16x32_bf16 over two key blocks at a
+//     time (16x16x16 for an odd KB): A = V^T from LDS, B = P^T, which is
+//     exactly the S^T layout above (no cross-lane moves); P is split hi + lo
+//     like q.  Result: lane l holds O^T[dim 16c + 4(l/16)+r][row l%16].
 // fp32 pools split K and V into hi + lo bf16 as well (three products each).
 // MFMA lane layouts (gfx950): 16x16x32: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16];
 // 16x16x16: A[l%16][4(l/16)+e], B[4(l/16)+e][l%16]; both D[4(l/16)+r][l%16].
@@ -112,10 +113,13 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
     }
     return __builtin_amdgcn_readlane(idv, j & 63);
   };
-  uint4 kr[PT], vr[PT];
+  // Two register sets: the loads of iteration it + 2 are issued while
+  // iteration it is computed (one workgroup fills a CU, so its own loads
+  // have to be in flight early).
+  uint4 kr0[PT], vr0[PT], kr1[PT], vr1[PT];
   // Issues iteration it's K/V loads (KB blocks) into registers; returns a
   // bit per block whose id is valid.
-  auto fetch = [&](int it) __attribute__((always_inline)) {
+  auto fetch = [&](int it, uint4 (&kr)[PT], uint4 (&vr)[PT]) __attribute__((always_inline)) {
     uint32_t okm = 0;
     int64_t base[KB];
 #pragma unroll
@@ -141,7 +145,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
     return okm;
   };
   // Writes the registers into LDS buffer buf: K row-major, V transposed.
-  auto stage = [&](int buf) __attribute__((always_inline)) {
+  auto stage = [&](int buf, const uint4 (&kr)[PT], const uint4 (&vr)[PT])
+                   __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
       const int ci = tid + i * NT;
@@ -177,7 +182,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
     }
   };
 
-  uint32_t ok_next = nit > 0 ? fetch(0) : 0u;
+  uint32_t ok0 = nit > 0 ? fetch(0, kr0, vr0) : 0u;
+  uint32_t ok1 = nit > 1 ? fetch(1, kr1, vr1) : 0u;
 
   // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8], hi and lo.
   uint4 qhi[NC], qlo[NC];
@@ -200,15 +206,11 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
   for (int c = 0; c < NO; ++c) o[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, l = 0.0f;
 
-  for (int it = 0; it < nit; ++it) {
-    const int buf = it & 1;
-    stage(buf);
-    const uint32_t okm = ok_next;
-    __syncthreads();
-    if (it + 1 < nit) ok_next = fetch(it + 1);
+  // Iteration it on LDS buffer buf (okm: valid blocks of the iteration).
+  auto compute = [&](int it, int buf, uint32_t okm) __attribute__((always_inline)) {
     // keys of this iteration that some row of this wave may attend to
     const int kfirst = it * KB * kBS;
-    if (!active || kfirst > wlast) continue;
+    if (!active || kfirst > wlast) return;
 
     // ---- S^T = K Q^T for the KB * 16 keys ----
     float s[KB][4];
@@ -268,30 +270,83 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
       for (int r = 0; r < 4; ++r) o[c][r] *= alpha;
 
     // ---- O^T += V^T P^T ----
+    if constexpr (KB % 2 == 0) {
+      // Two key blocks per v_mfma_f32_16x16x32_bf16: k-slot 8 grp + e holds
+      // key 4 grp + e of the first block (e < 4) or of the second (e >= 4),
+      // which is where this lane's P^T values are; V^T is read with the same
+      // key order.
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      uint2 ph, pl;
-      split2(s[kb][0], s[kb][1], ph.x, pl.x);
-      split2(s[kb][2], s[kb][3], ph.y, pl.y);
-      const uint16_t* vr0 = &s_vt[buf][0][(kb * D + r16) * VP + 4 * grp];
+      for (int kb = 0; kb < KB; kb += 2) {
+        uint4 ph, pl;
+        split2(s[kb][0], s[kb][1], ph.x, pl.x);
+        split2(s[kb][2], s[kb][3], ph.y, pl.y);
+        split2(s[kb + 1][0], s[kb + 1][1], ph.z, pl.z);
+        split2(s[kb + 1][2], s[kb + 1][3], ph.w, pl.w);
+        const uint16_t* va0 = &s_vt[buf][0][(kb * D + r16) * VP + 4 * grp];
+        const uint16_t* va1 = va0 + D * VP;  // the next block's V^T
 #pragma unroll
-      for (int c = 0; c < NO; ++c) {
-        const uint2 va = *reinterpret_cast<const uint2*>(vr0 + 16 * c * VP);
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
-                                                        __builtin_bit_cast(bf16x4_t, ph), o[c],
-                                                        0, 0, 0);
-        o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
-                                                        __builtin_bit_cast(bf16x4_t, pl), o[c],
-                                                        0, 0, 0);
-        if constexpr (F32) {
-          const uint2 vl =
-              *reinterpret_cast<const uint2*>(vr0 + KB * D * VP + 16 * c * VP);
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, vl),
+        for (int c = 0; c < NO; ++c) {
+          const uint2 a0 = *reinterpret_cast<const uint2*>(va0 + 16 * c * VP);
+          const uint2 a1 = *reinterpret_cast<const uint2*>(va1 + 16 * c * VP);
+          const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va),
+                                                         __builtin_bit_cast(bf16x8_t, ph), o[c],
+                                                         0, 0, 0);
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va),
+                                                         __builtin_bit_cast(bf16x8_t, pl), o[c],
+                                                         0, 0, 0);
+          if constexpr (F32) {
+            const uint2 l0 =
+                *reinterpret_cast<const uint2*>(va0 + KB * D * VP + 16 * c * VP);
+            const uint2 l1 =
+                *reinterpret_cast<const uint2*>(va1 + KB * D * VP + 16 * c * VP);
+            const uint4 vl = make_uint4(l0.x, l0.y, l1.x, l1.y);
+            o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vl),
+                                                           __builtin_bit_cast(bf16x8_t, ph),
+                                                           o[c], 0, 0, 0);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        uint2 ph, pl;
+        split2(s[kb][0], s[kb][1], ph.x, pl.x);
+        split2(s[kb][2], s[kb][3], ph.y, pl.y);
+        const uint16_t* vr0 = &s_vt[buf][0][(kb * D + r16) * VP + 4 * grp];
+#pragma unroll
+        for (int c = 0; c < NO; ++c) {
+          const uint2 va = *reinterpret_cast<const uint2*>(vr0 + 16 * c * VP);
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
                                                           __builtin_bit_cast(bf16x4_t, ph), o[c],
                                                           0, 0, 0);
+          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
+                                                          __builtin_bit_cast(bf16x4_t, pl), o[c],
+                                                          0, 0, 0);
+          if constexpr (F32) {
+            const uint2 vl =
+                *reinterpret_cast<const uint2*>(vr0 + KB * D * VP + 16 * c * VP);
+            o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, vl),
+                                                            __builtin_bit_cast(bf16x4_t, ph),
+                                                            o[c], 0, 0, 0);
+          }
         }
       }
     }
+    };
+
+  for (int it = 0; it < nit; it += 2) {
+    stage(0, kr0, vr0);
+    const uint32_t okA = ok0;
+    __syncthreads();
+    if (it + 2 < nit) ok0 = fetch(it + 2, kr0, vr0);
+    compute(it, 0, okA);
+    if (it + 1 >= nit) break;
+    stage(1, kr1, vr1);
+    const uint32_t okB = ok1;
+    __syncthreads();
+    if (it + 3 < nit) ok1 = fetch(it + 3, kr1, vr1);
+    compute(it + 1, 1, okB);
   }
 
   if (!row_ok) return;
