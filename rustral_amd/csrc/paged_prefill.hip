@@ -41,11 +41,19 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBS = 16;  // tokens per block = keys per staged block
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+
+// Two floats to packed bf16 (a in the low half), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
+
 // hi = bf16(x), lo = bf16(x - hi), packed in pairs (element 2i in the low half).
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const uint32_t ha = bf16_rne(a), hb = bf16_rne(b);
-  hi = ha | (hb << 16);
-  lo = bf16_rne(a - __uint_as_float(ha << 16)) | (bf16_rne(b - __uint_as_float(hb << 16)) << 16);
+  hi = cvt_bf16x2(a, b);
+  lo = cvt_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 
 template <typename T, int D, int G, int QS, int KB>
@@ -185,7 +193,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
   uint32_t ok0 = nit > 0 ? fetch(0, kr0, vr0) : 0u;
   uint32_t ok1 = nit > 1 ? fetch(1, kr1, vr1) : 0u;
 
-  // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8], hi and lo.
+  // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8] * q_scale, hi
+  // and lo (scores come out already scaled by scale * log2 e).
   uint4 qhi[NC], qlo[NC];
   {
     const float* qp = q + ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h) * D + 8 * grp;
@@ -194,6 +203,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
       float4 x = reinterpret_cast<const float4*>(qp + 32 * c)[0];
       float4 y = reinterpret_cast<const float4*>(qp + 32 * c)[1];
       if (!row_ok) x = y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      x.x *= q_scale; x.y *= q_scale; x.z *= q_scale; x.w *= q_scale;
+      y.x *= q_scale; y.y *= q_scale; y.z *= q_scale; y.w *= q_scale;
       split2(x.x, x.y, qhi[c].x, qlo[c].x);
       split2(x.z, x.w, qhi[c].y, qlo[c].y);
       split2(y.x, y.y, qhi[c].z, qlo[c].z);
@@ -211,6 +222,9 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
     // keys of this iteration that some row of this wave may attend to
     const int kfirst = it * KB * kBS;
     if (!active || kfirst > wlast) return;
+    // every key of the iteration is valid and at or before the wave's first
+    // query (wave-uniform): nothing to mask
+    const bool full = okm == (1u << KB) - 1u && kfirst + KB * kBS - 1 <= pos0 + qr0;
 
     // ---- S^T = K Q^T for the KB * 16 keys ----
     float s[KB][4];
@@ -235,12 +249,13 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
                                                        0, 0, 0);
         }
       }
-      // causal mask: key position > query position is excluded
+      // causal mask: key 4 grp + r of the block is kept when r <= lim.  A
+      // select, not a branch: the MFMA result is read in the block that
+      // computes it.
       const int kp0 = kfirst + kb * kBS + 4 * grp;
-      const bool bok = (okm >> kb) & 1u;
+      const int lim = full ? 3 : ((okm >> kb) & 1u) && row_ok ? qpos - kp0 : -1;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        s[kb][r] = (bok && row_ok && kp0 + r <= qpos) ? st[r] * q_scale : -INFINITY;
+      for (int r = 0; r < 4; ++r) s[kb][r] = r <= lim ? st[r] : -INFINITY;
     }
     // ---- online softmax of row r16 ----
     float mb = -INFINITY;
@@ -251,23 +266,29 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
     mb = fmaxf(mb, __shfl_xor(mb, 32));
     const float mn = fmaxf(m, mb);
     const float mref = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = exp2f(m - mref);
     float ls = 0.0f;
+    // v_exp_f32 directly: exp2(-inf) = 0, results below 2^-126 do not matter
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        s[kb][r] = exp2f(s[kb][r] - mref);
+        s[kb][r] = __builtin_amdgcn_exp2f(s[kb][r] - mref);
         ls += s[kb][r];
       }
     ls += __shfl_xor(ls, 16);
     ls += __shfl_xor(ls, 32);
-    l = l * alpha + ls;
+    // Rescale only when some row's maximum rose (wave-uniform); otherwise
+    // alpha is exactly 1 (or the row has seen no key yet and o = l = 0).
+    if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
+      const float alpha = __builtin_amdgcn_exp2f(m - mref);
+      l *= alpha;
+#pragma unroll
+      for (int c = 0; c < NO; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[c][r] *= alpha;
+    }
+    l += ls;
     m = mn;
-#pragma unroll
-    for (int c = 0; c < NO; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[c][r] *= alpha;
 
     // ---- O^T += V^T P^T ----
     if constexpr (KB % 2 == 0) {
