@@ -18,7 +18,8 @@
 //     significant bits of q).  Result: lane l holds S^T[key 4(l/16)+r][row
 //     l%16] -- every value a lane holds belongs to query row l % 16.
 //   * causal mask (key position > query position -> excluded), then an
-//     online softmax per row: running max m and sum l, the accumulator
+//     online softmax per row (reductions over the row's four lanes by
+//     permlane swaps): running max m and sum l, the accumulator
 //     rescaled by 2^(m_old - m_new).  Scores carry scale * log2(e) (exp2).
 //   * O^T += V^T P^T on v_mfma_f32_16x16x32_bf16 over two key blocks at a
 //     time (16x16x16 for an odd KB): A = V^T from LDS, B = P^T, which is
@@ -48,6 +49,23 @@ typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 // v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
+
+// x combined with x of lane l ^ 16, then of lane l ^ 32, through
+// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Called with
+// the same value twice, a swap returns the pair (x[l], x[l^16]) in some order,
+// so the sum or maximum equals that of a __shfl_xor exchange bit for bit.
+__device__ __forceinline__ float xor48_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor48_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // hi = bf16(x), lo = bf16(x - hi), packed in pairs (element 2i in the low half).
@@ -262,8 +280,7 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
       mb = fmaxf(mb, fmaxf(fmaxf(s[kb][0], s[kb][1]), fmaxf(s[kb][2], s[kb][3])));
-    mb = fmaxf(mb, __shfl_xor(mb, 16));
-    mb = fmaxf(mb, __shfl_xor(mb, 32));
+    mb = xor48_max(mb);
     const float mn = fmaxf(m, mb);
     const float mref = mn == -INFINITY ? 0.0f : mn;
     float ls = 0.0f;
@@ -275,8 +292,7 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
         s[kb][r] = __builtin_amdgcn_exp2f(s[kb][r] - mref);
         ls += s[kb][r];
       }
-    ls += __shfl_xor(ls, 16);
-    ls += __shfl_xor(ls, 32);
+    ls = xor48_sum(ls);
     // Rescale only when some row's maximum rose (wave-uniform); otherwise
     // alpha is exactly 1 (or the row has seen no key yet and o = l = 0).
     if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
