@@ -8,9 +8,9 @@
 // sub-tile, so each K/V byte staged in LDS serves G heads x QS sub-tiles.
 // The workgroup walks the 16-token blocks, KB per iteration, from position 0
 // to the tile's last query position:
-//   * stage: the KB blocks' K tiles (row-major, rows padded) and V tiles
-//     (stored transposed, V^T[dim][key]) go through registers into LDS,
-//     double buffered; the loads run two iterations ahead of the compute.
+//   * stage: the KB blocks' K and V tiles go through registers into LDS,
+//     row-major with padded rows, double buffered; the loads run two
+//     iterations ahead of the compute.
 //     A wave skips the arithmetic of key blocks that lie entirely after its
 //     last query (causal).
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = K rows from LDS, B = Q^T
@@ -22,7 +22,8 @@
 //     permlane swaps): running max m and sum l, the accumulator
 //     rescaled by 2^(m_old - m_new).  Scores carry scale * log2(e) (exp2).
 //   * O^T += V^T P^T on v_mfma_f32_16x16x32_bf16 over two key blocks at a
-//     time (16x16x16 for an odd KB): A = V^T from LDS, B = P^T, which is
+//     time (16x16x16 for an odd KB): A = V^T, read from the row-major V tile
+//     by ds_read_b64_tr_b16 (a transposing LDS read), B = P^T, which is
 //     exactly the S^T layout above (no cross-lane moves); P is split hi + lo
 //     like q.  Result: lane l holds O^T[dim 16c + 4(l/16)+r][row l%16].
 // fp32 pools split K and V into hi + lo bf16 as well (three products each).
@@ -38,6 +39,7 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) short bf16x4_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) short i16x4_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBS = 16;  // tokens per block = keys per staged block
@@ -68,6 +70,17 @@ __device__ __forceinline__ float xor48_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane i receives
+// as element j (j < 4) the 16-bit element i & 3 of the 8 bytes addressed by
+// lane 4 j + (i >> 2).  So when lane i of group g addresses row 4 g + (i >> 2),
+// columns c0 + 4 (i & 3) .. + 3 of a row-major tile, it receives column c0 + i
+// of rows 4 g .. 4 g + 3: four keys of one dim of a row-major V tile.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+  return __builtin_bit_cast(
+      uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)const_cast<uint16_t*>(p)));
+}
+
 // hi = bf16(x), lo = bf16(x - hi), packed in pairs (element 2i in the low half).
 __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
   hi = cvt_bf16x2(a, b);
@@ -86,8 +99,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
   constexpr int QT = 16 * QS;              // query tokens per workgroup
   constexpr int NS = F32 ? 2 : 1;          // bf16 slices per staged element (hi, lo)
   constexpr int KP = D + 8;                // padded K row in LDS (bf16 elements)
-  constexpr int VP = kBS + 4;              // padded V^T row (keys of one dim): spreads
-                                           // the transposing 2-byte stores over banks
+  constexpr int VKP = D + 16;              // padded V row: the 4 rows of one transposing
+                                           // read (8 bytes x 16 lanes) hit distinct banks
   constexpr int CE = 16 / sizeof(T);       // elements per 16-byte chunk
   constexpr int CPR = D / CE;              // chunks per token row
   constexpr int CH = kBS * CPR;            // chunks per (block, head) tile
@@ -95,7 +108,7 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
   constexpr int NC = D / 32;               // QK^T MFMAs per key block (per slice)
   constexpr int NO = D / 16;               // PV MFMAs per key block (per slice)
   __shared__ __align__(16) uint16_t s_k[2][NS][KB * kBS * KP];
-  __shared__ __align__(16) uint16_t s_vt[2][NS][KB * D * VP];
+  __shared__ __align__(16) uint16_t s_v[2][NS][KB * kBS * VKP];
 
   const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
   const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
@@ -170,7 +183,7 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
     }
     return okm;
   };
-  // Writes the registers into LDS buffer buf: K row-major, V transposed.
+  // Writes the registers into LDS buffer buf (K and V row-major).
   auto stage = [&](int buf, const uint4 (&kr)[PT], const uint4 (&vr)[PT])
                    __attribute__((always_inline)) {
 #pragma unroll
@@ -180,14 +193,12 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
         const int kb = ci / CH, cc = ci % CH;
         const int key = cc / CPR, col = (cc % CPR) * CE;
         uint16_t* kd = &s_k[buf][0][(kb * kBS + key) * KP + col];
-        uint16_t* vd = &s_vt[buf][0][(kb * D + col) * VP + key];
+        uint16_t* vd = &s_v[buf][0][(kb * kBS + key) * VKP + col];
         if constexpr (!F32) {
           *reinterpret_cast<uint4*>(kd) = kr[i];
-          const uint32_t wv[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vd[e * VP] = (uint16_t)(wv[e >> 1] >> (16 * (e & 1)));
+          *reinterpret_cast<uint4*>(vd) = vr[i];
         } else {
-          constexpr int KS = KB * kBS * KP, VS = KB * D * VP;  // slice strides
+          constexpr int KS = KB * kBS * KP, VS = KB * kBS * VKP;  // slice strides
           const float kf[4] = {__uint_as_float(kr[i].x), __uint_as_float(kr[i].y),
                                __uint_as_float(kr[i].z), __uint_as_float(kr[i].w)};
           const float vf[4] = {__uint_as_float(vr[i].x), __uint_as_float(vr[i].y),
@@ -197,12 +208,11 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
           split2(kf[2], kf[3], kh2.y, kl2.y);
           *reinterpret_cast<uint2*>(kd) = kh2;
           *reinterpret_cast<uint2*>(kd + KS) = kl2;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t hv = bf16_rne(vf[e]);
-            vd[e * VP] = (uint16_t)hv;
-            vd[e * VP + VS] = (uint16_t)bf16_rne(vf[e] - __uint_as_float(hv << 16));
-          }
+          uint2 vh2, vl2;
+          split2(vf[0], vf[1], vh2.x, vl2.x);
+          split2(vf[2], vf[3], vh2.y, vl2.y);
+          *reinterpret_cast<uint2*>(vd) = vh2;
+          *reinterpret_cast<uint2*>(vd + VS) = vl2;
         }
       }
     }
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
       // Two key blocks per v_mfma_f32_16x16x32_bf16: k-slot 8 grp + e holds
       // key 4 grp + e of the first block (e < 4) or of the second (e >= 4),
       // which is where this lane's P^T values are; V^T is read with the same
-      // key order.
+      // key order (one transposing read per block).
 #pragma unroll
       for (int kb = 0; kb < KB; kb += 2) {
         uint4 ph, pl;
@@ -319,12 +329,14 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
         split2(s[kb][2], s[kb][3], ph.y, pl.y);
         split2(s[kb + 1][0], s[kb + 1][1], ph.z, pl.z);
         split2(s[kb + 1][2], s[kb + 1][3], ph.w, pl.w);
-        const uint16_t* va0 = &s_vt[buf][0][(kb * D + r16) * VP + 4 * grp];
-        const uint16_t* va1 = va0 + D * VP;  // the next block's V^T
+        // this lane's transposing-read address: key 4 grp + (r16 >> 2),
+        // dims 16 c + 4 (r16 & 3) .. + 3
+        const uint16_t* va0 = &s_v[buf][0][(kb * kBS + 4 * grp + (r16 >> 2)) * VKP + 4 * (r16 & 3)];
+        const uint16_t* va1 = va0 + kBS * VKP;  // the next block
 #pragma unroll
         for (int c = 0; c < NO; ++c) {
-          const uint2 a0 = *reinterpret_cast<const uint2*>(va0 + 16 * c * VP);
-          const uint2 a1 = *reinterpret_cast<const uint2*>(va1 + 16 * c * VP);
+          const uint2 a0 = lds_read_tr16(va0 + 16 * c);
+          const uint2 a1 = lds_read_tr16(va1 + 16 * c);
           const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
           o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va),
                                                          __builtin_bit_cast(bf16x8_t, ph), o[c],
@@ -333,10 +345,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
                                                          __builtin_bit_cast(bf16x8_t, pl), o[c],
                                                          0, 0, 0);
           if constexpr (F32) {
-            const uint2 l0 =
-                *reinterpret_cast<const uint2*>(va0 + KB * D * VP + 16 * c * VP);
-            const uint2 l1 =
-                *reinterpret_cast<const uint2*>(va1 + KB * D * VP + 16 * c * VP);
+            const uint2 l0 = lds_read_tr16(va0 + KB * kBS * VKP + 16 * c);
+            const uint2 l1 = lds_read_tr16(va1 + KB * kBS * VKP + 16 * c);
             const uint4 vl = make_uint4(l0.x, l0.y, l1.x, l1.y);
             o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vl),
                                                            __builtin_bit_cast(bf16x8_t, ph),
@@ -350,10 +360,10 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
         uint2 ph, pl;
         split2(s[kb][0], s[kb][1], ph.x, pl.x);
         split2(s[kb][2], s[kb][3], ph.y, pl.y);
-        const uint16_t* vr0 = &s_vt[buf][0][(kb * D + r16) * VP + 4 * grp];
+        const uint16_t* vr0 = &s_v[buf][0][(kb * kBS + 4 * grp + (r16 >> 2)) * VKP + 4 * (r16 & 3)];
 #pragma unroll
         for (int c = 0; c < NO; ++c) {
-          const uint2 va = *reinterpret_cast<const uint2*>(vr0 + 16 * c * VP);
+          const uint2 va = lds_read_tr16(vr0 + 16 * c);
           o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
                                                           __builtin_bit_cast(bf16x4_t, ph), o[c],
                                                           0, 0, 0);
@@ -361,8 +371,7 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
                                                           __builtin_bit_cast(bf16x4_t, pl), o[c],
                                                           0, 0, 0);
           if constexpr (F32) {
-            const uint2 vl =
-                *reinterpret_cast<const uint2*>(vr0 + KB * D * VP + 16 * c * VP);
+            const uint2 vl = lds_read_tr16(vr0 + KB * kBS * VKP + 16 * c);
             o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, vl),
                                                             __builtin_bit_cast(bf16x4_t, ph),
                                                             o[c], 0, 0, 0);
