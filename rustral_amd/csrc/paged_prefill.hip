@@ -3,9 +3,11 @@
 // cached tokens and to each other (causal), reading K/V through the block
 // table.  The new tokens' K/V are appended to the pool first (rkv_append).
 //
-// One workgroup per (tile of 16 * QS query tokens, KV head, sequence), G * QS
-// waves: wave (g, t) serves query head kh * G + g for the t-th 16-token
-// sub-tile, so each K/V byte staged in LDS serves G heads x QS sub-tiles.
+// One workgroup per (tile of 16 * QS query tokens, KV head, sequence),
+// (G / HW) * QS waves: wave (g, t) serves the HW query heads kh * G + HW g ..
+// for the t-th 16-token sub-tile, so each K/V byte staged in LDS serves G
+// heads x QS sub-tiles, and each K/V fragment a wave reads from LDS feeds the
+// MFMAs of HW heads (two independent dependency chains per wave for HW = 2).
 // The workgroup walks the 16-token blocks, KB per iteration, from position 0
 // to the tile's last query position:
 //   * stage: the KB blocks' K and V tiles go through registers into LDS,
@@ -32,6 +34,7 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace rkv {
 namespace {
@@ -57,11 +60,17 @@ __device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
 // v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Called with
 // the same value twice, a swap returns the pair (x[l], x[l^16]) in some order,
 // so the sum or maximum equals that of a __shfl_xor exchange bit for bit.
+// max(a, b) as v_med3_f32(a, b, +inf): one instruction, without the
+// quieting copies fmaxf gets in IEEE mode (the values here are never NaN).
+__device__ __forceinline__ float max2(float a, float b) {
+  return __builtin_amdgcn_fmed3f(a, b, INFINITY);
+}
+
 __device__ __forceinline__ float xor48_max(float x) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  x = max2(__uint_as_float(r[0]), __uint_as_float(r[1]));
   r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor48_sum(float x) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -87,15 +96,16 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
   lo = cvt_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 
-template <typename T, int D, int G, int QS, int KB>
-__global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
+template <typename T, int D, int G, int HW, int QS, int KB>
+__global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     float* __restrict__ out, const float* __restrict__ q, const void* __restrict__ k_pool_,
     const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ q_start,
     const int32_t* __restrict__ ctx_lens, int num_kv_heads, int64_t num_blocks, int max_q_len,
     float q_scale) {
   constexpr bool F32 = sizeof(T) == 4;
-  constexpr int NT = 64 * G * QS;
+  static_assert(G % HW == 0, "heads per wave must divide the group");
+  constexpr int NT = 64 * (G / HW) * QS;
   constexpr int QT = 16 * QS;              // query tokens per workgroup
   constexpr int NS = F32 ? 2 : 1;          // bf16 slices per staged element (hi, lo)
   constexpr int KP = D + 8;                // padded K row in LDS (bf16 elements)
@@ -115,8 +125,8 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
   const int qt = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = w % G, rt = w / G;  // query head within the group, row sub-tile
-  const int num_q_heads = num_kv_heads * G, h = kh * G + g;
+  const int g = w % (G / HW), rt = w / (G / HW);  // head set within the group, row sub-tile
+  const int num_q_heads = num_kv_heads * G, h0 = kh * G + g * HW;  // the wave's first head
 
   const int s0 = q_start[b];
   const int n = q_start[b + 1] - s0;
@@ -223,9 +233,11 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
 
   // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8] * q_scale, hi
   // and lo (scores come out already scaled by scale * log2 e).
-  uint4 qhi[NC], qlo[NC];
-  {
-    const float* qp = q + ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h) * D + 8 * grp;
+  uint4 qhi[HW][NC], qlo[HW][NC];
+#pragma unroll
+  for (int hh = 0; hh < HW; ++hh) {
+    const float* qp =
+        q + ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h0 + hh) * D + 8 * grp;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       float4 x = reinterpret_cast<const float4*>(qp + 32 * c)[0];
@@ -233,88 +245,121 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
       if (!row_ok) x = y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       x.x *= q_scale; x.y *= q_scale; x.z *= q_scale; x.w *= q_scale;
       y.x *= q_scale; y.y *= q_scale; y.z *= q_scale; y.w *= q_scale;
-      split2(x.x, x.y, qhi[c].x, qlo[c].x);
-      split2(x.z, x.w, qhi[c].y, qlo[c].y);
-      split2(y.x, y.y, qhi[c].z, qlo[c].z);
-      split2(y.z, y.w, qhi[c].w, qlo[c].w);
+      split2(x.x, x.y, qhi[hh][c].x, qlo[hh][c].x);
+      split2(x.z, x.w, qhi[hh][c].y, qlo[hh][c].y);
+      split2(y.x, y.y, qhi[hh][c].z, qlo[hh][c].z);
+      split2(y.z, y.w, qhi[hh][c].w, qlo[hh][c].w);
     }
   }
 
-  f32x4_t o[NO];
+  f32x4_t o[HW][NO];
+  float m[HW], l[HW];
 #pragma unroll
-  for (int c = 0; c < NO; ++c) o[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m = -INFINITY, l = 0.0f;
+  for (int hh = 0; hh < HW; ++hh) {
+#pragma unroll
+    for (int c = 0; c < NO; ++c) o[hh][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    m[hh] = -INFINITY;
+    l[hh] = 0.0f;
+  }
 
   // Iteration it on LDS buffer buf (okm: valid blocks of the iteration).
-  auto compute = [&](int it, int buf, uint32_t okm) __attribute__((always_inline)) {
-    // keys of this iteration that some row of this wave may attend to
+  // MASKED: some key of the iteration is invalid or after some query of the
+  // wave (the choice is made before any MFMA, so the MFMA results are read
+  // in the block that computes them).
+  auto compute = [&](auto masked, int it, int buf, uint32_t okm) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked)::value;
     const int kfirst = it * KB * kBS;
-    if (!active || kfirst > wlast) return;
-    // every key of the iteration is valid and at or before the wave's first
-    // query (wave-uniform): nothing to mask
-    const bool full = okm == (1u << KB) - 1u && kfirst + KB * kBS - 1 <= pos0 + qr0;
 
-    // ---- S^T = K Q^T for the KB * 16 keys ----
-    float s[KB][4];
+    // ---- S^T = K Q^T for the KB * 16 keys, per head ----
+    float s[HW][KB][4];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      f32x4_t st = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4_t st[HW];
+#pragma unroll
+      for (int hh = 0; hh < HW; ++hh) st[hh] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
       const uint16_t* kr0 = &s_k[buf][0][(kb * kBS + r16) * KP + 8 * grp];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const uint4 ka = *reinterpret_cast<const uint4*>(kr0 + 32 * c);
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka),
-                                                     __builtin_bit_cast(bf16x8_t, qhi[c]), st,
-                                                     0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka),
-                                                     __builtin_bit_cast(bf16x8_t, qlo[c]), st,
-                                                     0, 0, 0);
+#pragma unroll
+        for (int hh = 0; hh < HW; ++hh)
+          st[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, ka), __builtin_bit_cast(bf16x8_t, qhi[hh][c]), st[hh],
+              0, 0, 0);
+#pragma unroll
+        for (int hh = 0; hh < HW; ++hh)
+          st[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, ka), __builtin_bit_cast(bf16x8_t, qlo[hh][c]), st[hh],
+              0, 0, 0);
         if constexpr (F32) {
           const uint4 kl =
               *reinterpret_cast<const uint4*>(kr0 + KB * kBS * KP + 32 * c);
-          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kl),
-                                                       __builtin_bit_cast(bf16x8_t, qhi[c]), st,
-                                                       0, 0, 0);
+#pragma unroll
+          for (int hh = 0; hh < HW; ++hh)
+            st[hh] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, kl), __builtin_bit_cast(bf16x8_t, qhi[hh][c]),
+                st[hh], 0, 0, 0);
         }
       }
-      // causal mask: key 4 grp + r of the block is kept when r <= lim.  A
-      // select, not a branch: the MFMA result is read in the block that
-      // computes it.
-      const int kp0 = kfirst + kb * kBS + 4 * grp;
-      const int lim = full ? 3 : ((okm >> kb) & 1u) && row_ok ? qpos - kp0 : -1;
+      if constexpr (MASKED) {
+        // causal mask: key 4 grp + r of the block is kept when r <= lim
+        const int kp0 = kfirst + kb * kBS + 4 * grp;
+        const int lim = ((okm >> kb) & 1u) && row_ok ? qpos - kp0 : -1;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[kb][r] = r <= lim ? st[r] : -INFINITY;
-    }
-    // ---- online softmax of row r16 ----
-    float mb = -INFINITY;
+        for (int hh = 0; hh < HW; ++hh)
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-      mb = fmaxf(mb, fmaxf(fmaxf(s[kb][0], s[kb][1]), fmaxf(s[kb][2], s[kb][3])));
-    mb = xor48_max(mb);
-    const float mn = fmaxf(m, mb);
-    const float mref = mn == -INFINITY ? 0.0f : mn;
-    float ls = 0.0f;
-    // v_exp_f32 directly: exp2(-inf) = 0, results below 2^-126 do not matter
+          for (int r = 0; r < 4; ++r) s[hh][kb][r] = r <= lim ? st[hh][r] : -INFINITY;
+      } else {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+        for (int hh = 0; hh < HW; ++hh)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s[kb][r] = __builtin_amdgcn_exp2f(s[kb][r] - mref);
-        ls += s[kb][r];
+          for (int r = 0; r < 4; ++r) s[hh][kb][r] = st[hh][r];
       }
-    ls = xor48_sum(ls);
-    // Rescale only when some row's maximum rose (wave-uniform); otherwise
-    // alpha is exactly 1 (or the row has seen no key yet and o = l = 0).
-    if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {
-      const float alpha = __builtin_amdgcn_exp2f(m - mref);
-      l *= alpha;
-#pragma unroll
-      for (int c = 0; c < NO; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[c][r] *= alpha;
     }
-    l += ls;
-    m = mn;
+    // ---- online softmax of row r16, per head ----
+    // The reference maximum m moves only when a row's maximum exceeds it by
+    // more than kSlack (log2 units, a factor 2^8): exponentials stay <= 2^8,
+    // exact in fp32 and split hi + lo as before, and the rare rescale of the
+    // accumulators is one wave-uniform branch for all heads of the wave.
+    constexpr float kSlack = 8.0f;
+    float mn[HW];
+    bool up = false;
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) {
+      float mb = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+        mb = max2(mb, max2(max2(s[hh][kb][0], s[hh][kb][1]), max2(s[hh][kb][2], s[hh][kb][3])));
+      mn[hh] = max2(m[hh], xor48_max(mb));
+      up = up || mn[hh] > m[hh] + kSlack;  // -inf + 8 = -inf: the first key always moves m
+    }
+    if (__builtin_amdgcn_ballot_w64(up) != 0) {
+#pragma unroll
+      for (int hh = 0; hh < HW; ++hh) {
+        // rows without any key so far (m = -inf) get alpha = 0 on o = l = 0
+        const float alpha = __builtin_amdgcn_exp2f(m[hh] - (mn[hh] == -INFINITY ? 0.0f : mn[hh]));
+        l[hh] *= alpha;
+#pragma unroll
+        for (int c = 0; c < NO; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[hh][c][r] *= alpha;
+        m[hh] = mn[hh];
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) {
+      const float mref = m[hh] == -INFINITY ? 0.0f : m[hh];
+      float ls = 0.0f;
+      // v_exp_f32 directly: exp2(-inf) = 0, results below 2^-126 do not matter
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[hh][kb][r] = __builtin_amdgcn_exp2f(s[hh][kb][r] - mref);
+          ls += s[hh][kb][r];
+        }
+      l[hh] += xor48_sum(ls);
+    }
 
     // ---- O^T += V^T P^T ----
     if constexpr (KB % 2 == 0) {
@@ -324,11 +369,14 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
       // key order (one transposing read per block).
 #pragma unroll
       for (int kb = 0; kb < KB; kb += 2) {
-        uint4 ph, pl;
-        split2(s[kb][0], s[kb][1], ph.x, pl.x);
-        split2(s[kb][2], s[kb][3], ph.y, pl.y);
-        split2(s[kb + 1][0], s[kb + 1][1], ph.z, pl.z);
-        split2(s[kb + 1][2], s[kb + 1][3], ph.w, pl.w);
+        uint4 ph[HW], pl[HW];
+#pragma unroll
+        for (int hh = 0; hh < HW; ++hh) {
+          split2(s[hh][kb][0], s[hh][kb][1], ph[hh].x, pl[hh].x);
+          split2(s[hh][kb][2], s[hh][kb][3], ph[hh].y, pl[hh].y);
+          split2(s[hh][kb + 1][0], s[hh][kb + 1][1], ph[hh].z, pl[hh].z);
+          split2(s[hh][kb + 1][2], s[hh][kb + 1][3], ph[hh].w, pl[hh].w);
+        }
         // this lane's transposing-read address: key 4 grp + (r16 >> 2),
         // dims 16 c + 4 (r16 & 3) .. + 3
         const uint16_t* va0 = &s_v[buf][0][(kb * kBS + 4 * grp + (r16 >> 2)) * VKP + 4 * (r16 & 3)];
@@ -338,104 +386,162 @@ __global__ __launch_bounds__(64 * G * QS) void prefill_kernel(
           const uint2 a0 = lds_read_tr16(va0 + 16 * c);
           const uint2 a1 = lds_read_tr16(va1 + 16 * c);
           const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va),
-                                                         __builtin_bit_cast(bf16x8_t, ph), o[c],
-                                                         0, 0, 0);
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, va),
-                                                         __builtin_bit_cast(bf16x8_t, pl), o[c],
-                                                         0, 0, 0);
+#pragma unroll
+          for (int hh = 0; hh < HW; ++hh)
+            o[hh][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, va), __builtin_bit_cast(bf16x8_t, ph[hh]), o[hh][c],
+                0, 0, 0);
+#pragma unroll
+          for (int hh = 0; hh < HW; ++hh)
+            o[hh][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, va), __builtin_bit_cast(bf16x8_t, pl[hh]), o[hh][c],
+                0, 0, 0);
           if constexpr (F32) {
             const uint2 l0 = lds_read_tr16(va0 + KB * kBS * VKP + 16 * c);
             const uint2 l1 = lds_read_tr16(va1 + KB * kBS * VKP + 16 * c);
             const uint4 vl = make_uint4(l0.x, l0.y, l1.x, l1.y);
-            o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vl),
-                                                           __builtin_bit_cast(bf16x8_t, ph),
-                                                           o[c], 0, 0, 0);
+#pragma unroll
+            for (int hh = 0; hh < HW; ++hh)
+              o[hh][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bf16x8_t, vl), __builtin_bit_cast(bf16x8_t, ph[hh]),
+                  o[hh][c], 0, 0, 0);
           }
         }
       }
     } else {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        uint2 ph, pl;
-        split2(s[kb][0], s[kb][1], ph.x, pl.x);
-        split2(s[kb][2], s[kb][3], ph.y, pl.y);
+        uint2 ph[HW], pl[HW];
+#pragma unroll
+        for (int hh = 0; hh < HW; ++hh) {
+          split2(s[hh][kb][0], s[hh][kb][1], ph[hh].x, pl[hh].x);
+          split2(s[hh][kb][2], s[hh][kb][3], ph[hh].y, pl[hh].y);
+        }
         const uint16_t* vr0 = &s_v[buf][0][(kb * kBS + 4 * grp + (r16 >> 2)) * VKP + 4 * (r16 & 3)];
 #pragma unroll
         for (int c = 0; c < NO; ++c) {
           const uint2 va = lds_read_tr16(vr0 + 16 * c);
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
-                                                          __builtin_bit_cast(bf16x4_t, ph), o[c],
-                                                          0, 0, 0);
-          o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, va),
-                                                          __builtin_bit_cast(bf16x4_t, pl), o[c],
-                                                          0, 0, 0);
+#pragma unroll
+          for (int hh = 0; hh < HW; ++hh) {
+            o[hh][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                __builtin_bit_cast(bf16x4_t, va), __builtin_bit_cast(bf16x4_t, ph[hh]), o[hh][c],
+                0, 0, 0);
+            o[hh][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                __builtin_bit_cast(bf16x4_t, va), __builtin_bit_cast(bf16x4_t, pl[hh]), o[hh][c],
+                0, 0, 0);
+          }
           if constexpr (F32) {
             const uint2 vl = lds_read_tr16(vr0 + KB * kBS * VKP + 16 * c);
-            o[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(bf16x4_t, vl),
-                                                            __builtin_bit_cast(bf16x4_t, ph),
-                                                            o[c], 0, 0, 0);
+#pragma unroll
+            for (int hh = 0; hh < HW; ++hh)
+              o[hh][c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                  __builtin_bit_cast(bf16x4_t, vl), __builtin_bit_cast(bf16x4_t, ph[hh]),
+                  o[hh][c], 0, 0, 0);
           }
         }
       }
     }
     };
-
-  for (int it = 0; it < nit; it += 2) {
+  // Iteration it on buffer buf: skipped when no row of the wave attends to
+  // any of its keys.
+  auto step = [&](auto masked, int it, int buf, uint32_t okm) __attribute__((always_inline)) {
+    if (active && it * KB * kBS <= wlast) compute(masked, it, buf, okm);
+  };
+  // Iterations it and it + 1 (the two LDS buffers); false when it + 1 is past
+  // the end.
+  auto pair = [&](auto masked, int it) __attribute__((always_inline)) {
     stage(0, kr0, vr0);
     const uint32_t okA = ok0;
     __syncthreads();
     if (it + 2 < nit) ok0 = fetch(it + 2, kr0, vr0);
-    compute(it, 0, okA);
-    if (it + 1 >= nit) break;
+    step(masked, it, 0, okA);
+    if (it + 1 >= nit) return false;
     stage(1, kr1, vr1);
     const uint32_t okB = ok1;
     __syncthreads();
     if (it + 3 < nit) ok1 = fetch(it + 3, kr1, vr1);
-    compute(it + 1, 1, okB);
+    step(masked, it + 1, 1, okB);
+    return true;
+  };
+  // First the pairs whose keys are all valid and at or before the wave's
+  // first query (no mask), then the rest with the mask.  The switch point is
+  // per wave (wave-uniform); both loops pass the same barriers, so the waves
+  // of the workgroup stay in step.  Separate loops, not a branch per
+  // iteration, keep the two variants' registers apart.
+  constexpr uint32_t kAllValid = (1u << KB) - 1u;
+  int it = 0;
+  for (; it < nit; it += 2) {
+    const int klast = (it + 2 < nit ? it + 2 : nit) * KB * kBS - 1;  // last key of the pair
+    const bool plain = !active || (ok0 == kAllValid && (it + 1 >= nit || ok1 == kAllValid) &&
+                                   klast <= pos0 + qr0);
+    if (!plain) break;
+    if (!pair(std::false_type{}, it)) break;
   }
+  for (; it < nit; it += 2)
+    if (!pair(std::true_type{}, it)) break;
 
   if (!row_ok) return;
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  float* op = out + ((int64_t)(s0 + qi) * num_q_heads + h) * D + 4 * grp;
 #pragma unroll
-  for (int c = 0; c < NO; ++c)
-    *reinterpret_cast<float4*>(op + 16 * c) =
-        make_float4(o[c][0] * inv, o[c][1] * inv, o[c][2] * inv, o[c][3] * inv);
+  for (int hh = 0; hh < HW; ++hh) {
+    const float inv = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
+    float* op = out + ((int64_t)(s0 + qi) * num_q_heads + h0 + hh) * D + 4 * grp;
+#pragma unroll
+    for (int c = 0; c < NO; ++c)
+      *reinterpret_cast<float4*>(op + 16 * c) = make_float4(
+          o[hh][c][0] * inv, o[hh][c][1] * inv, o[hh][c][2] * inv, o[hh][c][3] * inv);
+  }
 }
 
 using PrefillFn = void (*)(float*, const float*, const void*, const void*, const int32_t*, int,
                            const int32_t*, const int32_t*, int, int64_t, int, float);
 
-// Query row sub-tiles per KV-head group (waves per query head) and key blocks
-// per staged iteration.
-#ifndef RKV_PREFILL_QS
-#define RKV_PREFILL_QS 4
+// Waves per workgroup, query heads per wave (for groups of at least 4 heads)
+// and key blocks per staged iteration.  With 8 waves a workgroup may hold up
+// to 256 VGPRs per lane, which two heads per wave need at D = 128.
+#ifndef RKV_PREFILL_WAVES
+#define RKV_PREFILL_WAVES 8
+#endif
+#ifndef RKV_PREFILL_HW
+#define RKV_PREFILL_HW 2
 #endif
 #ifndef RKV_PREFILL_KB
 #define RKV_PREFILL_KB 2
 #endif
-constexpr int kQS = RKV_PREFILL_QS;
+constexpr int kWaves = RKV_PREFILL_WAVES;
+constexpr int kHW = RKV_PREFILL_HW;
 constexpr int kKB = RKV_PREFILL_KB;
 
+struct PrefillCfg {
+  PrefillFn fn;
+  int waves;   // per workgroup
+  int tile;    // query tokens per workgroup
+};
+
+template <typename T, int D, int G>
+PrefillCfg cfg_g() {
+  constexpr int HW = G >= 4 && G % kHW == 0 ? kHW : 1;
+  constexpr int QS = kWaves / (G / HW) > 0 ? kWaves / (G / HW) : 1;  // row sub-tiles
+  return {&prefill_kernel<T, D, G, HW, QS, kKB>, (G / HW) * QS, 16 * QS};
+}
+
 template <typename T, int D>
-PrefillFn pick_g(int G) {
+PrefillCfg pick_g(int G) {
   switch (G) {
-    case 1: return &prefill_kernel<T, D, 1, kQS, kKB>;
-    case 2: return &prefill_kernel<T, D, 2, kQS, kKB>;
-    case 4: return &prefill_kernel<T, D, 4, kQS, kKB>;
-    case 8: return &prefill_kernel<T, D, 8, kQS * 8 <= 16 ? kQS : 2, kKB>;
-    default: return nullptr;
+    case 1: return cfg_g<T, D, 1>();
+    case 2: return cfg_g<T, D, 2>();
+    case 4: return cfg_g<T, D, 4>();
+    case 8: return cfg_g<T, D, 8>();
+    default: return {nullptr, 0, 0};
   }
 }
 
 template <typename T>
-PrefillFn pick_d(int D, int G) {
+PrefillCfg pick_d(int D, int G) {
   switch (D) {
     case 32: return pick_g<T, 32>(G);
     case 64: return pick_g<T, 64>(G);
     case 128: return pick_g<T, 128>(G);
-    default: return nullptr;
+    default: return {nullptr, 0, 0};
   }
 }
 
@@ -462,8 +568,9 @@ extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_p
   if (block_size != kBS)
     return fail(RKV_ERR_UNSUPPORTED, "rkv_prefill_attention: block_size must be 16");
   const int G = num_q_heads / num_kv_heads;
-  PrefillFn fn = dtype == RKV_BF16 ? pick_d<uint16_t>(head_dim, G) : pick_d<float>(head_dim, G);
-  if (!fn)
+  const PrefillCfg cfg =
+      dtype == RKV_BF16 ? pick_d<uint16_t>(head_dim, G) : pick_d<float>(head_dim, G);
+  if (!cfg.fn)
     return fail(RKV_ERR_UNSUPPORTED,
                 "rkv_prefill_attention: head_dim must be 32, 64 or 128 and num_q_heads / "
                 "num_kv_heads 1, 2, 4 or 8");
@@ -479,11 +586,9 @@ extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_p
   if (!aligned16(out) || !aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG,
                 "rkv_prefill_attention: out, q and pools must be 16-byte aligned");
-  const int qs = G == 8 && kQS * 8 > 16 ? 2 : kQS;  // at most 16 waves per workgroup
-  const int qt = 16 * qs;
-  const dim3 grid((unsigned)((max_q_len + qt - 1) / qt), (unsigned)num_kv_heads,
+  const dim3 grid((unsigned)((max_q_len + cfg.tile - 1) / cfg.tile), (unsigned)num_kv_heads,
                   (unsigned)num_seqs);
-  hipLaunchKernelGGL(fn, grid, dim3(64 * G * qs), 0, static_cast<hipStream_t>(stream), out, q, k_pool,
+  hipLaunchKernelGGL(cfg.fn, grid, dim3(64 * cfg.waves), 0, static_cast<hipStream_t>(stream), out, q, k_pool,
                      v_pool, block_tables, max_blocks_per_seq, q_start, ctx_lens, num_kv_heads,
                      num_blocks, max_q_len, scale * kLog2e);
   return check_launch("rkv_prefill_attention");
