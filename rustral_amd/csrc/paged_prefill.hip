@@ -148,33 +148,30 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   const int qpos = pos0 + qi;
   const int wlast = pos0 + (qr0 + 16 < nr ? qr0 + 16 : nr) - 1;  // this wave's last query position
 
-  const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
-  // Block ids come from a 64-entry window held one per lane (one vector load
-  // per 64 blocks) and are read with readlane, so issuing a block's K/V loads
-  // never waits on a table read.
-  int win = 0;
-  int32_t idv = lane < max_blocks_per_seq ? tab[lane] : -1;
-  auto block_id = [&](int j) __attribute__((always_inline)) {
-    if ((j >> 6) != win) {  // wave-uniform
-      win = j >> 6;
-      const int jj = (win << 6) + lane;
-      idv = jj < max_blocks_per_seq ? tab[jj] : -1;
+  const int32_t* __restrict__ tab = block_tables + (int64_t)b * max_blocks_per_seq;
+  // Block ids are wave-uniform loads (scalar memory, counted apart from the
+  // K/V vector loads), read one iteration before the fetch that uses them,
+  // so the fetch neither waits on the table nor on earlier K/V loads.
+  auto load_ids = [&](int it, int32_t (&id)[KB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int j = it * KB + kb;
+      id[kb] = j < nblk ? tab[j] : -1;
     }
-    return __builtin_amdgcn_readlane(idv, j & 63);
   };
   // Two register sets: the loads of iteration it + 2 are issued while
   // iteration it is computed (one workgroup fills a CU, so its own loads
   // have to be in flight early).
   uint4 kr0[PT], vr0[PT], kr1[PT], vr1[PT];
-  // Issues iteration it's K/V loads (KB blocks) into registers; returns a
-  // bit per block whose id is valid.
-  auto fetch = [&](int it, uint4 (&kr)[PT], uint4 (&vr)[PT]) __attribute__((always_inline)) {
+  // Issues the K/V loads of the KB blocks with ids id into registers;
+  // returns a bit per block whose id is valid.
+  auto fetch = [&](const int32_t (&id)[KB], uint4 (&kr)[PT], uint4 (&vr)[PT])
+                   __attribute__((always_inline)) {
     uint32_t okm = 0;
     int64_t base[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      const int j = it * KB + kb;
-      int32_t blk = j < nblk ? block_id(j) : -1;
+      const int32_t blk = id[kb];
       const bool ok = blk >= 0 && blk < num_blocks;
       okm |= ok ? 1u << kb : 0u;
       base[kb] = ((int64_t)(ok ? blk : 0) * num_kv_heads + kh) * kBS * D;
@@ -228,20 +225,39 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     }
   };
 
-  uint32_t ok0 = nit > 0 ? fetch(0, kr0, vr0) : 0u;
-  uint32_t ok1 = nit > 1 ? fetch(1, kr1, vr1) : 0u;
-
-  // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8] * q_scale, hi
-  // and lo (scores come out already scaled by scale * log2 e).
-  uint4 qhi[HW][NC], qlo[HW][NC];
+  // This wave's q rows, loaded first: their conversion then waits for them
+  // alone, not for the K/V loads queued behind.
+  float4 qraw[HW][NC][2];
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
     const float* qp =
         q + ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h0 + hh) * D + 8 * grp;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float4 x = reinterpret_cast<const float4*>(qp + 32 * c)[0];
-      float4 y = reinterpret_cast<const float4*>(qp + 32 * c)[1];
+      qraw[hh][c][0] = reinterpret_cast<const float4*>(qp + 32 * c)[0];
+      qraw[hh][c][1] = reinterpret_cast<const float4*>(qp + 32 * c)[1];
+    }
+  }
+
+  int32_t ids[KB];
+  load_ids(0, ids);
+  // Every fetch is issued, also past the last iteration (ids -1: block 0's
+  // tile is read and never used), so each body issues the same loads and the
+  // compiler's load counters wait for exactly the set being staged.
+  uint32_t ok0 = fetch(ids, kr0, vr0);
+  load_ids(1, ids);
+  uint32_t ok1 = fetch(ids, kr1, vr1);
+  load_ids(2, ids);  // for the first fetch inside the loop
+
+  // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8] * q_scale, hi
+  // and lo (scores come out already scaled by scale * log2 e), converted
+  // from the raw rows loaded before the first K/V fetch.
+  uint4 qhi[HW][NC], qlo[HW][NC];
+#pragma unroll
+  for (int hh = 0; hh < HW; ++hh)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float4 x = qraw[hh][c][0], y = qraw[hh][c][1];
       if (!row_ok) x = y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       x.x *= q_scale; x.y *= q_scale; x.z *= q_scale; x.w *= q_scale;
       y.x *= q_scale; y.y *= q_scale; y.z *= q_scale; y.w *= q_scale;
@@ -250,7 +266,6 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
       split2(y.x, y.y, qhi[hh][c].z, qlo[hh][c].z);
       split2(y.z, y.w, qhi[hh][c].w, qlo[hh][c].w);
     }
-  }
 
   f32x4_t o[HW][NO];
   float m[HW], l[HW];
@@ -447,21 +462,23 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   auto step = [&](auto masked, int it, int buf, uint32_t okm) __attribute__((always_inline)) {
     if (active && it * KB * kBS <= wlast) compute(masked, it, buf, okm);
   };
-  // Iterations it and it + 1 (the two LDS buffers); false when it + 1 is past
-  // the end.
+  // Iterations it and it + 1 (the two LDS buffers).  The loops run an even
+  // number of iterations: an iteration past the last one only stages (its
+  // keys are after every query, so no wave computes), which keeps the
+  // bodies free of exits between the two halves.
   auto pair = [&](auto masked, int it) __attribute__((always_inline)) {
     stage(0, kr0, vr0);
     const uint32_t okA = ok0;
     __syncthreads();
-    if (it + 2 < nit) ok0 = fetch(it + 2, kr0, vr0);
+    ok0 = fetch(ids, kr0, vr0);
+    load_ids(it + 3, ids);
     step(masked, it, 0, okA);
-    if (it + 1 >= nit) return false;
     stage(1, kr1, vr1);
     const uint32_t okB = ok1;
     __syncthreads();
-    if (it + 3 < nit) ok1 = fetch(it + 3, kr1, vr1);
+    ok1 = fetch(ids, kr1, vr1);
+    load_ids(it + 4, ids);
     step(masked, it + 1, 1, okB);
-    return true;
   };
   // First the pairs whose keys are all valid and at or before the wave's
   // first query (no mask), then the rest with the mask.  The switch point is
@@ -469,16 +486,16 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   // of the workgroup stay in step.  Separate loops, not a branch per
   // iteration, keep the two variants' registers apart.
   constexpr uint32_t kAllValid = (1u << KB) - 1u;
+  const int nit2 = (nit + 1) & ~1;
   int it = 0;
-  for (; it < nit; it += 2) {
+  for (; it < nit2; it += 2) {
     const int klast = (it + 2 < nit ? it + 2 : nit) * KB * kBS - 1;  // last key of the pair
     const bool plain = !active || (ok0 == kAllValid && (it + 1 >= nit || ok1 == kAllValid) &&
                                    klast <= pos0 + qr0);
     if (!plain) break;
-    if (!pair(std::false_type{}, it)) break;
+    pair(std::false_type{}, it);
   }
-  for (; it < nit; it += 2)
-    if (!pair(std::true_type{}, it)) break;
+  for (; it < nit2; it += 2) pair(std::true_type{}, it);
 
   if (!row_ok) return;
 #pragma unroll
