@@ -107,12 +107,14 @@ int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int 
 
 /* Workspace (bytes) rkv_decode_attention needs for split-K partials.
  * max_context: host-side upper bound on every ctx_lens[b] (for example
- * max_blocks_per_seq*block_size).  partition_size <= 0 picks the default. */
+ * max_blocks_per_seq*block_size).  partition_size: the size
+ * rkv_decode_partition_size returns for the pool dtype, or <= 0 for the
+ * smallest partition size of the library (enough for every dtype). */
 size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_context,
                                   int partition_size);
 
-/* Partition size (tokens) rkv_decode_attention uses for a request of
- * partition_size (<= 0: the library default). */
+/* Partition size (tokens) rkv_decode_attention uses for pools of dtype, for a
+ * request of partition_size (<= 0: the library default). */
 int rkv_decode_partition_size(int partition_size, int head_dim, int dtype);
 
 /* Single-token paged decode attention with GQA (two passes: partitions of

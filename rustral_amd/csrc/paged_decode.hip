@@ -641,8 +641,23 @@ constexpr int kBS = 16;
 #ifndef RKV_DECODE_RING_LOADS_Q  // 1-byte pools (more registers per tile)
 #define RKV_DECODE_RING_LOADS_Q 8
 #endif
+// 1-byte pools carry half the bytes per token: their own partition size and
+// waves per partition.
+#ifndef RKV_DECODE_P_Q
+#define RKV_DECODE_P_Q RKV_DECODE_P
+#endif
+#ifndef RKV_DECODE_SPLIT_Q
+#define RKV_DECODE_SPLIT_Q RKV_DECODE_SPLIT
+#endif
 constexpr int kP = RKV_DECODE_P;
-constexpr int kSplit = RKV_DECODE_SPLIT;
+constexpr int kPQ = RKV_DECODE_P_Q;
+constexpr int kPMin = kP < kPQ ? kP : kPQ;
+template <typename T>
+constexpr int part_of() { return sizeof(T) == 1 ? kPQ : kP; }
+template <typename T>
+constexpr int split_of() { return sizeof(T) == 1 ? RKV_DECODE_SPLIT_Q : RKV_DECODE_SPLIT; }
+// tokens per partition of a pool dtype
+inline int part_size(int dtype) { return (dtype == RKV_I8 || dtype == RKV_FP8) ? kPQ : kP; }
 
 struct Launch {
   int nw = 0;
@@ -657,15 +672,16 @@ template <typename T, int D>
 constexpr int ring_for() {
   constexpr int nl = kBS / (64 / (D / Traits<T>::E));
   constexpr int r = (sizeof(T) == 1 ? RKV_DECODE_RING_LOADS_Q : RKV_DECODE_RING_LOADS) / nl;
-  constexpr int nt = 2 * (kP / kBS) / kSplit;
+  constexpr int nt = 2 * (part_of<T>() / kBS) / split_of<T>();
   return r < 1 ? 1 : (r > nt ? nt : r);
 }
 
 template <typename T, int D, int G, int FMT>
 Launch make_launch() {
   Launch l;
-  l.nw = kSplit;
-  l.kernel = &decode_stream_kernel<T, D, G, kBS, kP / kBS, ring_for<T, D>(), kSplit, FMT>;
+  l.nw = split_of<T>();
+  l.kernel = &decode_stream_kernel<T, D, G, kBS, part_of<T>() / kBS, ring_for<T, D>(),
+                                   split_of<T>(), FMT>;
   return l;
 }
 
@@ -752,14 +768,15 @@ int validate(const DecodeArgs& a, int& max_parts) {
   const int G = a.num_q_heads / a.num_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(RKV_ERR_UNSUPPORTED, "num_q_heads / num_kv_heads must be 1, 2, 4 or 8");
-  if (a.partition_size > 0 && a.partition_size != kP)
+  const int P = part_size(a.dtype);
+  if (a.partition_size > 0 && a.partition_size != P)
     return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
   if (a.num_seqs > 65535 || a.num_kv_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_kv_heads must be <= 65535");
   if (a.max_context < 0) return fail(RKV_ERR_INVALID_ARG, "max_context must be >= 0");
   if (a.num_blocks < 1) return fail(RKV_ERR_INVALID_ARG, "num_blocks must be >= 1");
   const int cap = ctx_cap_of(a.max_context, a.max_blocks_per_seq, a.block_size);
-  max_parts = cap <= 0 ? 1 : (cap + kP - 1) / kP;
+  max_parts = cap <= 0 ? 1 : (cap + P - 1) / P;
   if (max_parts > kMaxMergeParts)
     return fail(RKV_ERR_UNSUPPORTED, "max_context / partition size above 4096 partitions");
   if (a.num_seqs == 0) return RKV_OK;
@@ -803,7 +820,7 @@ int launch_partitions(const DecodeArgs& a, int max_parts) {
 }
 
 int launch_merge(float* out, const int32_t* ctx_lens, int num_seqs, int num_q_heads, int head_dim,
-                 int cap, int max_parts, void* ws, hipStream_t stream) {
+                 int cap, int P, int max_parts, void* ws, hipStream_t stream) {
   if (max_parts <= 1 || num_seqs == 0) return RKV_OK;
   float *acc = nullptr, *ml = nullptr;
   split_ws(ws, num_seqs, num_q_heads, head_dim, max_parts, acc, ml);
@@ -812,15 +829,15 @@ int launch_merge(float* out, const int32_t* ctx_lens, int num_seqs, int num_q_he
   switch (head_dim) {
     case 32:
       decode_merge_kernel<32><<<grid, 64 * kMergeWaves, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
-                                                       kP, max_parts);
+                                                       P, max_parts);
       break;
     case 64:
       decode_merge_kernel<64><<<grid, 64 * kMergeWaves, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
-                                                       kP, max_parts);
+                                                       P, max_parts);
       break;
     default:
       decode_merge_kernel<128><<<grid, 64 * kMergeWaves, lds, stream>>>(out, acc, ml, ctx_lens, cap, num_q_heads,
-                                                        kP, max_parts);
+                                                        P, max_parts);
       break;
   }
   return check_launch("decode_merge_kernel");
@@ -833,17 +850,18 @@ using namespace rkv;
 
 extern "C" size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim,
                                              int max_context, int partition_size) {
-  (void)partition_size;
   if (num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_context <= 0) return 0;
-  const int max_parts = (max_context + kP - 1) / kP;
+  // a given partition size (one of the library's), else the smallest one:
+  // enough for every pool dtype
+  const int P = partition_size > 0 ? partition_size : kPMin;
+  const int max_parts = (max_context + P - 1) / P;
   return ws_bytes(num_seqs, num_q_heads, head_dim, max_parts);
 }
 
 extern "C" int rkv_decode_partition_size(int partition_size, int head_dim, int dtype) {
   (void)partition_size;
   (void)head_dim;
-  (void)dtype;
-  return kP;
+  return part_size(dtype);
 }
 
 extern "C" int rkv_decode_attention_partitions(
@@ -869,18 +887,18 @@ extern "C" int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens,
                                           int dtype, int partition_size, const void* workspace,
                                           size_t workspace_bytes, void* stream) {
   clear_error();
-  (void)dtype;
+  const int P = part_size(dtype);
   if (num_seqs < 0 || num_q_heads <= 0 || max_blocks_per_seq < 0 || max_context < 0)
     return fail(RKV_ERR_INVALID_ARG, "bad size argument");
   if (block_size != kBS) return fail(RKV_ERR_UNSUPPORTED, "block_size must be 16");
   if (head_dim != 32 && head_dim != 64 && head_dim != 128)
     return fail(RKV_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128");
-  if (partition_size > 0 && partition_size != kP)
+  if (partition_size > 0 && partition_size != P)
     return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
   if (num_seqs > 65535 || num_q_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_q_heads must be <= 65535");
   const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
-  const int max_parts = cap <= 0 ? 1 : (cap + kP - 1) / kP;
+  const int max_parts = cap <= 0 ? 1 : (cap + P - 1) / P;
   if (max_parts > kMaxMergeParts)
     return fail(RKV_ERR_UNSUPPORTED, "max_context / partition size above 4096 partitions");
   if (max_parts <= 1 || num_seqs == 0) return RKV_OK;
@@ -888,7 +906,7 @@ extern "C" int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens,
   const size_t need = ws_bytes(num_seqs, num_q_heads, head_dim, max_parts);
   if (!workspace || workspace_bytes < need)
     return fail(RKV_ERR_WORKSPACE, "workspace missing or smaller than rkv_decode_workspace_bytes()");
-  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, max_parts,
+  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, P, max_parts,
                       const_cast<void*>(workspace), static_cast<hipStream_t>(stream));
 }
 
@@ -931,6 +949,6 @@ extern "C" int rkv_decode_attention_q(float* out, const float* q, const void* k_
   if (num_seqs == 0) return RKV_OK;
   if (int rc = launch_partitions(a, max_parts)) return rc;
   const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
-  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, max_parts, workspace,
-                      a.stream);
+  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, part_size(dtype),
+                      max_parts, workspace, a.stream);
 }

@@ -8,7 +8,7 @@ import pytest
 
 from rustral_amd import _lib
 from rustral_amd._lib import (RKV_BF16, RKV_ERR_INVALID_ARG, RKV_ERR_UNSUPPORTED,
-                              RKV_ERR_WORKSPACE, RKV_F32)
+                              RKV_ERR_WORKSPACE, RKV_F32, RKV_FP8, RKV_I8)
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -73,6 +73,12 @@ def test_workspace_size():
     ws = L.rkv_decode_workspace_bytes(64, 32, 128, 4096, 0)
     rows = 64 * 32 * (4096 // P)
     assert ws >= rows * (128 + 2) * 4
+    # each pool dtype has its partition size; the default workspace (partition
+    # size 0) covers every one of them
+    for dt in (RKV_F32, RKV_BF16, RKV_I8, RKV_FP8):
+        Pd = L.rkv_decode_partition_size(0, 128, dt)
+        assert Pd > 0 and Pd % 16 == 0
+        assert ws >= L.rkv_decode_workspace_bytes(64, 32, 128, 4096, Pd)
 
 
 def test_copy_kernels_reject_bad_arguments():
