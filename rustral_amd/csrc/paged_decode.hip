@@ -130,6 +130,18 @@ __device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
   return make_uint4(pack(a[0], a[1]), pack(a[2], a[3]), pack(b[0], b[1]), pack(b[2], b[3]));
 }
 
+// ds_read_b64_tr_b8 (gfx950): within each group of 16 lanes, lane i receives
+// as byte j (j < 8) byte i & 7 of the 8 bytes addressed by lane 2 j + (i >> 3).
+// So when lane i of group g addresses row 8 g + (i >> 1), bytes c0 + 8 (i & 1)
+// .. + 7 of a row-major byte tile, it receives column c0 + i of rows 8 g ..
+// 8 g + 7: eight keys of one dim of a row-major V tile.
+__device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
+  typedef __attribute__((ext_vector_type(2))) int i32x2_t;
+  typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
+  return __builtin_bit_cast(
+      uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)const_cast<uint8_t*>(p)));
+}
+
 // ---- streaming variant ---------------------------------------------------------
 // SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
 // item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
@@ -198,6 +210,22 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
   constexpr bool QNT = FMT == RKV_I8 || FMT == RKV_FP8;
   static_assert(QNT == (sizeof(T) == 1), "1-byte element type iff a 1-byte format");
   constexpr bool MFMA = (sizeof(T) == 2 || QNT) && 2 * G <= 16;
+  // 1-byte pools: PV on the matrix cores as well.  Per pair of V tiles
+  // (32 keys) O^T[dim][col] += V^T[dim][key] P^T[key][col] on
+  // v_mfma_f32_16x16x32_bf16: A = V^T, read with ds_read_b64_tr_b8 from the
+  // pair staged row-major in this wave's LDS buffer and converted to bf16
+  // exactly; B = P^T with columns 0..G-1 = bf16(p) of the G heads and
+  // G..2G-1 = bf16(p - bf16(p)) (the V scale already folded into p).
+  constexpr bool MPV = QNT && MFMA;
+  constexpr int VROW = D + 16;   // staged V row (bytes): the 8 rows of one
+                                 // transposing read hit distinct banks
+  constexpr int NK = NTW * BS;   // keys of this wave's slice
+  static_assert(!MPV || NTW % 2 == 0, "MFMA PV takes V tiles in pairs");
+  __shared__ __align__(16) uint8_t s_vq[MPV ? SPLIT : 1][MPV ? 2 * BS * VROW : 16];
+  __shared__ __align__(16) float s_pq[MPV ? SPLIT : 1][MPV ? G * NK : 4];  // p, head-major
+  f32x4_t ov[MPV ? D / 16 : 1];
+#pragma unroll
+  for (int c = 0; c < (MPV ? D / 16 : 1); ++c) ov[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   constexpr int NC = D / 32;                     // MFMAs per tile
   const int kt = lane & 15, kq = lane >> 4;      // MFMA lanes: token row, k-quarter
   // VALU path: this lane's E dims of each head.  MFMA path: the A operand
@@ -409,7 +437,9 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
               l[g] += pv;
               // 1-byte pools: the V row scale goes into the weight (selected,
               // so the unwritten scale of a masked token never enters)
-              if constexpr (QNT)
+              if constexpr (MPV)
+                s_pq[w][g * NK + x] = pv > 0.0f ? pv * vsc[j] : 0.0f;
+              else if constexpr (QNT)
                 s_p[x * G + g] = pv > 0.0f ? pv * vsc[j] : 0.0f;
               else
                 s_p[x * G + g] = pv;
@@ -424,6 +454,58 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    } else if constexpr (MPV) {
+      // ---- PV on the matrix cores, a pair of V tiles at a time ----
+      // Stage tile i's rows into half i & 1 of this wave's buffer; rows past
+      // the context or of a bad block id are zeroed (an fp8 NaN byte times a
+      // zero p would still be NaN).
+      const int tbase = (lb0 + i) * BS;
+      uint8_t* vb = s_vq[w];
+#pragma unroll
+      for (int n = 0; n < NL; ++n) {
+        const bool keep = ok[i] & (tbase + n * TPL + slot < L);
+        uint4 vv = tile[n];
+        vv.x = keep ? vv.x : 0u;
+        vv.y = keep ? vv.y : 0u;
+        vv.z = keep ? vv.z : 0u;
+        vv.w = keep ? vv.w : 0u;
+        *reinterpret_cast<uint4*>(vb + ((i & 1) * BS + n * TPL + slot) * VROW + dl * E) = vv;
+      }
+      if constexpr (i & 1) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the pair's rows ...
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads below
+        // B = P^T: lane (kq, kt) holds keys 8 kq .. + 7 of the pair, column kt
+        const int pc = kt < G ? kt : (kt < 2 * G ? kt - G : 0);
+        const float* pp = &s_pq[w][pc * NK + (i - 1) * BS + 8 * kq];
+        const float4 p0 = reinterpret_cast<const float4*>(pp)[0];
+        const float4 p1 = reinterpret_cast<const float4*>(pp)[1];
+        const float pv8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        uint32_t pw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = pv8[2 * e], y = pv8[2 * e + 1];
+          const uint32_t hx = bf16_rne(x), hy = bf16_rne(y);
+          const uint32_t hi = hx | (hy << 16);
+          const uint32_t lo = bf16_rne(x - __uint_as_float(hx << 16)) |
+                              (bf16_rne(y - __uint_as_float(hy << 16)) << 16);
+          pw[e] = kt < G ? hi : (kt < 2 * G ? lo : 0u);
+        }
+        const uint4 pb = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+        // A = V^T, 16 dims per MFMA: this lane's read address is key
+        // 8 kq + (kt >> 1), bytes 16 c + 8 (kt & 1) .. + 7
+        const uint8_t* va = vb + (8 * kq + (kt >> 1)) * VROW + 8 * (kt & 1);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const uint2 raw = lds_read_tr8(va + 16 * c);
+          ov[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(raw.x, raw.y)),
+              __builtin_bit_cast(bf16x8_t, pb), ov[c], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before the
+        __builtin_amdgcn_wave_barrier();                         // next pair overwrites
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
     } else {
@@ -468,14 +550,50 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
     __builtin_amdgcn_sched_barrier(0);
   });
 
-  // sum over the TPL token rows, then lanes of row 0 hold the result
+  // MFMA PV: lane (kq, kt) holds O^T[dim 16 c + 4 kq + r][column kt]; head
+  // g's sum is column g (hi) plus column G + g (lo): lanes kt < G take it.
+  f32x4_t hv[MPV ? D / 16 : 1];
+  if constexpr (MPV) {
 #pragma unroll
-  for (int o = LPT; o < 64; o <<= 1)
+    for (int c = 0; c < D / 16; ++c)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+      for (int r = 0; r < 4; ++r) hv[c][r] = ov[c][r] + __shfl_xor(ov[c][r], G);
+  } else {
+    // sum over the TPL token rows, then lanes of row 0 hold the result
 #pragma unroll
-      for (int e = 0; e < E; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
-  if constexpr (SPLIT == 1) {
+    for (int o = LPT; o < 64; o <<= 1)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
+  }
+  if constexpr (SPLIT == 1 && MPV) {
+    if (kt < G) {
+      float mg = m[0], lg = l[0];  // head kt's state (selects: kt is not constant)
+#pragma unroll
+      for (int x = 1; x < G; ++x) {
+        mg = kt == x ? m[x] : mg;
+        lg = kt == x ? l[x] : lg;
+      }
+      float* dst;
+      float scl = 1.0f;
+      if (nparts == 1) {
+        dst = out + (head0 + kt) * D;
+        scl = lg > 0.0f ? 1.0f / lg : 0.0f;
+      } else {
+        const int64_t row = (head0 + kt) * max_parts + part;
+        dst = part_acc + row * D;
+        if (kq == 0) {
+          part_ml[row * 2 + 0] = mg;
+          part_ml[row * 2 + 1] = lg;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c)
+        *reinterpret_cast<float4*>(dst + 16 * c + 4 * kq) =
+            make_float4(hv[c][0] * scl, hv[c][1] * scl, hv[c][2] * scl, hv[c][3] * scl);
+    }
+  } else if constexpr (SPLIT == 1) {
     if (slot == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -505,7 +623,21 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
     // m = -inf and weight 0).
     __shared__ float s_cm[SPLIT][G], s_cl[SPLIT][G];
     __shared__ __align__(16) float s_cacc[SPLIT][G * D];
-    if (slot == 0) {
+    if constexpr (MPV) {
+      if (kt < G) {
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c)
+          *reinterpret_cast<float4*>(&s_cacc[sub][kt * D + 16 * c + 4 * kq]) =
+              make_float4(hv[c][0], hv[c][1], hv[c][2], hv[c][3]);
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          s_cm[sub][g] = m[g];
+          s_cl[sub][g] = l[g];
+        }
+      }
+    } else if (slot == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
 #pragma unroll
