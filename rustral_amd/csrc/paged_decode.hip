@@ -130,6 +130,14 @@ __device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
   return make_uint4(pack(a[0], a[1]), pack(a[2], a[3]), pack(b[0], b[1]), pack(b[2], b[3]));
 }
 
+// Two floats to packed bf16 (a in the low half), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
+
 // ds_read_b64_tr_b8 (gfx950): within each group of 16 lanes, lane i receives
 // as byte j (j < 8) byte i & 7 of the 8 bytes addressed by lane 2 j + (i >> 3).
 // So when lane i of group g addresses row 8 g + (i >> 1), bytes c0 + 8 (i & 1)
@@ -487,10 +495,9 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float x = pv8[2 * e], y = pv8[2 * e + 1];
-          const uint32_t hx = bf16_rne(x), hy = bf16_rne(y);
-          const uint32_t hi = hx | (hy << 16);
-          const uint32_t lo = bf16_rne(x - __uint_as_float(hx << 16)) |
-                              (bf16_rne(y - __uint_as_float(hy << 16)) << 16);
+          const uint32_t hi = cvt_bf16x2(x, y);  // round to nearest even (p is finite)
+          const uint32_t lo =
+              cvt_bf16x2(x - __uint_as_float(hi << 16), y - __uint_as_float(hi & 0xffff0000u));
           pw[e] = kt < G ? hi : (kt < 2 * G ? lo : 0u);
         }
         const uint4 pb = make_uint4(pw[0], pw[1], pw[2], pw[3]);
