@@ -143,6 +143,37 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
+// Two floats to packed bf16 (a in the low half), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
+
+// Transposing LDS reads of gfx950 (lane mappings probed on the GPU).
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives as
+// element j (j < 4) the 16-bit element i & 3 of the 8 bytes addressed by lane
+// 4 j + (i >> 2).  So when lane i of group g addresses row 4 g + (i >> 2),
+// columns c0 + 4 (i & 3) .. + 3 of a row-major 16-bit tile, it receives
+// column c0 + i of rows 4 g .. 4 g + 3.
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+  typedef __attribute__((ext_vector_type(4))) short i16x4_t;
+  typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+  return __builtin_bit_cast(
+      uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)const_cast<void*>(p)));
+}
+// ds_read_b64_tr_b8: within each group of 16 lanes, lane i receives as byte j
+// (j < 8) byte i & 7 of the 8 bytes addressed by lane 2 j + (i >> 3).  So when
+// lane i of group g addresses row 8 g + (i >> 1), bytes c0 + 8 (i & 1) .. + 7
+// of a row-major byte tile, it receives column c0 + i of rows 8 g .. 8 g + 7.
+__device__ __forceinline__ uint2 lds_read_tr8(const void* p) {
+  typedef __attribute__((ext_vector_type(2))) int i32x2_t;
+  typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
+  return __builtin_bit_cast(
+      uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)const_cast<void*>(p)));
+}
+
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));

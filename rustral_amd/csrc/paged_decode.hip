@@ -11,16 +11,18 @@
 //     coalesced 1 KiB loads: lane l takes 16 bytes of token row l / LPT at
 //     dims (l % LPT) * E ... + E, where E = 16 / sizeof(elem) and
 //     LPT = D / E lanes cover one row.
-//   * QK^T: on the matrix cores for bf16 pools (below); for fp32 pools each
-//     lane multiplies its E key elements with the
-//     matching E elements of the G (pre-scaled) queries held in registers,
-//     then a DPP sum over the LPT lanes of the row gives the G scores.
+//   * QK^T: on the matrix cores for bf16 and 1-byte pools (below); for fp32
+//     pools each lane multiplies its E key elements with the matching E
+//     elements of the G (pre-scaled) queries held in registers, then a DPP
+//     sum over the LPT lanes of the row gives the G scores.
 //   * Scores go to LDS; the max and the sum of exp2(s - max) are taken over
 //     the scores in LDS before PV (two-pass softmax inside the partition: no
 //     running rescale of the accumulators).
-//   * PV: the same lane mapping over V; each lane accumulates
-//     p[g][token] * v for its E dims, then lanes of different rows and
-//     different waves are summed (shuffles + LDS).
+//   * PV: bf16 and 1-byte pools on the matrix cores, V tiles staged in LDS
+//     and read transposed (below); fp32 pools on the VALU with the same lane
+//     mapping as the loads (each lane accumulates p[g][token] * v for its E
+//     dims, then lanes of different rows are summed by shuffles).  The waves
+//     of a partition combine their states through LDS.
 // Pass 2 (decode_merge_kernel): per (query head, sequence) merge of the
 // partition partials m (max), l (sum), acc (unnormalised PV):
 //   M = max m_p;  out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.
@@ -69,6 +71,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // Matrix-core operand types (v_mfma_f32_16x16x32_bf16).
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) short bf16x4_t;
 
 // Converts one 16-byte load into E floats.
 __device__ __forceinline__ void to_float(const uint4& w, float (&f)[8]) {
@@ -142,26 +145,6 @@ __device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
   return make_uint4(pack(a[0], a[1]), pack(a[2], a[3]), pack(b[0], b[1]), pack(b[2], b[3]));
 }
 
-// Two floats to packed bf16 (a in the low half), round to nearest even: one
-// v_cvt_pk_bf16_f32 on gfx950.
-__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
-  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-  typedef __attribute__((ext_vector_type(2))) float f32x2_t;
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
-}
-
-// ds_read_b64_tr_b8 (gfx950): within each group of 16 lanes, lane i receives
-// as byte j (j < 8) byte i & 7 of the 8 bytes addressed by lane 2 j + (i >> 3).
-// So when lane i of group g addresses row 8 g + (i >> 1), bytes c0 + 8 (i & 1)
-// .. + 7 of a row-major byte tile, it receives column c0 + i of rows 8 g ..
-// 8 g + 7: eight keys of one dim of a row-major V tile.
-__device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
-  typedef __attribute__((ext_vector_type(2))) int i32x2_t;
-  typedef __attribute__((address_space(3))) i32x2_t lds_i32x2;
-  return __builtin_bit_cast(
-      uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)const_cast<uint8_t*>(p)));
-}
-
 // ---- streaming variant ---------------------------------------------------------
 // SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
 // item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
@@ -179,9 +162,16 @@ __device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
 //                 at dims 32c + 8 (l / 16) straight from the pool.
 //   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
 // (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
-// D[4(l/16)+r][l%16].)  PV stays on the VALU.
+// D[4(l/16)+r][l%16].)  PV runs on the matrix cores too (below); fp32 pools
+// keep QK^T and PV on the VALU.
+// Waves per SIMD the register allocation aims for: 3 keeps the bf16 and
+// 1-byte kernels at D = 128, G <= 4 at 3 waves per SIMD without spilling.
+#ifndef RKV_DECODE_WAVES_PER_SIMD
+#define RKV_DECODE_WAVES_PER_SIMD 3
+#endif
 template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT>
-__global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
+__global__ __launch_bounds__(64 * SPLIT)
+__attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stream_kernel(
     float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
     const float* __restrict__ q, const void* __restrict__ k_pool_,
     const void* __restrict__ v_pool_, const float* __restrict__ k_scale,
@@ -230,18 +220,23 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
   constexpr bool QNT = FMT == RKV_I8 || FMT == RKV_FP8;
   static_assert(QNT == (sizeof(T) == 1), "1-byte element type iff a 1-byte format");
   constexpr bool MFMA = (sizeof(T) == 2 || QNT) && 2 * G <= 16;
-  // 1-byte pools: PV on the matrix cores as well.  Per pair of V tiles
-  // (32 keys) O^T[dim][col] += V^T[dim][key] P^T[key][col] on
-  // v_mfma_f32_16x16x32_bf16: A = V^T, read with ds_read_b64_tr_b8 from the
-  // pair staged row-major in this wave's LDS buffer and converted to bf16
-  // exactly; B = P^T with columns 0..G-1 = bf16(p) of the G heads and
-  // G..2G-1 = bf16(p - bf16(p)) (the V scale already folded into p).
-  constexpr bool MPV = QNT && MFMA;
-  constexpr int VROW = D + 16;   // staged V row (bytes): the 8 rows of one
-                                 // transposing read hit distinct banks
+  // PV on the matrix cores as well (bf16 and 1-byte pools):
+  // O^T[dim][col] += V^T[dim][key] P^T[key][col], A = V^T read with a
+  // transposing LDS read from V tiles staged row-major in this wave's LDS
+  // buffer, B = P^T with columns 0..G-1 = bf16(p) of the G heads and
+  // G..2G-1 = bf16(p - bf16(p)) (1-byte pools: the V scale already folded
+  // into p).  1-byte pools: a pair of tiles (32 keys) per
+  // v_mfma_f32_16x16x32_bf16, ds_read_b64_tr_b8 (8 keys of one dim per lane),
+  // converted to bf16 exactly.  bf16: one tile (16 keys) per
+  // v_mfma_f32_16x16x16_bf16, ds_read_b64_tr_b16 (4 keys of one dim per lane),
+  // which keeps the staging buffer at one tile.
+  constexpr bool MPV = MFMA;
+  constexpr int VROW = QNT ? D + 16 : 2 * (D + 16);  // staged V row (bytes): the rows of
+                                                      // one transposing read hit distinct banks
   constexpr int NK = NTW * BS;   // keys of this wave's slice
-  static_assert(!MPV || NTW % 2 == 0, "MFMA PV takes V tiles in pairs");
-  __shared__ __align__(16) uint8_t s_vq[MPV ? SPLIT : 1][MPV ? 2 * BS * VROW : 16];
+  constexpr int VT = QNT ? 2 : 1;  // V tiles per staged group
+  static_assert(!MPV || NTW % VT == 0, "MFMA PV takes 1-byte V tiles in pairs");
+  __shared__ __align__(16) uint8_t s_vq[MPV ? SPLIT : 1][MPV ? VT * BS * VROW : 16];
   __shared__ __align__(16) float s_pq[MPV ? SPLIT : 1][MPV ? G * NK : 4];  // p, head-major
   f32x4_t ov[MPV ? D / 16 : 1];
 #pragma unroll
@@ -457,8 +452,10 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
               l[g] += pv;
               // 1-byte pools: the V row scale goes into the weight (selected,
               // so the unwritten scale of a masked token never enters)
-              if constexpr (MPV)
+              if constexpr (MPV && QNT)
                 s_pq[w][g * NK + x] = pv > 0.0f ? pv * vsc[j] : 0.0f;
+              else if constexpr (MPV)
+                s_pq[w][g * NK + x] = pv;
               else if constexpr (QNT)
                 s_p[x * G + g] = pv > 0.0f ? pv * vsc[j] : 0.0f;
               else
@@ -477,10 +474,10 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       }
     } else if constexpr (MPV) {
-      // ---- PV on the matrix cores, a pair of V tiles at a time ----
-      // Stage tile i's rows into half i & 1 of this wave's buffer; rows past
-      // the context or of a bad block id are zeroed (an fp8 NaN byte times a
-      // zero p would still be NaN).
+      // ---- PV on the matrix cores ----
+      // Stage tile i's rows into this wave's buffer (half i & 1 for 1-byte
+      // pairs); rows past the context or of a bad block id are zeroed (a NaN
+      // element times a zero p would still be NaN).
       const int tbase = (lb0 + i) * BS;
       uint8_t* vb = s_vq[w];
 #pragma unroll
@@ -491,9 +488,36 @@ __global__ __launch_bounds__(64 * SPLIT) void decode_stream_kernel(
         vv.y = keep ? vv.y : 0u;
         vv.z = keep ? vv.z : 0u;
         vv.w = keep ? vv.w : 0u;
-        *reinterpret_cast<uint4*>(vb + ((i & 1) * BS + n * TPL + slot) * VROW + dl * E) = vv;
+        *reinterpret_cast<uint4*>(vb + ((i % VT) * BS + n * TPL + slot) * VROW + dl * 16) = vv;
       }
-      if constexpr (i & 1) {
+      if constexpr (!QNT) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the tile's rows ...
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads below
+        // B = P^T (16 x 16 x 16): k-slot 4 kq + e holds key 4 kq + e of the
+        // tile, column kt
+        const int pc = kt < G ? kt : (kt < 2 * G ? kt - G : 0);
+        const float4 p4 = *reinterpret_cast<const float4*>(&s_pq[w][pc * NK + i * BS + 4 * kq]);
+        const uint32_t h0 = cvt_bf16x2(p4.x, p4.y), h1 = cvt_bf16x2(p4.z, p4.w);
+        const uint32_t l0 =
+            cvt_bf16x2(p4.x - __uint_as_float(h0 << 16), p4.y - __uint_as_float(h0 & 0xffff0000u));
+        const uint32_t l1 =
+            cvt_bf16x2(p4.z - __uint_as_float(h1 << 16), p4.w - __uint_as_float(h1 & 0xffff0000u));
+        const uint2 pb = kt < G ? make_uint2(h0, h1)
+                                : (kt < 2 * G ? make_uint2(l0, l1) : make_uint2(0u, 0u));
+        // A = V^T: this lane's read address is key 4 kq + (kt >> 2), dims
+        // 16 c + 4 (kt & 3) .. + 3
+        const uint8_t* va = vb + (4 * kq + (kt >> 2)) * VROW + 8 * (kt & 3);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const uint2 a = lds_read_tr16(va + 32 * c);
+          ov[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              __builtin_bit_cast(bf16x4_t, a), __builtin_bit_cast(bf16x4_t, pb), ov[c], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before the
+        __builtin_amdgcn_wave_barrier();                         // next tile overwrites
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      } else if constexpr (i & 1) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the pair's rows ...
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads below

@@ -42,30 +42,20 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) short bf16x4_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
-typedef __attribute__((ext_vector_type(4))) short i16x4_t;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBS = 16;  // tokens per block = keys per staged block
 
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
-typedef __attribute__((ext_vector_type(2))) float f32x2_t;
-
-// Two floats to packed bf16 (a in the low half), round to nearest even: one
-// v_cvt_pk_bf16_f32 on gfx950.
-__device__ __forceinline__ uint32_t cvt_bf16x2(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
-}
-
-// x combined with x of lane l ^ 16, then of lane l ^ 32, through
-// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Called with
-// the same value twice, a swap returns the pair (x[l], x[l^16]) in some order,
-// so the sum or maximum equals that of a __shfl_xor exchange bit for bit.
 // max(a, b) as v_med3_f32(a, b, +inf): one instruction, without the
 // quieting copies fmaxf gets in IEEE mode (the values here are never NaN).
 __device__ __forceinline__ float max2(float a, float b) {
   return __builtin_amdgcn_fmed3f(a, b, INFINITY);
 }
 
+// x combined with x of lane l ^ 16, then of lane l ^ 32, through
+// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).  Called with
+// the same value twice, a swap returns the pair (x[l], x[l^16]) in some order,
+// so the sum or maximum equals that of a __shfl_xor exchange bit for bit.
 __device__ __forceinline__ float xor48_max(float x) {
   auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = max2(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -77,17 +67,6 @@ __device__ __forceinline__ float xor48_sum(float x) {
   x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane i receives
-// as element j (j < 4) the 16-bit element i & 3 of the 8 bytes addressed by
-// lane 4 j + (i >> 2).  So when lane i of group g addresses row 4 g + (i >> 2),
-// columns c0 + 4 (i & 3) .. + 3 of a row-major tile, it receives column c0 + i
-// of rows 4 g .. 4 g + 3: four keys of one dim of a row-major V tile.
-__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
-  return __builtin_bit_cast(
-      uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)const_cast<uint16_t*>(p)));
 }
 
 // hi = bf16(x), lo = bf16(x - hi), packed in pairs (element 2i in the low half).
