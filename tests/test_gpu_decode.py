@@ -57,6 +57,23 @@ def test_decode_small_shapes(dev, dtype, hq, hkv, d):
         assert np.abs(got - want32).max() <= BF16_VS_F32_ATOL
 
 
+@pytest.mark.parametrize("g", [1, 2, 4, 8])
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_decode_bf16_every_group_and_head_dim(dev, g, d):
+    """Every (G, D) instantiation of the bf16 kernel (QK^T and PV on the
+    matrix cores, V tiles through LDS): ragged contexts, a sequence spanning
+    several partitions and one short of a block, against the oracle on the
+    same pool."""
+    hkv = 2
+    ctx = np.array([1, 16, 47, 513, 1500, 2049], np.int32)
+    say(f"decode bf16 grid g={g} d={d}")
+    q, kp, vp, kf, vf, tables = case(g * 100 + d, len(ctx), g * hkv, hkv, d, ctx, "bf16")
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    got = run_gpu(dev, q, kp, vp, tables, ctx, scale)
+    want = oracle.decode_attention(q, kp, vp, tables, ctx, scale)
+    assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle (same pool)")
+
+
 def test_decode_matches_committed_golden(dev):
     import os
     say("decode golden fixture")

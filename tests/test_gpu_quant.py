@@ -100,7 +100,8 @@ def run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, fmt, max_context=None):
 
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64), (16, 2, 128), (8, 1, 128),
-                                      (4, 4, 64), (2, 1, 64)])
+                                      (4, 4, 64), (2, 1, 64), (2, 2, 128), (4, 2, 128),
+                                      (16, 2, 64)])
 def test_decode_q_matches_oracle_on_dequantized_pool(dev, fmt, hq, hkv, d):
     say(f"decode_q fmt={fmt} hq={hq} hkv={hkv} d={d}")
     rng = np.random.default_rng(hq * 7 + d)
