@@ -747,6 +747,47 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge_kernel(
   const int np = (L + P - 1) / P;
   if (np <= 1) return;
   const int64_t row0 = ((int64_t)b * num_q_heads + h) * max_parts;
+  const int r = lane / V4, c = lane % V4;
+  if (np <= kMergeWaves * RPW) {
+    // At most one partition row per lane group: the row's acc and its
+    // (m, l) are requested together, so the merge waits on memory once.
+    __shared__ float s_den[kMergeWaves];
+    const int p = w * RPW + r;
+    const bool has = p < np;
+    const float4 a = has ? *reinterpret_cast<const float4*>(part_acc + (row0 + p) * D + 4 * c)
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float2 ml = has ? *reinterpret_cast<const float2*>(part_ml + (row0 + p) * 2)
+                          : make_float2(-INFINITY, 0.0f);
+    float M = wave_max(ml.x);
+    if (lane == 0) s_red[w] = M;
+    __syncthreads();
+    M = s_red[0];
+#pragma unroll
+    for (int x = 1; x < kMergeWaves; ++x) M = fmaxf(M, s_red[x]);
+    const float wgt = (ml.x == -INFINITY || M == -INFINITY) ? 0.0f : exp2f(ml.x - M);
+    float4 num = make_float4(wgt * a.x, wgt * a.y, wgt * a.z, wgt * a.w);
+    const float den = wave_sum(c == 0 ? wgt * ml.y : 0.0f);  // each row's l once
+#pragma unroll
+    for (int o = V4; o < 64; o <<= 1) {
+      num.x += __shfl_xor(num.x, o);
+      num.y += __shfl_xor(num.y, o);
+      num.z += __shfl_xor(num.z, o);
+      num.w += __shfl_xor(num.w, o);
+    }
+    if (r == 0) *reinterpret_cast<float4*>(&s_acc[w][4 * c]) = num;
+    if (lane == 0) s_den[w] = den;
+    __syncthreads();
+    float dsum = 0.0f;
+#pragma unroll
+    for (int x = 0; x < kMergeWaves; ++x) dsum += s_den[x];
+    for (int dd = tid; dd < D; dd += NT) {
+      float v = 0.0f;
+#pragma unroll
+      for (int x = 0; x < kMergeWaves; ++x) v += s_acc[x][dd];
+      out[((int64_t)b * num_q_heads + h) * D + dd] = dsum > 0.0f ? v / dsum : 0.0f;
+    }
+    return;
+  }
   float M = -INFINITY;
   for (int p = tid; p < np; p += NT) M = fmaxf(M, part_ml[(row0 + p) * 2]);
   M = wave_max(M);
@@ -770,7 +811,6 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge_kernel(
 #pragma unroll
   for (int x = 0; x < kMergeWaves; ++x) den += s_red[x];
   // weighted sum of the acc rows
-  const int r = lane / V4, c = lane % V4;
   float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
   for (int p = w * RPW + r; p < np; p += kMergeWaves * RPW) {
