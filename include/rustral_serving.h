@@ -1,6 +1,8 @@
 /*
- * rustral_serving.h -- host-side paged block manager and continuous-batching
- * scheduler of librustral_kv.so (plain C ABI, host memory only).
+ * rustral_serving.h -- paged block manager (host-side and device-side) and
+ * continuous-batching scheduler of librustral_kv.so (plain C ABI; the
+ * rkv_bm_* / rkv_sched_* handles keep their state in host memory, the
+ * rkv_dbm_* manager in device memory).
  *
  * These are the callers of the device path: the block manager hands out the
  * block ids that rkv_append / rkv_gather / rkv_decode_attention index, and
@@ -79,6 +81,69 @@ int rkv_bm_fill_tables(const rkv_block_manager* bm, const int64_t* seq_ids, int 
  * list is sorted ascending, so new allocations fill the low end. */
 int64_t rkv_bm_plan_compaction(rkv_block_manager* bm, int64_t max_moves, int32_t* pairs,
                                int64_t cap_pairs);
+
+/* ---- device-side block manager ----------------------------------------------
+ * The same FIFO manager with its state in device memory: the free list is a
+ * ring of block ids, the tables are an int32 [max_seqs][max_blocks_per_seq]
+ * array indexed by the caller's sequence slot, the lengths an int32
+ * [max_seqs] array.  Calls are enqueued on the stream (no host
+ * synchronisation, so a decode step -- reserve, slot mapping, append,
+ * attention -- can run from device memory alone and be captured in a HIP
+ * graph); arguments named slots / num_tokens / positions / slot_mapping /
+ * tables are device pointers.  One call over n sequences hands out ids in
+ * call order, as n host calls would (the same ids in the same tables);
+ * sequences of one call must be distinct.  Errors found on the device are
+ * recorded in a flag read by rkv_dbm_status; the call that fails changes
+ * nothing.  No reference counterpart: PagedCache (crates/nn/src/
+ * kv_cache.rs:381-432) lives on the host; this is its device-resident form
+ * for the serving loop of continuous_batching.rs:516-537. */
+typedef struct rkv_device_block_manager rkv_device_block_manager;
+
+#define RKV_DBM_ERR_OOM 1        /* a reserve needed more blocks than are free */
+#define RKV_DBM_ERR_TABLE_FULL 2 /* a table would exceed max_blocks_per_seq */
+#define RKV_DBM_ERR_ARG 4        /* a slot outside [0, max_seqs) or a negative count */
+
+/* Allocates the state (device memory) and starts the free list with ids
+ * 0..num_blocks-1 in ascending order (initialised on stream).  NULL on bad
+ * arguments or allocation failure (see rkv_last_error). */
+rkv_device_block_manager* rkv_dbm_create(int64_t num_blocks, int block_size, int max_seqs,
+                                         int max_blocks_per_seq, void* stream);
+void rkv_dbm_destroy(rkv_device_block_manager* bm);
+
+/* Grows the table of slots[i] to ceil(num_tokens[i] / block_size) blocks
+ * (as rkv_bm_reserve), i in call order.  All or nothing: if the free list
+ * cannot cover the whole call, or a table would overflow, nothing changes
+ * and the error flag is set. */
+int rkv_dbm_reserve(rkv_device_block_manager* bm, const int32_t* slots, const int32_t* num_tokens,
+                    int n, void* stream);
+
+/* Returns every block of slots[i] to the back of the free list in table
+ * order (as rkv_bm_free), i in call order, and empties the tables. */
+int rkv_dbm_free(rkv_device_block_manager* bm, const int32_t* slots, int n, void* stream);
+
+/* slot_mapping[i] = table[slots[i]][positions[i] / block_size] * block_size +
+ * positions[i] % block_size, or -1 when the table does not cover the
+ * position (rkv_append skips negative slots). */
+int rkv_dbm_slot_mapping(const rkv_device_block_manager* bm, const int32_t* slots,
+                         const int32_t* positions, int n, int64_t* slot_mapping, void* stream);
+
+/* Dense block tables [n][max_blocks] of the given slots for
+ * rkv_decode_attention / rkv_prefill_attention / rkv_gather (-1 past a
+ * table's length). */
+int rkv_dbm_batch_tables(const rkv_device_block_manager* bm, const int32_t* slots, int n,
+                         int32_t* tables, int max_blocks, void* stream);
+
+/* Synchronises the stream and reports the number of free blocks and the
+ * error flag (RKV_DBM_ERR_* bits of the last failed call; clear != 0 resets
+ * it). */
+int rkv_dbm_status(rkv_device_block_manager* bm, int64_t* num_free, int32_t* err, int clear,
+                   void* stream);
+
+/* Synchronises and copies the state to host memory (any pointer may be
+ * NULL): tables [max_seqs * max_blocks_per_seq], lengths [max_seqs], the
+ * free list front first [num_blocks], and its length. */
+int rkv_dbm_download(const rkv_device_block_manager* bm, int32_t* tables, int32_t* lengths,
+                     int32_t* free_list, int64_t* num_free, void* stream);
 
 /* ---- scheduler (Scheduler / Batch / Request) -------------------------------- */
 

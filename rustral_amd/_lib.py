@@ -40,6 +40,14 @@ SIGNATURES = {
     "rkv_decode_attention_q": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,
                                     _i, _f, _i, _i, _p, _sz, _p]),
     # include/rustral_serving.h (host memory)
+    "rkv_dbm_create": (_p, [_i64, _i, _i, _i, _p]),
+    "rkv_dbm_destroy": (None, [_p]),
+    "rkv_dbm_reserve": (_i, [_p, _p, _p, _i, _p]),
+    "rkv_dbm_free": (_i, [_p, _p, _i, _p]),
+    "rkv_dbm_slot_mapping": (_i, [_p, _p, _p, _i, _p, _p]),
+    "rkv_dbm_batch_tables": (_i, [_p, _p, _i, _p, _i, _p]),
+    "rkv_dbm_status": (_i, [_p, _p, _p, _i, _p]),
+    "rkv_dbm_download": (_i, [_p, _p, _p, _p, _p, _p]),
     "rkv_bm_create": (_p, [_i64, _i]),
     "rkv_bm_destroy": (None, [_p]),
     "rkv_bm_allocate": (_i64, [_p, _i64, _i64, _p, _i64]),

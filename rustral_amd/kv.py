@@ -287,5 +287,88 @@ def prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tenso
     return out
 
 
+class DeviceBlockManager:
+    """The FIFO paged block manager with its state in device memory
+    (``rkv_dbm_*``): same ids in the same tables as the host ``PagedCache``
+    for the same calls, but every operation is enqueued on the stream, so a
+    decode step (reserve, slot mapping, append, attention) needs no host
+    round trip.  Sequences are addressed by slot (0 .. max_seqs-1)."""
+
+    def __init__(self, num_blocks: int, block_size: int = 16, max_seqs: int = 256,
+                 max_blocks_per_seq: int = 256, device=None):
+        self.device = torch.device(device if device is not None else "cuda")
+        self.num_blocks, self.block_size = num_blocks, block_size
+        self.max_seqs, self.max_blocks = max_seqs, max_blocks_per_seq
+        s = torch.cuda.current_stream(self.device).cuda_stream
+        self._h = lib().rkv_dbm_create(num_blocks, block_size, max_seqs, max_blocks_per_seq, s)
+        if not self._h:
+            raise _lib.RkvError(-1, lib().rkv_last_error().decode())
+
+    def close(self) -> None:
+        """Frees the device state (hipFree waits for the work in flight)."""
+        if getattr(self, "_h", None):
+            lib().rkv_dbm_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown
+            pass
+
+    def _s(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _i32(self, x) -> torch.Tensor:
+        return torch.as_tensor(x, dtype=torch.int32, device=self.device).contiguous()
+
+    def reserve(self, slots, num_tokens) -> None:
+        """Grow each slot's table to ceil(num_tokens / block_size) blocks
+        (all or nothing; failures show in ``status()``)."""
+        sl, nt = self._i32(slots), self._i32(num_tokens)
+        assert sl.numel() == nt.numel()
+        check(lib().rkv_dbm_reserve(self._h, sl.data_ptr(), nt.data_ptr(), sl.numel(), self._s()))
+
+    def free(self, slots) -> None:
+        sl = self._i32(slots)
+        check(lib().rkv_dbm_free(self._h, sl.data_ptr(), sl.numel(), self._s()))
+
+    def slot_mapping(self, slots, positions) -> torch.Tensor:
+        sl, pos = self._i32(slots), self._i32(positions)
+        out = torch.empty(sl.numel(), dtype=torch.int64, device=self.device)
+        check(lib().rkv_dbm_slot_mapping(self._h, sl.data_ptr(), pos.data_ptr(), sl.numel(),
+                                         out.data_ptr(), self._s()))
+        return out
+
+    def batch_tables(self, slots, max_blocks: int) -> torch.Tensor:
+        sl = self._i32(slots)
+        out = torch.empty((sl.numel(), max_blocks), dtype=torch.int32, device=self.device)
+        check(lib().rkv_dbm_batch_tables(self._h, sl.data_ptr(), sl.numel(), out.data_ptr(),
+                                         max_blocks, self._s()))
+        return out
+
+    def status(self, clear: bool = False):
+        """(free blocks, error bits); synchronises the stream."""
+        import ctypes as C
+        nf, err = C.c_int64(0), C.c_int32(0)
+        check(lib().rkv_dbm_status(self._h, C.addressof(nf), C.addressof(err), int(clear),
+                                   self._s()))
+        return nf.value, err.value
+
+    def download(self):
+        """(tables [max_seqs, max_blocks], lengths [max_seqs], free list front
+        first) as numpy arrays; synchronises the stream."""
+        import ctypes as C
+        import numpy as np
+        tables = np.empty((self.max_seqs, self.max_blocks), np.int32)
+        lengths = np.empty(self.max_seqs, np.int32)
+        free = np.empty(self.num_blocks, np.int32)
+        nf = C.c_int64(0)
+        check(lib().rkv_dbm_download(self._h, tables.ctypes.data, lengths.ctypes.data,
+                                     free.ctypes.data, C.addressof(nf), self._s()))
+        return tables, lengths, free[:nf.value].copy()
+
+
 __all__ = ["append", "gather", "copy_blocks", "decode_attention", "prefill_attention",
-           "append_q", "gather_q", "decode_attention_q", "workspace_bytes", "_lib"]
+           "append_q", "gather_q", "decode_attention_q", "workspace_bytes",
+           "DeviceBlockManager", "_lib"]
