@@ -50,7 +50,7 @@ def parse():
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
                    choices=["config0", "config1", "config2", "config3", "config4", "prefill",
-                            "decode_q"],
+                            "decode_q", "device_step"],
                    help="config2 (default): the headline decode line; the others print "
                         "their own line (BASELINE.json configs[0], [1], [3], [4])")
     return p.parse_args()
@@ -707,6 +707,92 @@ def run_config4(torch, dev, args):
                  steps_detail=[{k: v for k, v in s.items() if k != "bytes"} for s in steps[:n]])
 
 
+def run_device_step(torch, dev, args):
+    """configs[2]'s batch (64 sequences, contexts U[512,4096]) stepping one
+    decode token at a time through a 32-layer attention stack with the cache
+    managed on the device: per step rkv_dbm_reserve (tables grow at block
+    boundaries), rkv_dbm_slot_mapping, one multi-layer rkv_append of the new
+    token's K/V, rkv_dbm_batch_tables and 32 rkv_decode_attention calls, the
+    context lengths advanced in place -- captured once in a HIP graph and
+    replayed, no host work per step.  Blocks were handed out by growing all
+    sequences one block at a time (interleaved, as a running batch grows),
+    so each sequence's blocks are spread through the pool."""
+    import numpy as np
+    from rustral_amd import kv
+    n_layers = args.layers
+    steps, warm = args.steps, args.warmup
+    rng = np.random.default_rng(SEED)
+    ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B).astype(np.int32)
+    grow = warm + steps + 1
+    mbs = (CTX_HI + grow + BS - 1) // BS
+    nb = int(((ctx + grow + BS - 1) // BS).sum()) + 64
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    kpool = torch.empty((n_layers, nb, HKV, BS, D), dtype=torch.bfloat16, device=dev)
+    vpool = torch.empty_like(kpool)
+    for l in range(n_layers):  # N(0, 1) values, one layer at a time (bf16)
+        kpool[l].copy_(torch.randn((nb, HKV, BS, D), generator=g, device=dev))
+        vpool[l].copy_(torch.randn((nb, HKV, BS, D), generator=g, device=dev))
+    dbm = kv.DeviceBlockManager(nb, BS, B, mbs, device=dev)
+    slots = torch.arange(B, dtype=torch.int32, device=dev)
+    # interleaved growth: round r gives every sequence with more than r
+    # blocks its block r
+    for r in range(int(((ctx + BS - 1) // BS).max())):
+        dbm.reserve(slots, torch.as_tensor(np.minimum(ctx, (r + 1) * BS), dtype=torch.int32))
+    nf, err = dbm.status()
+    assert err == 0
+    q = [torch.randn((B, HQ, D), generator=g, device=dev) for _ in range(n_layers)]
+    k_new = torch.randn((n_layers, B, HKV, D), generator=g, device=dev)
+    v_new = torch.randn((n_layers, B, HKV, D), generator=g, device=dev)
+    lens = torch.as_tensor(ctx, dtype=torch.int32, device=dev)   # tokens cached before the step
+    nlen = torch.empty_like(lens)
+    max_ctx = mbs * BS
+    ws = torch.empty(kv.workspace_bytes(B, HQ, D, max_ctx), dtype=torch.uint8, device=dev)
+    outs = [torch.empty((B, HQ, D), device=dev) for _ in range(n_layers)]
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        torch.add(lens, 1, out=nlen)
+        dbm.reserve(slots, nlen)
+        sm = dbm.slot_mapping(slots, lens)      # the new token's position = old length
+        kv.append(kpool, vpool, k_new, v_new, sm)
+        tab = dbm.batch_tables(slots, mbs)
+        for l in range(n_layers):
+            kv.decode_attention(q[l], kpool[l], vpool[l], tab, nlen, scale, max_context=max_ctx,
+                                out=outs[l], workspace=ws)
+        lens.copy_(nlen)
+
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    torch.cuda.synchronize(dev)
+    lens.copy_(torch.as_tensor(ctx, dtype=torch.int32))  # the capture does not run the step
+    torch.cuda.synchronize(dev)
+    for _ in range(warm):
+        graph.replay()
+    ctx_mid = ctx + warm + 1 + steps // 2   # mean context over the timed steps
+    ms = _timed(torch, graph.replay, steps)
+    nf_end, err = dbm.status()
+    assert err == 0, "device block manager reported an error during the bench"
+    attn_bytes = algorithmic_bytes(ctx_mid) * n_layers
+    app_bytes = n_layers * B * HKV * D * 2 * (4 + 2) + B * 8
+    tok_s = B / (ms / 1e3)
+    dbm.close()
+    return _line("decode step tokens/s at batch 64 with the KV cache managed on the device "
+                 "(configs[2] shape, 32 layers)", tok_s, "tokens/s", ms, args, "bf16",
+                 {"workload": "configs[2] decode steps, device-resident block tables",
+                  "batch": B, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
+                  "block_size": BS, "layers": n_layers, "context": [CTX_LO, CTX_HI],
+                  "step": "reserve + slot mapping + append (all layers) + batch tables + "
+                          "32 decode calls, one HIP graph replay"},
+                 step_GBps=round((attn_bytes + app_bytes) / (ms / 1e3) / 1e9, 1),
+                 attention_bytes_per_step=attn_bytes, append_bytes_per_step=app_bytes,
+                 free_blocks_after=nf_end)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -721,7 +807,8 @@ def main():
     if args.workload != "config2":
         line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
                 "prefill": run_prefill, "decode_q": run_decode_q,
-                "config4": run_config4}[args.workload](torch, dev, args)
+                "config4": run_config4, "device_step": run_device_step}[args.workload](
+                    torch, dev, args)
         print(json.dumps(line), flush=True)
         return
     if args.copy_only:
