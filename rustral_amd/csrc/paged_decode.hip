@@ -191,7 +191,13 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
                 "unsupported tile shape");
   static_assert(NTILE % SPLIT == 0, "the partition splits evenly over the waves");
 
-  __shared__ __align__(16) float s_pw[SPLIT][NTW * BS * G];  // per wave: scores, then probabilities
+  // Per wave: scores, then probabilities; at the end the wave's (unnormalised)
+  // output rows for the combine of the SPLIT slices (the same buffer: a wave
+  // reads its probabilities before it writes its rows, and the combine reads
+  // the rows only after the barrier).  One buffer instead of two keeps the
+  // workgroup's LDS small enough for four workgroups per CU.
+  constexpr int SPW = NTW * BS * G > G * D ? NTW * BS * G : G * D;
+  __shared__ __align__(16) float s_pw[SPLIT][SPW];
 
   // The SPLIT waves stream consecutive NTW-tile slices of one partition and
   // combine their softmax states in LDS at the end.  The grid is KV-head
@@ -665,7 +671,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     // l = sum w_s l_s, acc = sum w_s acc_s (a slice without a valid token has
     // m = -inf and weight 0).
     __shared__ float s_cm[SPLIT][G], s_cl[SPLIT][G];
-    __shared__ __align__(16) float s_cacc[SPLIT][G * D];
+    float(*s_cacc)[SPW] = s_pw;
     if constexpr (MPV) {
       if (kt < G) {
 #pragma unroll
