@@ -92,7 +92,8 @@ int64_t rkv_bm_plan_compaction(rkv_block_manager* bm, int64_t max_moves, int32_t
  * graph); arguments named slots / num_tokens / positions / slot_mapping /
  * tables are device pointers.  One call over n sequences hands out ids in
  * call order, as n host calls would (the same ids in the same tables);
- * sequences of one call must be distinct.  Errors found on the device are
+ * sequences of one call must be distinct (a repeated slot fails the call
+ * with RKV_DBM_ERR_ARG).  Errors found on the device are
  * recorded in a flag read by rkv_dbm_status; the call that fails changes
  * nothing.  No reference counterpart: PagedCache (crates/nn/src/
  * kv_cache.rs:381-432) lives on the host; this is its device-resident form
@@ -101,11 +102,12 @@ typedef struct rkv_device_block_manager rkv_device_block_manager;
 
 #define RKV_DBM_ERR_OOM 1        /* a reserve needed more blocks than are free */
 #define RKV_DBM_ERR_TABLE_FULL 2 /* a table would exceed max_blocks_per_seq */
-#define RKV_DBM_ERR_ARG 4        /* a slot outside [0, max_seqs) or a negative count */
+#define RKV_DBM_ERR_ARG 4        /* a slot outside [0, max_seqs), repeated, or a negative count */
 
 /* Allocates the state (device memory) and starts the free list with ids
  * 0..num_blocks-1 in ascending order (initialised on stream).  NULL on bad
- * arguments or allocation failure (see rkv_last_error). */
+ * arguments (max_blocks_per_seq must be below 2^30) or allocation failure
+ * (see rkv_last_error). */
 rkv_device_block_manager* rkv_dbm_create(int64_t num_blocks, int block_size, int max_seqs,
                                          int max_blocks_per_seq, void* stream);
 void rkv_dbm_destroy(rkv_device_block_manager* bm);

@@ -30,6 +30,30 @@ struct Ctl {
   int32_t pad;
 };
 
+// Set in a sequence's length while a call checks its slots for repeats
+// (lengths stay below it: max_blocks_per_seq < 2^30).
+constexpr int32_t kMark = 1 << 30;
+
+// Flags RKV_DBM_ERR_ARG in *bad when a slot occurs twice in slots[0, n): each
+// thread sets the mark bit of its slot's length, and a mark already set means
+// an earlier occurrence; then clears the marks again.  Slots outside
+// [0, max_seqs) are left to the caller's own check.
+__device__ void find_repeats(int32_t* __restrict__ nblk, const int32_t* __restrict__ slots,
+                             int n, int max_seqs, int* bad) {
+  const int t = threadIdx.x;
+  for (int i = t; i < n; i += kThreads) {
+    const int s = slots[i];
+    if (s >= 0 && s < max_seqs && (atomicOr(&nblk[s], kMark) & kMark))
+      atomicOr(bad, RKV_DBM_ERR_ARG);
+  }
+  __syncthreads();
+  for (int i = t; i < n; i += kThreads) {
+    const int s = slots[i];
+    if (s >= 0 && s < max_seqs) atomicAnd(&nblk[s], ~kMark);
+  }
+  __syncthreads();
+}
+
 // Exclusive prefix sum of v over the workgroup (kThreads values); returns the
 // thread's offset and the chunk total in *total.
 __device__ int64_t block_scan(int64_t v, int64_t* s, int64_t* total) {
@@ -75,6 +99,7 @@ __global__ __launch_bounds__(kThreads) void reserve_kernel(
   const int t = threadIdx.x;
   if (t == 0) s_bad = 0;
   __syncthreads();
+  find_repeats(nblk, slots, n, max_seqs, &s_bad);
   // pass 1: validate and count
   int64_t need_all = 0;
   for (int c0 = 0; c0 < n; c0 += kThreads) {
@@ -134,6 +159,7 @@ __global__ __launch_bounds__(kThreads) void free_kernel(
   const int t = threadIdx.x;
   if (t == 0) s_bad = 0;
   __syncthreads();
+  find_repeats(nblk, slots, n, max_seqs, &s_bad);
   for (int c0 = 0; c0 < n; c0 += kThreads) {
     const int i = c0 + t;
     if (i < n && (slots[i] < 0 || slots[i] >= max_seqs)) atomicOr(&s_bad, RKV_DBM_ERR_ARG);
@@ -223,7 +249,7 @@ extern "C" rkv_device_block_manager* rkv_dbm_create(int64_t num_blocks, int bloc
                                                     void* stream) {
   clear_error();
   if (num_blocks < 1 || num_blocks > 0x7fffffff || block_size < 1 || max_seqs < 1 ||
-      max_blocks_per_seq < 1) {
+      max_blocks_per_seq < 1 || max_blocks_per_seq >= kMark) {
     fail(RKV_ERR_INVALID_ARG, "rkv_dbm_create: bad argument");
     return nullptr;
   }

@@ -97,6 +97,41 @@ def test_reserve_is_all_or_nothing(dev):
     dbm.close()
 
 
+def test_repeated_slot_fails_the_call(dev):
+    """A slot twice in one reserve or free -- within one 1024-thread chunk of
+    the call or in different chunks -- fails the call with ERR_ARG and
+    changes nothing; later calls behave as the host's (the repeat check
+    leaves no marks in the lengths)."""
+    say("device block manager: repeated slots fail the call")
+    nb, bs, max_seqs = 3000, 16, 1500
+    dbm = kv.DeviceBlockManager(nb, bs, max_seqs, 8, device=dev)
+    host = PagedCache(bs, nb)
+    dbm.reserve([0, 1], [20, 40])
+    host.reserve(0, 20), host.reserve(1, 40)
+    before = dbm.download()
+    for slots in ([2, 5, 2], [1, 0], list(range(2, 1300)) + [7]):
+        dbm.reserve(slots, [16] * len(slots))
+        if slots == [1, 0]:                       # distinct, no growth: a no-op
+            assert dbm.status() == (host.num_free(), 0)
+        else:
+            assert dbm.status(clear=True)[1] == ERR_ARG
+        assert all(np.array_equal(x, y) for x, y in zip(before, dbm.download()))
+    dbm.free([1, 0, 1])
+    assert dbm.status(clear=True)[1] == ERR_ARG
+    assert all(np.array_equal(x, y) for x, y in zip(before, dbm.download()))
+    slots = list(range(2, 1300))
+    dbm.reserve(slots, [16] * len(slots))
+    for s in slots:
+        host.reserve(s, 16)
+    assert dbm.status() == (host.num_free(), 0)
+    assert_same_state(dbm, host, {0, 1, *slots})
+    dbm.free([1, 0])
+    host.free(1), host.free(0)
+    assert dbm.status() == (host.num_free(), 0)
+    assert_same_state(dbm, host, set(slots))
+    dbm.close()
+
+
 def test_device_resident_decode_step_equals_host_driven_step(dev):
     """Prompts of 1..300 tokens, then 3 decode steps; all of it from device
     memory vs the same steps with host-built slots and tables."""
