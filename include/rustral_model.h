@@ -45,6 +45,27 @@ int rkv_linear(float* y, const float* x, const float* w, const float* b, int row
 int rkv_layer_norm(float* y, const float* x, const float* g, const float* b, int rows, int dim,
                    float eps, void* stream);
 
+/* The attention input of one decoder layer in one launch, for n_tokens rows
+ * of x [n_tokens][d_model]:
+ *   h = LayerNorm(x; ln_g, ln_b, eps)   (ln_g == ln_b == NULL: h = x)
+ *   q_out[t] = h[t] wq^T + bq           ([n_tokens][q_dim], wq [q_dim][d_model])
+ *   k = h wk^T + bk, v = h wv^T + bv    (wk, wv [num_kv_heads*head_dim][d_model])
+ * and k[t], v[t] appended to the paged pools at slot_mapping[t] as rkv_append
+ * does (pool layout [num_blocks][num_kv_heads][block_size][head_dim], dtype
+ * RKV_F32 or RKV_BF16; a slot outside the pool appends nothing).  Biases may
+ * be NULL.  The arithmetic and its order are those of rkv_layer_norm, three
+ * rkv_linear calls and rkv_append, so the results are the same bits.
+ * Replaces the pre-norm and q / k / v projections of the reference's layer
+ * (crates/nn/src/tape_transformer.rs:242 ln1, :94-96 wq / wk / wv) followed by
+ * the KV append (KVCache::append, crates/nn/src/kv_cache.rs:172-216).
+ * d_model <= 8192, n_tokens <= 65535. */
+int rkv_qkv_append(float* q_out, void* k_pool, void* v_pool, const int64_t* slot_mapping,
+                   const float* x, const float* ln_g, const float* ln_b, float eps,
+                   const float* wq, const float* bq, const float* wk, const float* bk,
+                   const float* wv, const float* bv, int n_tokens, int d_model, int q_dim,
+                   int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                   int dtype, void* stream);
+
 /* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).  Replaces TensorOps::gelu
  * (lib.rs:565-598). */
 int rkv_gelu(float* y, const float* x, int64_t n, void* stream);

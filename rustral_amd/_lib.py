@@ -75,6 +75,8 @@ SIGNATURES = {
     "rkv_embed": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "rkv_linear": (_i, [_p, _p, _p, _p, _i, _i, _i, _p]),
     "rkv_layer_norm": (_i, [_p, _p, _p, _p, _i, _i, _f, _p]),
+    "rkv_qkv_append": (_i, [_p, _p, _p, _p, _p, _p, _p, _f, _p, _p, _p, _p, _p, _p, _i, _i, _i,
+                            _i, _i, _i, _i64, _i, _p]),
     "rkv_gelu": (_i, [_p, _p, _i64, _p]),
     "rkv_add": (_i, [_p, _p, _p, _i64, _p]),
     "rkv_argmax": (_i, [_p, _p, _i, _i, _p]),

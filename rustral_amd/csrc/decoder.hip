@@ -125,8 +125,7 @@ struct rkv_decoder {
   int64_t* slots = nullptr;  // [max_seq] pool slot of position p
   int32_t* table = nullptr;  // [max_blocks] block table of the sequence
   float* logits = nullptr;   // [max_seq][vocab]
-  float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr,
-        *f2 = nullptr;
+  float *x = nullptr, *q = nullptr, *o = nullptr, *f2 = nullptr;
   void* ws = nullptr;
   size_t ws_bytes = 0;
   rkv_block_manager* bm = nullptr;
@@ -142,8 +141,8 @@ bool dalloc(T*& p, size_t n) {
 void release(rkv_decoder* dec) {
   if (!dec) return;
   void* bufs[] = {dec->params, dec->pe,  dec->k_pool, dec->v_pool, dec->ids,   dec->pos,
-                  dec->ctx,    dec->slots, dec->table, dec->logits, dec->x,     dec->h,
-                  dec->q,      dec->k,   dec->v,      dec->o,       dec->f2,    dec->ws};
+                  dec->ctx,    dec->slots, dec->table, dec->logits, dec->x,     dec->q,
+                  dec->o,      dec->f2,  dec->ws};
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   if (dec->bm) rkv_bm_destroy(dec->bm);
@@ -190,10 +189,8 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
             dalloc(dec->k_pool, pool) && dalloc(dec->v_pool, pool) && dalloc(dec->ids, S + 1) &&
             dalloc(dec->pos, S) && dalloc(dec->ctx, S) && dalloc(dec->slots, S) &&
             dalloc(dec->table, (size_t)dec->num_blocks) &&
-            dalloc(dec->logits, S * (size_t)c.vocab) && dalloc(dec->x, d) && dalloc(dec->h, d) &&
-            dalloc(dec->q, d) && dalloc(dec->k, (size_t)dec->kvd) &&
-            dalloc(dec->v, (size_t)dec->kvd) && dalloc(dec->o, d) &&
-            dalloc(dec->f2, (size_t)c.d_ff);
+            dalloc(dec->logits, S * (size_t)c.vocab) && dalloc(dec->x, d) && dalloc(dec->q, d) &&
+            dalloc(dec->o, d) && dalloc(dec->f2, (size_t)c.d_ff);
   dec->ws_bytes = rkv_decode_workspace_bytes(1, c.n_heads, dh, c.max_seq, 0);
   if (ok && dec->ws_bytes) ok = hipMalloc(&dec->ws, dec->ws_bytes) == hipSuccess;
   if (!ok) {
@@ -267,7 +264,7 @@ extern "C" int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int
   (void)nb;
 
   const int d = c.d_model, f = c.d_ff, V = c.vocab, H = c.n_heads, Hk = c.n_kv_heads;
-  const int dh = dec->d_head, kvd = dec->kvd;
+  const int dh = dec->d_head;
   const float scale = 1.0f / std::sqrt((float)dh);  // tape_transformer.rs:75
   const int64_t layer_pool = (int64_t)dec->num_blocks * Hk * 16 * dh;
   const float* P = dec->params;
@@ -279,25 +276,23 @@ extern "C" int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int
       const LayerOffsets o = layer_offsets(c, l);
       float* kp = dec->k_pool + l * layer_pool;
       float* vp = dec->v_pool + l * layer_pool;
-      RKV_TRY(rkv_layer_norm(dec->h, dec->x, P + o.ln1_g, P + o.ln1_b, 1, d, c.eps, s));
-      RKV_TRY(rkv_linear(dec->q, dec->h, P + o.wq, P + o.bq, 1, d, d, s));
-      RKV_TRY(rkv_linear(dec->k, dec->h, P + o.wk, P + o.bk, 1, d, kvd, s));
-      RKV_TRY(rkv_linear(dec->v, dec->h, P + o.wv, P + o.bv, 1, d, kvd, s));
-      RKV_TRY(rkv_append(kp, vp, 0, dec->k, dec->v, 0, kvd, dh, dec->slots + p, 1, 1, Hk, dh, 16,
-                         dec->num_blocks, RKV_F32, s));
+      // LN1, q / k / v projections and the KV append in one launch
+      RKV_TRY(rkv_qkv_append(dec->q, kp, vp, dec->slots + p, dec->x, P + o.ln1_g, P + o.ln1_b,
+                             c.eps, P + o.wq, P + o.bq, P + o.wk, P + o.bk, P + o.wv, P + o.bv, 1,
+                             d, d, Hk, dh, 16, dec->num_blocks, RKV_F32, s));
       RKV_TRY(rkv_decode_attention(dec->o, dec->q, kp, vp, dec->table, dec->num_blocks,
                                    dec->ctx + p, 1, H, Hk, dh, 16, dec->num_blocks, c.max_seq,
                                    scale, RKV_F32, 0, dec->ws, dec->ws_bytes, s));
       // x += o W_o^T + b_o; x += gelu(LN2(x) W_1^T + b_1) W_2^T + b_2 (fused epilogues)
       RKV_TRY(linear_launch(dec->x, dec->o, P + o.wo, P + o.bo, dec->x, 1, 1, d, d, s));
-      RKV_TRY(rkv_layer_norm(dec->h, dec->x, P + o.ln2_g, P + o.ln2_b, 1, d, c.eps, s));
-      RKV_TRY(linear_launch(dec->f2, dec->h, P + o.w1, P + o.b1, nullptr, 2, 1, d, f, s));
+      RKV_TRY(linear_launch(dec->f2, dec->x, P + o.w1, P + o.b1, nullptr, 2, 1, d, f, s,
+                            P + o.ln2_g, P + o.ln2_b, c.eps));
       RKV_TRY(linear_launch(dec->x, dec->f2, P + o.w2, P + o.b2, dec->x, 1, 1, f, d, s));
     }
     if (p + 1 < n_prompt) continue;  // prompt ids are known
     float* lg = dec->logits + (int64_t)produced * V;
-    RKV_TRY(rkv_layer_norm(dec->h, dec->x, P + fin, P + fin + d, 1, d, c.eps, s));
-    RKV_TRY(rkv_linear(lg, dec->h, P + fin + 2 * d, nullptr, 1, d, V, s));
+    RKV_TRY(linear_launch(lg, dec->x, P + fin + 2 * d, nullptr, nullptr, 0, 1, d, V, s, P + fin,
+                          P + fin + d, c.eps));
     RKV_TRY(rkv_argmax(dec->ids + p + 1, lg, 1, V, s));
     ++produced;
   }

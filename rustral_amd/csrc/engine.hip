@@ -46,8 +46,8 @@ struct rkv_engine {
   int32_t *ids = nullptr, *pos = nullptr, *q_start = nullptr, *ctx = nullptr, *tables = nullptr,
           *last = nullptr, *out_tok = nullptr;
   int64_t* slots = nullptr;
-  float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr,
-        *f2 = nullptr, *xl = nullptr, *hl = nullptr, *logits = nullptr;
+  float *x = nullptr, *q = nullptr, *o = nullptr, *f2 = nullptr, *xl = nullptr,
+        *logits = nullptr;
 };
 
 namespace {
@@ -66,8 +66,8 @@ void dfree(T*& p) {
 void free_step_buffers(rkv_engine* e) {
   dfree(e->ids), dfree(e->pos), dfree(e->q_start), dfree(e->ctx), dfree(e->tables);
   dfree(e->last), dfree(e->out_tok), dfree(e->slots);
-  dfree(e->x), dfree(e->h), dfree(e->q), dfree(e->k), dfree(e->v), dfree(e->o);
-  dfree(e->f2), dfree(e->xl), dfree(e->hl), dfree(e->logits);
+  dfree(e->x), dfree(e->q), dfree(e->o);
+  dfree(e->f2), dfree(e->xl), dfree(e->logits);
   e->cap_tok = e->cap_req = e->cap_tab = 0;
 }
 
@@ -93,11 +93,8 @@ bool reserve(rkv_engine* e, int64_t n_tok, int64_t n_req, int64_t mb) {
   const bool ok = dalloc(e->ids, ct) && dalloc(e->pos, ct) && dalloc(e->slots, ct) &&
                   dalloc(e->q_start, cr + 1) && dalloc(e->ctx, cr) && dalloc(e->last, cr) &&
                   dalloc(e->out_tok, cr) && dalloc(e->tables, cb) && dalloc(e->x, ct * d) &&
-                  dalloc(e->h, ct * d) && dalloc(e->q, ct * d) &&
-                  dalloc(e->k, ct * (size_t)e->kvd) && dalloc(e->v, ct * (size_t)e->kvd) &&
-                  dalloc(e->o, ct * d) && dalloc(e->f2, ct * f) && dalloc(e->xl, cr * d) &&
-                  dalloc(e->hl, cr * d) &&
-                  dalloc(e->logits, cr * (size_t)c.vocab);
+                  dalloc(e->q, ct * d) && dalloc(e->o, ct * d) && dalloc(e->f2, ct * f) &&
+                  dalloc(e->xl, cr * d) && dalloc(e->logits, cr * (size_t)c.vocab);
   if (!ok) {
     free_step_buffers(e);
     return false;
@@ -227,7 +224,7 @@ extern "C" int rkv_engine_step(rkv_engine* e) {
     return fail(RKV_ERR_HIP, "rkv_engine_step: upload failed");
 
   const int d = c.d_model, f = c.d_ff, V = c.vocab, H = c.n_heads, Hk = c.n_kv_heads;
-  const int dh = e->d_head, kvd = e->kvd, T = (int)n_tok;
+  const int dh = e->d_head, T = (int)n_tok;
   const float scale = 1.0f / std::sqrt((float)dh);  // tape_transformer.rs:75
   const int64_t layer_pool = e->num_blocks * Hk * 16 * dh;
   const float* P = e->params;
@@ -236,25 +233,23 @@ extern "C" int rkv_engine_step(rkv_engine* e) {
     const LayerOffsets o = layer_offsets(c, l);
     float* kp = e->k_pool + l * layer_pool;
     float* vp = e->v_pool + l * layer_pool;
-    RKV_TRY(rkv_layer_norm(e->h, e->x, P + o.ln1_g, P + o.ln1_b, T, d, c.eps, s));
-    RKV_TRY(rkv_linear(e->q, e->h, P + o.wq, P + o.bq, T, d, d, s));
-    RKV_TRY(rkv_linear(e->k, e->h, P + o.wk, P + o.bk, T, d, kvd, s));
-    RKV_TRY(rkv_linear(e->v, e->h, P + o.wv, P + o.bv, T, d, kvd, s));
-    RKV_TRY(rkv_append(kp, vp, 0, e->k, e->v, 0, kvd, dh, e->slots, T, 1, Hk, dh, 16,
-                       e->num_blocks, RKV_F32, s));
+    // LN1, q / k / v projections and the KV append in one launch
+    RKV_TRY(rkv_qkv_append(e->q, kp, vp, e->slots, e->x, P + o.ln1_g, P + o.ln1_b, c.eps,
+                           P + o.wq, P + o.bq, P + o.wk, P + o.bk, P + o.wv, P + o.bv, T, d, d,
+                           Hk, dh, 16, e->num_blocks, RKV_F32, s));
     RKV_TRY(rkv_prefill_attention(e->o, e->q, kp, vp, e->tables, mb, e->q_start, e->ctx, n_req,
                                   H, Hk, dh, 16, e->num_blocks, max_q, scale, RKV_F32, s));
     // x += o W_o^T + b_o; x += gelu(LN2(x) W_1^T + b_1) W_2^T + b_2 (fused epilogues)
     RKV_TRY(linear_launch(e->x, e->o, P + o.wo, P + o.bo, e->x, 1, T, d, d, s));
-    RKV_TRY(rkv_layer_norm(e->h, e->x, P + o.ln2_g, P + o.ln2_b, T, d, c.eps, s));
-    RKV_TRY(linear_launch(e->f2, e->h, P + o.w1, P + o.b1, nullptr, 2, T, d, f, s));
+    RKV_TRY(linear_launch(e->f2, e->x, P + o.w1, P + o.b1, nullptr, 2, T, d, f, s, P + o.ln2_g,
+                          P + o.ln2_b, c.eps));
     RKV_TRY(linear_launch(e->x, e->f2, P + o.w2, P + o.b2, e->x, 1, T, f, d, s));
   }
   // each request's last row: final norm, lm_head (no bias, transformer.rs:789), greedy
   const int64_t fin = layer_offsets(c, c.n_layers - 1).end;
   RKV_TRY(rkv_embed(e->xl, e->x, e->last, nullptr, nullptr, n_req, T, d, 0, s));
-  RKV_TRY(rkv_layer_norm(e->hl, e->xl, P + fin, P + fin + d, n_req, d, c.eps, s));
-  RKV_TRY(rkv_linear(e->logits, e->hl, P + fin + 2 * d, nullptr, n_req, d, V, s));
+  RKV_TRY(linear_launch(e->logits, e->xl, P + fin + 2 * d, nullptr, nullptr, 0, n_req, d, V, s,
+                        P + fin, P + fin + d, c.eps));
   RKV_TRY(rkv_argmax(e->out_tok, e->logits, n_req, V, s));
   std::vector<int32_t> tokens((size_t)n_req);
   if (hipMemcpyAsync(tokens.data(), e->out_tok, tokens.size() * 4, hipMemcpyDeviceToHost, s) !=

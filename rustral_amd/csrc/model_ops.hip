@@ -10,6 +10,7 @@
 #include "model_ops.hpp"
 
 #include <cmath>
+#include <type_traits>
 
 namespace rkv {
 namespace {
@@ -53,18 +54,53 @@ __device__ __forceinline__ float gelu_f(float v) {
   return 0.5f * v * (1.0f + t);
 }
 
-template <int EPI, bool VEC>
+// Stages the n floats of row xr in s_x (64 threads); with LN the row is then
+// layer-normed in place exactly as layer_norm_kernel does it (lane 0's serial
+// sums, the same expression per element), so the staged values are the bits
+// rkv_layer_norm writes.
+template <bool LN>
+__device__ __forceinline__ void stage_row(float* s_x, float* s_stat, const float* xr, int n,
+                                          const float* __restrict__ ln_g,
+                                          const float* __restrict__ ln_b, float eps) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x;
+  for (int i = lane; i < n; i += 64) s_x[i] = xr[i];
+  __syncthreads();
+  if constexpr (LN) {
+    if (lane == 0) {
+      float sum = 0.0f;
+      for (int i = 0; i < n; ++i) sum += s_x[i];
+      const float mean = sum / (float)n;
+      float vs = 0.0f;
+      for (int i = 0; i < n; ++i) {
+        const float t = s_x[i] - mean;
+        vs += t * t;
+      }
+      s_stat[0] = mean;
+      s_stat[1] = sqrtf(vs / (float)n + eps);
+    }
+    __syncthreads();
+    const float mean = s_stat[0], sd = s_stat[1];
+    for (int i = lane; i < n; i += 64) s_x[i] = (s_x[i] - mean) / sd * ln_g[i] + ln_b[i];
+    __syncthreads();
+  }
+}
+
+// LN: the input row is layer-normed first (ln_g, ln_b, eps), as rkv_layer_norm
+// followed by the linear.
+template <int EPI, bool VEC, bool LN>
 __global__ __launch_bounds__(64) void linear_kernel(float* y, const float* __restrict__ x,
                                                     const float* __restrict__ w,
                                                     const float* __restrict__ b, const float* res,
-                                                    int rows, int in_dim, int out_dim) {
+                                                    int rows, int in_dim, int out_dim,
+                                                    const float* __restrict__ ln_g,
+                                                    const float* __restrict__ ln_b, float eps) {
 #pragma clang fp contract(off)
   __shared__ float s_x[kMaxStagedIn];
+  __shared__ float s_stat[2];
   const int o = blockIdx.x * blockDim.x + threadIdx.x;
   const int r = blockIdx.y;
-  const float* xr = x + (int64_t)r * in_dim;
-  for (int i = threadIdx.x; i < in_dim; i += 64) s_x[i] = xr[i];
-  __syncthreads();
+  stage_row<LN>(s_x, s_stat, x + (int64_t)r * in_dim, in_dim, ln_g, ln_b, eps);
   if (o >= out_dim || r >= rows) return;
   const float* wo = w + (int64_t)o * in_dim;
   float sum = 0.0f;
@@ -178,13 +214,73 @@ __global__ __launch_bounds__(64) void argmax_kernel(int32_t* __restrict__ out,
   if (lane == 0) out[r] = bi;
 }
 
+// The attention input of one decoder layer in one launch: LN1 of the token's
+// row, its q / k / v projections, and the K / V rows appended to the paged
+// pools.  grid = (columns of [q | k | v] / 64, tokens); one thread per column.
+// The row is normalised in LDS by stage_row and every column's dot product
+// runs serially in linear_kernel's order, so q and the pool rows are
+// the bits of rkv_layer_norm + 3 x rkv_linear + rkv_append.  K / V columns go
+// straight to slot_mapping[t]'s pool row (bf16 pools: round to nearest even,
+// as rkv_append); a slot outside the pool appends nothing.
+template <bool LN, bool VEC, bool BF16>
+__global__ __launch_bounds__(64) void qkv_append_kernel(
+    float* __restrict__ q_out, void* __restrict__ k_pool, void* __restrict__ v_pool,
+    const int64_t* __restrict__ slot_mapping, const float* __restrict__ x,
+    const float* __restrict__ ln_g, const float* __restrict__ ln_b, float eps,
+    const float* __restrict__ wq, const float* __restrict__ bq, const float* __restrict__ wk,
+    const float* __restrict__ bk, const float* __restrict__ wv, const float* __restrict__ bv,
+    int d_model, int q_dim, int num_kv_heads, int head_dim, int block_size, int64_t num_slots) {
+#pragma clang fp contract(off)
+  __shared__ float s_x[kMaxStagedIn];
+  __shared__ float s_stat[2];
+  const int r = blockIdx.y, lane = threadIdx.x;
+  stage_row<LN>(s_x, s_stat, x + (int64_t)r * d_model, d_model, ln_g, ln_b, eps);
+  const int kvd = num_kv_heads * head_dim;
+  const int o = blockIdx.x * 64 + lane;
+  if (o >= q_dim + 2 * kvd) return;
+  const int part = o < q_dim ? 0 : (o < q_dim + kvd ? 1 : 2);  // q, k or v
+  const int col = part == 0 ? o : (part == 1 ? o - q_dim : o - q_dim - kvd);
+  const float* w = part == 0 ? wq : (part == 1 ? wk : wv);
+  const float* b = part == 0 ? bq : (part == 1 ? bk : bv);
+  const float* wo = w + (int64_t)col * d_model;
+  float sum = 0.0f;
+  if constexpr (VEC) {  // d_model % 4 == 0 and the weights 16-byte aligned
+#pragma unroll 8
+    for (int i = 0; i < d_model; i += 4) {
+      const float4 wv4 = *reinterpret_cast<const float4*>(wo + i);
+      sum += s_x[i] * wv4.x;
+      sum += s_x[i + 1] * wv4.y;
+      sum += s_x[i + 2] * wv4.z;
+      sum += s_x[i + 3] * wv4.w;
+    }
+  } else {
+    for (int i = 0; i < d_model; ++i) sum += s_x[i] * wo[i];
+  }
+  const float v = b ? sum + b[col] : sum;
+  if (part == 0) {
+    q_out[(int64_t)r * q_dim + col] = v;
+    return;
+  }
+  const int64_t slot = slot_mapping[r];
+  if (slot < 0 || slot >= num_slots) return;  // padding or out-of-range slot
+  const int64_t blk = slot / block_size, row = slot - blk * block_size;
+  const int h = col / head_dim, e = col - h * head_dim;
+  const int64_t dst = ((blk * num_kv_heads + h) * block_size + row) * head_dim + e;
+  void* pool = part == 1 ? k_pool : v_pool;
+  if constexpr (BF16)
+    static_cast<uint16_t*>(pool)[dst] = (uint16_t)bf16_rne(v);
+  else
+    static_cast<float*>(pool)[dst] = v;
+}
+
 unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
 
 // Shared by rkv_linear and the decoder / engine (fused epilogues).
 int linear_launch(float* y, const float* x, const float* w, const float* b, const float* res,
-                  int epi, int rows, int in_dim, int out_dim, hipStream_t s) {
+                  int epi, int rows, int in_dim, int out_dim, hipStream_t s, const float* ln_g,
+                  const float* ln_b, float eps) {
   if (rows < 0 || in_dim <= 0 || out_dim <= 0)
     return fail(RKV_ERR_INVALID_ARG, "rkv_linear: bad size argument");
   if (rows == 0) return RKV_OK;
@@ -192,17 +288,32 @@ int linear_launch(float* y, const float* x, const float* w, const float* b, cons
   if (in_dim > kMaxStagedIn) return fail(RKV_ERR_UNSUPPORTED, "rkv_linear: in_dim must be <= 8192");
   if (!y || !x || !w || (epi == 1 && !res))
     return fail(RKV_ERR_INVALID_ARG, "rkv_linear: null pointer argument");
+  if (!ln_g != !ln_b) return fail(RKV_ERR_INVALID_ARG, "rkv_linear: ln_g and ln_b go together");
   const bool vec = in_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
   const dim3 grid(blocks_for(out_dim, 64), (unsigned)rows);
-#define RKV_LIN(E, V) linear_kernel<E, V><<<grid, 64, 0, s>>>(y, x, w, b, res, rows, in_dim, out_dim)
-  if (epi == 1) {
-    if (vec) RKV_LIN(1, true); else RKV_LIN(1, false);
-  } else if (epi == 2) {
-    if (vec) RKV_LIN(2, true); else RKV_LIN(2, false);
-  } else {
-    if (vec) RKV_LIN(0, true); else RKV_LIN(0, false);
-  }
-#undef RKV_LIN
+  // one instantiation per (epilogue, weight loads, layer norm)
+  auto go = [&](auto epi_c, auto ln_c) {
+    constexpr int E = decltype(epi_c)::value;
+    constexpr bool L = decltype(ln_c)::value;
+    if (vec)
+      linear_kernel<E, true, L><<<grid, 64, 0, s>>>(y, x, w, b, res, rows, in_dim, out_dim, ln_g,
+                                                    ln_b, eps);
+    else
+      linear_kernel<E, false, L><<<grid, 64, 0, s>>>(y, x, w, b, res, rows, in_dim, out_dim, ln_g,
+                                                     ln_b, eps);
+  };
+  auto with_epi = [&](auto ln_c) {
+    if (epi == 1)
+      go(std::integral_constant<int, 1>{}, ln_c);
+    else if (epi == 2)
+      go(std::integral_constant<int, 2>{}, ln_c);
+    else
+      go(std::integral_constant<int, 0>{}, ln_c);
+  };
+  if (ln_g)
+    with_epi(std::true_type{});
+  else
+    with_epi(std::false_type{});
   return check_launch("rkv_linear");
 }
 
@@ -231,6 +342,53 @@ extern "C" int rkv_linear(float* y, const float* x, const float* w, const float*
   clear_error();
   return linear_launch(y, x, w, b, nullptr, 0, rows, in_dim, out_dim,
                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rkv_qkv_append(float* q_out, void* k_pool, void* v_pool,
+                              const int64_t* slot_mapping, const float* x, const float* ln_g,
+                              const float* ln_b, float eps, const float* wq, const float* bq,
+                              const float* wk, const float* bk, const float* wv,
+                              const float* bv, int n_tokens, int d_model, int q_dim,
+                              int num_kv_heads, int head_dim, int block_size,
+                              int64_t num_blocks, int dtype, void* stream) {
+  clear_error();
+  if (n_tokens < 0 || d_model <= 0 || q_dim <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || num_blocks <= 0)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_qkv_append: bad size argument");
+  if (d_model > kMaxStagedIn)
+    return fail(RKV_ERR_UNSUPPORTED, "rkv_qkv_append: d_model must be <= 8192");
+  if (n_tokens > 65535)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_qkv_append: n_tokens must be <= 65535");
+  if ((int64_t)q_dim + 2 * (int64_t)num_kv_heads * head_dim > (int64_t)INT32_MAX - 64)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_qkv_append: too many output columns");
+  if (dtype != RKV_F32 && dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, "rkv_qkv_append: pools must be RKV_F32 or RKV_BF16");
+  if (!ln_g != !ln_b)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_qkv_append: ln_g and ln_b are both given or both NULL");
+  if (n_tokens == 0) return RKV_OK;
+  if (!q_out || !k_pool || !v_pool || !slot_mapping || !x || !wq || !wk || !wv)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_qkv_append: null pointer argument");
+  const auto a16 = [](const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool vec = d_model % 4 == 0 && a16(wq) && a16(wk) && a16(wv);
+  const int cols = q_dim + 2 * num_kv_heads * head_dim;
+  const dim3 grid(blocks_for(cols, 64), (unsigned)n_tokens);
+  const int64_t num_slots = num_blocks * block_size;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define RKV_QKV(LN, V, B)                                                                     \
+  qkv_append_kernel<LN, V, B><<<grid, 64, 0, s>>>(q_out, k_pool, v_pool, slot_mapping, x, ln_g, \
+                                                  ln_b, eps, wq, bq, wk, bk, wv, bv, d_model,  \
+                                                  q_dim, num_kv_heads, head_dim, block_size,   \
+                                                  num_slots)
+  const bool ln = ln_g != nullptr, bf = dtype == RKV_BF16;
+  if (ln) {
+    if (vec) { if (bf) RKV_QKV(true, true, true); else RKV_QKV(true, true, false); }
+    else { if (bf) RKV_QKV(true, false, true); else RKV_QKV(true, false, false); }
+  } else {
+    if (vec) { if (bf) RKV_QKV(false, true, true); else RKV_QKV(false, true, false); }
+    else { if (bf) RKV_QKV(false, false, true); else RKV_QKV(false, false, false); }
+  }
+#undef RKV_QKV
+  return check_launch("rkv_qkv_append");
 }
 
 extern "C" int rkv_layer_norm(float* y, const float* x, const float* g, const float* b, int rows,

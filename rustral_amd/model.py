@@ -11,7 +11,7 @@ import numpy as np
 import torch
 
 from ._lib import RkvError, check, lib
-from .kv import _dev, _stream
+from .kv import _dev, _dtype_code, _stream
 
 
 class DecoderConfig(C.Structure):
@@ -173,6 +173,40 @@ def layer_norm(x: torch.Tensor, g: torch.Tensor, b: torch.Tensor, eps: float = 1
     return y
 
 
+def qkv_append(x: torch.Tensor, wq: torch.Tensor, wk: torch.Tensor, wv: torch.Tensor,
+               k_pool: torch.Tensor, v_pool: torch.Tensor, slot_mapping: torch.Tensor,
+               bq: torch.Tensor | None = None, bk: torch.Tensor | None = None,
+               bv: torch.Tensor | None = None, ln_g: torch.Tensor | None = None,
+               ln_b: torch.Tensor | None = None, eps: float = 1e-5) -> torch.Tensor:
+    """LN1 (when ln_g / ln_b are given), q / k / v projections and the KV
+    append of one layer in one launch; returns q [n_tokens, q_dim].  The pools
+    ([num_blocks, Hkv, BS, D], float32 or bfloat16) receive k and v at
+    slot_mapping (int64 [n_tokens], < 0: skip)."""
+    _dev(x, "x", torch.float32), _dev(slot_mapping, "slot_mapping", torch.int64)
+    for name, w in (("wq", wq), ("wk", wk), ("wv", wv)):
+        _dev(w, name, torch.float32)
+    _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    n_tok, d_model = x.shape
+    nb, hkv, bs, hd = k_pool.shape
+    if v_pool.shape != k_pool.shape or v_pool.dtype != k_pool.dtype:
+        raise ValueError("K and V pools differ")
+    if wq.shape[1] != d_model or wk.shape != (hkv * hd, d_model) or wv.shape != wk.shape:
+        raise ValueError("projection shapes do not match x and the pools")
+    if slot_mapping.shape != (n_tok,):
+        raise ValueError("slot_mapping must be [n_tokens]")
+    if (ln_g is None) != (ln_b is None):
+        raise ValueError("ln_g and ln_b are given together")
+    q = torch.empty((n_tok, wq.shape[0]), dtype=torch.float32, device=x.device)
+    opt = lambda t, n: None if t is None else _dev(t, n, torch.float32).data_ptr()  # noqa: E731
+    check(lib().rkv_qkv_append(q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
+                               slot_mapping.data_ptr(), x.data_ptr(), opt(ln_g, "ln_g"),
+                               opt(ln_b, "ln_b"), eps, wq.data_ptr(), opt(bq, "bq"),
+                               wk.data_ptr(), opt(bk, "bk"), wv.data_ptr(), opt(bv, "bv"),
+                               n_tok, d_model, wq.shape[0], hkv, hd, bs, nb,
+                               _dtype_code(k_pool), _stream(x)))
+    return q
+
+
 def gelu(x: torch.Tensor) -> torch.Tensor:
     _dev(x, "x", torch.float32)
     y = torch.empty_like(x)
@@ -208,4 +242,5 @@ def embed(table: torch.Tensor, ids: torch.Tensor, pe: torch.Tensor | None = None
 
 
 __all__ = ["DecoderConfig", "CONFIG0", "config", "param_count", "init_params", "rng_raw",
-           "fill_normal", "Decoder", "linear", "layer_norm", "gelu", "add", "argmax", "embed"]
+           "fill_normal", "Decoder", "linear", "layer_norm", "qkv_append", "gelu", "add", "argmax",
+           "embed"]

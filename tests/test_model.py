@@ -243,6 +243,61 @@ def test_gpu_layer_norm_add_embed_bit_exact(torch_dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n,d,hq,hkv,dtype,ln,bias", [
+    (1, 128, 4, 4, "f32", True, True),        # configs[0] decode row
+    (300, 128, 4, 2, "f32", True, True),      # a prompt's rows, GQA
+    (7, 256, 8, 1, "bf16", True, False),
+    (5, 4096, 32, 8, "bf16", False, True),    # Llama-3-8B layer shape
+    (3, 33, 3, 1, "f32", True, True)])        # odd d_model: the scalar weight path
+def test_gpu_qkv_append_bit_exact(torch_dev, n, d, hq, hkv, dtype, ln, bias):
+    """The fused LN1 -> q / k / v -> append launch equals the oracle's
+    layer_norm + 3 x linear + append bit for bit (pools and q), with padding
+    and out-of-range slots appending nothing."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(n * 7 + d + hq)
+    hd = d // hq
+    kvd = hkv * hd
+    nb, bs = (n + 15) // 16 + 3, 16
+    x = (rng.standard_normal((n, d)) * 1.5 + 0.3).astype(np.float32)
+    wq, wk, wv = ((rng.standard_normal((o, d)) * 0.05).astype(np.float32) for o in (hq * hd, kvd, kvd))
+    bq, bk, bv = (rng.standard_normal(o).astype(np.float32) if bias else None for o in (hq * hd, kvd, kvd))
+    g = rng.standard_normal(d).astype(np.float32) if ln else None
+    b = rng.standard_normal(d).astype(np.float32) if ln else None
+    slots = rng.permutation(nb * bs)[:n].astype(np.int64)
+    slots[::5] = -1
+    if n > 2:
+        slots[1] = nb * bs + 3                          # outside the pool: skipped
+    np_dt = np.float32
+    kp = rng.standard_normal((nb, hkv, bs, hd)).astype(np_dt)
+    vp = rng.standard_normal((nb, hkv, bs, hd)).astype(np_dt)
+    if dtype == "bf16":
+        kp, vp = oracle.bf16_from_f32(kp), oracle.bf16_from_f32(vp)
+    h = oracle.layer_norm(x, g, b) if ln else x
+    want_q = oracle.linear(h, wq, bq)
+    k_new = oracle.linear(h, wk, bk).reshape(n, hkv, hd)
+    v_new = oracle.linear(h, wv, bv).reshape(n, hkv, hd)
+    want_k, want_v = kp.copy(), vp.copy()
+    oracle.append(want_k, want_v, k_new, v_new, slots)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    if dtype == "bf16":
+        gk = torch.from_numpy(kp.view(np.int16)).to(dev).view(torch.bfloat16)
+        gv = torch.from_numpy(vp.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        gk, gv = t(kp), t(vp)
+    q = model.qkv_append(t(x), t(wq), t(wk), t(wv), gk, gv, t(slots), t(bq), t(bk), t(bv),
+                         t(g), t(b))
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), want_q)
+    if dtype == "bf16":
+        got_k = gk.view(torch.int16).cpu().numpy().view(np.uint16)
+        got_v = gv.view(torch.int16).cpu().numpy().view(np.uint16)
+    else:
+        got_k, got_v = gk.cpu().numpy(), gv.cpu().numpy()
+    assert np.array_equal(got_k.view(np.uint8), want_k.view(np.uint8))
+    assert np.array_equal(got_v.view(np.uint8), want_v.view(np.uint8))
+
+
+@pytest.mark.gpu
 def test_gpu_gelu_close(torch_dev):
     torch, dev = torch_dev
     x = np.linspace(-10, 10, 4097).astype(np.float32)
