@@ -117,15 +117,18 @@ int rkv_decoder_init_params(const rkv_decoder_config* cfg, uint64_t seed, float 
 
 /* Uploads host_params (rkv_decoder_param_count floats) and allocates the
  * paged KV pools (ceil(max_seq / 16) blocks per layer) on the current
- * device.  NULL on failure (rkv_last_error).  Supported: d_model / n_heads in
- * {32, 64, 128}, n_heads / n_kv_heads in {1, 2, 4, 8}. */
+ * device.  stream NULL: the decoder creates a stream of its own.  NULL on
+ * failure (rkv_last_error).  Supported: d_model / n_heads in {32, 64, 128},
+ * n_heads / n_kv_heads in {1, 2, 4, 8}. */
 rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const float* host_params,
                                 int64_t n_params, void* stream);
 void rkv_decoder_destroy(rkv_decoder* dec);
 
 /* Greedy generation of n_new tokens after n_prompt prompt ids (host arrays).
  * out_tokens: host [n_new]; out_logits: host [n_new][vocab] or NULL.
- * n_prompt + n_new - 1 <= max_seq.  Synchronizes the stream at the end. */
+ * n_prompt + n_new - 1 <= max_seq.  Synchronizes the stream at the end.  The
+ * launch sequence of a (n_prompt, n_new) shape is captured into a HIP graph
+ * by the first call of that shape and replayed by later ones. */
 int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int n_prompt, int n_new,
                          int32_t* out_tokens, float* out_logits);
 

@@ -6,7 +6,11 @@
 // A step keeps everything on the device: the token ids live in a device
 // array (prompt ids uploaded once, generated ids written there by
 // rkv_argmax), the slot of every position and the context length of every
-// step are precomputed, so the stream is synchronized once per call.
+// step are precomputed, so the stream is synchronized once per call.  The
+// launch sequence depends only on the call's shape (prompt length, tokens to
+// generate): it is captured once into a HIP graph and replayed by every
+// later call of that shape, the per-call data (ids, block table, slots)
+// uploaded into the same device buffers beforehand.
 #include "common.hpp"
 
 #include <cmath>
@@ -114,6 +118,9 @@ extern "C" int rkv_decoder_init_params(const rkv_decoder_config* cfg, uint64_t s
 struct rkv_decoder {
   rkv_decoder_config cfg{};
   hipStream_t stream = nullptr;
+  hipStream_t own_stream = nullptr;  // created when the caller passes no stream
+  hipGraphExec_t graph = nullptr;    // the launch sequence of the last shape
+  int graph_prompt = -1, graph_total = -1;
   int d_head = 0, kvd = 0, num_blocks = 0;
   float* params = nullptr;   // device copy of the parameter array
   float* pe = nullptr;       // [max_seq][d] positional table
@@ -143,9 +150,11 @@ void release(rkv_decoder* dec) {
   void* bufs[] = {dec->params, dec->pe,  dec->k_pool, dec->v_pool, dec->ids,   dec->pos,
                   dec->ctx,    dec->slots, dec->table, dec->logits, dec->x,     dec->q,
                   dec->o,      dec->f2,  dec->ws};
+  if (dec->graph) (void)hipGraphExecDestroy(dec->graph);
   for (void* b : bufs)
     if (b) (void)hipFree(b);
   if (dec->bm) rkv_bm_destroy(dec->bm);
+  if (dec->own_stream) (void)hipStreamDestroy(dec->own_stream);
   delete dec;
 }
 
@@ -180,6 +189,14 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
   if (!dec) return nullptr;
   dec->cfg = c;
   dec->stream = static_cast<hipStream_t>(stream);
+  if (!dec->stream) {  // graph capture needs a stream of its own
+    if (hipStreamCreateWithFlags(&dec->own_stream, hipStreamNonBlocking) != hipSuccess) {
+      set_error("rkv_decoder_create: stream creation failed");
+      release(dec);
+      return nullptr;
+    }
+    dec->stream = dec->own_stream;
+  }
   dec->d_head = dh;
   dec->kvd = c.n_kv_heads * dh;
   dec->num_blocks = (c.max_seq + 15) / 16;
@@ -229,6 +246,77 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
   return dec;
 }
 
+namespace {
+
+// Enqueues the launch sequence of one generation on s: positions 0 ..
+// total - 1, logits and the greedy id for every position from n_prompt - 1
+// on.  Everything it reads per call (ids, block table, slots) comes from the
+// decoder's device buffers, so the sequence depends only on the shape.
+int enqueue_generation(rkv_decoder* dec, int n_prompt, int total, hipStream_t s) {
+  const rkv_decoder_config& c = dec->cfg;
+  const int d = c.d_model, f = c.d_ff, V = c.vocab, H = c.n_heads, Hk = c.n_kv_heads;
+  const int dh = dec->d_head;
+  const float scale = 1.0f / std::sqrt((float)dh);  // tape_transformer.rs:75
+  const int64_t layer_pool = (int64_t)dec->num_blocks * Hk * 16 * dh;
+  const float* P = dec->params;
+  const int64_t fin = layer_offsets(c, c.n_layers - 1).end;
+  int produced = 0;
+  for (int p = 0; p < total; ++p) {
+    RKV_TRY(rkv_embed(dec->x, P, dec->ids + p, dec->pe, dec->pos + p, 1, V, d, c.max_seq, s));
+    for (int l = 0; l < c.n_layers; ++l) {
+      const LayerOffsets o = layer_offsets(c, l);
+      float* kp = dec->k_pool + l * layer_pool;
+      float* vp = dec->v_pool + l * layer_pool;
+      // LN1, q / k / v projections and the KV append in one launch
+      RKV_TRY(rkv_qkv_append(dec->q, kp, vp, dec->slots + p, dec->x, P + o.ln1_g, P + o.ln1_b,
+                             c.eps, P + o.wq, P + o.bq, P + o.wk, P + o.bk, P + o.wv, P + o.bv, 1,
+                             d, d, Hk, dh, 16, dec->num_blocks, RKV_F32, s));
+      RKV_TRY(rkv_decode_attention(dec->o, dec->q, kp, vp, dec->table, dec->num_blocks,
+                                   dec->ctx + p, 1, H, Hk, dh, 16, dec->num_blocks, c.max_seq,
+                                   scale, RKV_F32, 0, dec->ws, dec->ws_bytes, s));
+      // x += o W_o^T + b_o; x += gelu(LN2(x) W_1^T + b_1) W_2^T + b_2 (fused epilogues)
+      RKV_TRY(linear_launch(dec->x, dec->o, P + o.wo, P + o.bo, dec->x, 1, 1, d, d, s));
+      RKV_TRY(linear_launch(dec->f2, dec->x, P + o.w1, P + o.b1, nullptr, 2, 1, d, f, s,
+                            P + o.ln2_g, P + o.ln2_b, c.eps));
+      RKV_TRY(linear_launch(dec->x, dec->f2, P + o.w2, P + o.b2, dec->x, 1, 1, f, d, s));
+    }
+    if (p + 1 < n_prompt) continue;  // prompt ids are known
+    float* lg = dec->logits + (int64_t)produced * V;
+    RKV_TRY(linear_launch(lg, dec->x, P + fin + 2 * d, nullptr, nullptr, 0, 1, d, V, s, P + fin,
+                          P + fin + d, c.eps));
+    RKV_TRY(rkv_argmax(dec->ids + p + 1, lg, 1, V, s));
+    ++produced;
+  }
+  return RKV_OK;
+}
+
+// Captures enqueue_generation for this shape into dec->graph (replacing the
+// previous shape's graph).
+int capture_generation(rkv_decoder* dec, int n_prompt, int total) {
+  hipStream_t s = dec->stream;
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess)
+    return fail(RKV_ERR_HIP, "rkv_decoder_generate: stream capture failed to start");
+  const int rc = enqueue_generation(dec, n_prompt, total, s);
+  hipGraph_t g = nullptr;
+  const hipError_t ec = hipStreamEndCapture(s, &g);
+  if (rc != RKV_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (ec != hipSuccess || !g) return fail(RKV_ERR_HIP, "rkv_decoder_generate: stream capture failed");
+  hipGraphExec_t x = nullptr;
+  const hipError_t ei = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (ei != hipSuccess) return fail(RKV_ERR_HIP, "rkv_decoder_generate: graph instantiation failed");
+  if (dec->graph) (void)hipGraphExecDestroy(dec->graph);
+  dec->graph = x;
+  dec->graph_prompt = n_prompt;
+  dec->graph_total = total;
+  return RKV_OK;
+}
+
+}  // namespace
+
 extern "C" int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int n_prompt,
                                     int n_new, int32_t* out_tokens, float* out_logits) {
   clear_error();
@@ -263,42 +351,13 @@ extern "C" int rkv_decoder_generate(rkv_decoder* dec, const int32_t* prompt, int
     return fail(RKV_ERR_HIP, "rkv_decoder_generate: upload failed");
   (void)nb;
 
-  const int d = c.d_model, f = c.d_ff, V = c.vocab, H = c.n_heads, Hk = c.n_kv_heads;
-  const int dh = dec->d_head;
-  const float scale = 1.0f / std::sqrt((float)dh);  // tape_transformer.rs:75
-  const int64_t layer_pool = (int64_t)dec->num_blocks * Hk * 16 * dh;
-  const float* P = dec->params;
-  const int64_t fin = layer_offsets(c, c.n_layers - 1).end;
-  int produced = 0;
-  for (int p = 0; p < total; ++p) {
-    RKV_TRY(rkv_embed(dec->x, P, dec->ids + p, dec->pe, dec->pos + p, 1, V, d, c.max_seq, s));
-    for (int l = 0; l < c.n_layers; ++l) {
-      const LayerOffsets o = layer_offsets(c, l);
-      float* kp = dec->k_pool + l * layer_pool;
-      float* vp = dec->v_pool + l * layer_pool;
-      // LN1, q / k / v projections and the KV append in one launch
-      RKV_TRY(rkv_qkv_append(dec->q, kp, vp, dec->slots + p, dec->x, P + o.ln1_g, P + o.ln1_b,
-                             c.eps, P + o.wq, P + o.bq, P + o.wk, P + o.bk, P + o.wv, P + o.bv, 1,
-                             d, d, Hk, dh, 16, dec->num_blocks, RKV_F32, s));
-      RKV_TRY(rkv_decode_attention(dec->o, dec->q, kp, vp, dec->table, dec->num_blocks,
-                                   dec->ctx + p, 1, H, Hk, dh, 16, dec->num_blocks, c.max_seq,
-                                   scale, RKV_F32, 0, dec->ws, dec->ws_bytes, s));
-      // x += o W_o^T + b_o; x += gelu(LN2(x) W_1^T + b_1) W_2^T + b_2 (fused epilogues)
-      RKV_TRY(linear_launch(dec->x, dec->o, P + o.wo, P + o.bo, dec->x, 1, 1, d, d, s));
-      RKV_TRY(linear_launch(dec->f2, dec->x, P + o.w1, P + o.b1, nullptr, 2, 1, d, f, s,
-                            P + o.ln2_g, P + o.ln2_b, c.eps));
-      RKV_TRY(linear_launch(dec->x, dec->f2, P + o.w2, P + o.b2, dec->x, 1, 1, f, d, s));
-    }
-    if (p + 1 < n_prompt) continue;  // prompt ids are known
-    float* lg = dec->logits + (int64_t)produced * V;
-    RKV_TRY(linear_launch(lg, dec->x, P + fin + 2 * d, nullptr, nullptr, 0, 1, d, V, s, P + fin,
-                          P + fin + d, c.eps));
-    RKV_TRY(rkv_argmax(dec->ids + p + 1, lg, 1, V, s));
-    ++produced;
-  }
+  if (!dec->graph || dec->graph_prompt != n_prompt || dec->graph_total != total)
+    RKV_TRY(capture_generation(dec, n_prompt, total));
+  if (hipGraphLaunch(dec->graph, s) != hipSuccess)
+    return fail(RKV_ERR_HIP, "rkv_decoder_generate: graph launch failed");
   if (hipMemcpyAsync(out_tokens, dec->ids + n_prompt, (size_t)n_new * sizeof(int32_t),
                      hipMemcpyDeviceToHost, s) != hipSuccess ||
-      (out_logits && hipMemcpyAsync(out_logits, dec->logits, (size_t)n_new * V * sizeof(float),
+      (out_logits && hipMemcpyAsync(out_logits, dec->logits, (size_t)n_new * c.vocab * sizeof(float),
                                     hipMemcpyDeviceToHost, s) != hipSuccess) ||
       hipStreamSynchronize(s) != hipSuccess)
     return fail(RKV_ERR_HIP, "rkv_decoder_generate: copy back failed");

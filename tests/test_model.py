@@ -343,5 +343,14 @@ def test_gpu_decoder_config0_tokens_equal_oracle(dev):
     assert toks.tolist() == want.tolist()
     np.testing.assert_allclose(lg, wlg, atol=1e-4, rtol=1e-3)
     # a second call reuses the pools (blocks come back in a different order)
+    # and replays the captured launch sequence
     toks2 = dec.generate(prompt, 64)
     assert toks2.tolist() == want.tolist()
+    # replays with other data of the same shape, a new shape (a new capture),
+    # and the first shape again: every call equals the CPU decoder's
+    rng = np.random.default_rng(1)
+    for n_prompt, n_new in ((32, 64), (32, 64), (5, 20), (32, 64)):
+        p2 = rng.integers(0, 1000, n_prompt).astype(np.int32)
+        got = dec.generate(p2, n_new)
+        ref = oracle.decoder_generate(oracle.decoder_config(), params, p2, n_new)
+        assert got.tolist() == ref.tolist(), (n_prompt, n_new)
