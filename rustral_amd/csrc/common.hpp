@@ -127,8 +127,16 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (N >= 4) x += dpp<0x4E>(x);
   if constexpr (N >= 8) x += dpp<0x141>(x);
   if constexpr (N >= 16) x += dpp<0x140>(x);
-  if constexpr (N >= 32) x += __shfl_xor(x, 16);
-  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  if constexpr (N >= 32) {
+    const auto r =
+        __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (N >= 64) {
+    const auto r =
+        __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
   return x;
 }
 
@@ -174,16 +182,39 @@ __device__ __forceinline__ uint2 lds_read_tr8(const void* p) {
       uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)const_cast<void*>(p)));
 }
 
+// x[l] + x[l ^ 16] and x[l] + x[l ^ 32] through v_permlane16_swap /
+// v_permlane32_swap (VALU, no LDS round trip).  Called with the same value
+// twice, a swap returns the pair (x[l], x[l ^ 16]) in some order, so the sum
+// (commutative) is the bits of x + __shfl_xor(x, 16).
+__device__ __forceinline__ float pair16_sum(float x) {
+  const auto r =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+  const auto r =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair16_max(float x) {
+  const auto r =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_max(float x) {
+  const auto r =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Maximum / sum over the 64 lanes, every lane receiving it: DPP inside each
+// 16-lane row, then the row pairs by permlane swaps.
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  return pair32_max(pair16_max(group_max<16>(x)));
 }
 
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-  return x;
+  return pair32_sum(pair16_sum(group_sum<16>(x)));
 }
 
 }  // namespace rkv

@@ -145,6 +145,19 @@ __device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
   return make_uint4(pack(a[0], a[1]), pack(a[2], a[3]), pack(b[0], b[1]), pack(b[2], b[3]));
 }
 
+// The value of lane l + G within its 16-lane row, for the lanes l % 16 < G
+// (other lanes receive another lane's value or 0): the lo-row column that
+// pairs with hi column l of the MFMA PV result.  DPP inside the row:
+// quad_perm xor 1 / xor 2, row_ror:8 (= xor 8); for G = 4 the sum of a
+// row_shl:4 and a row_shr:4 move, one of which reads lane l + 4 while the
+// other reads past the row edge and contributes 0.
+template <int G>
+__device__ __forceinline__ float lo_col(float x) {
+  if constexpr (G == 4) return dpp<0x104>(x) + dpp<0x114>(x);
+  constexpr int CTRL = G == 1 ? 0xB1 : G == 2 ? 0x4E : 0x128;
+  return dpp<CTRL>(x);
+}
+
 // ---- streaming variant ---------------------------------------------------------
 // SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
 // item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
@@ -403,7 +416,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
           constexpr int XOR = G == 4 ? 16 : 32;  // lanes between hi and lo rows
           float sc[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[r] = (sacc[r] + __shfl_xor(sacc[r], XOR)) * qs;
+          for (int r = 0; r < 4; ++r)
+            sc[r] = (XOR == 16 ? pair16_sum(sacc[r]) : pair32_sum(sacc[r])) * qs;
           if (lane < XOR) {  // lanes kq * 16 + kt hold heads 4 kq .. 4 kq + 3
             *reinterpret_cast<float4*>(&s_p[tp * G + 4 * kq]) =
                 valid ? make_float4(sc[0], sc[1], sc[2], sc[3])
@@ -610,7 +624,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) hv[c][r] = ov[c][r] + __shfl_xor(ov[c][r], G);
+      for (int r = 0; r < 4; ++r) hv[c][r] = ov[c][r] + lo_col<G>(ov[c][r]);
   } else {
     // sum over the TPL token rows, then lanes of row 0 hold the result
 #pragma unroll
