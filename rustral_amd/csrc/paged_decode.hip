@@ -352,20 +352,22 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   }
 
   // MFMA A operands: q split into bf16 hi + lo rows (after the ring loads
-  // are issued, so the conversion overlaps them)
+  // are issued, so the conversion overlaps them), two values per
+  // v_cvt_pk_bf16_f32 (round to nearest even, no branch)
   uint4 qa[MFMA ? NC : 1];
   if constexpr (MFMA) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      uint32_t h[8];
+      uint32_t h[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t hi = bf16_rne(qv[c * 8 + e]);
-        const uint32_t lo = bf16_rne(qv[c * 8 + e] - __uint_as_float(hi << 16));
+      for (int e = 0; e < 4; ++e) {
+        const float x = qv[c * 8 + 2 * e], y = qv[c * 8 + 2 * e + 1];
+        const uint32_t hi = cvt_bf16x2(x, y);
+        const uint32_t lo =
+            cvt_bf16x2(x - __uint_as_float(hi << 16), y - __uint_as_float(hi & 0xffff0000u));
         h[e] = kt < G ? hi : (kt < 2 * G ? lo : 0u);
       }
-      qa[c] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                         h[6] | (h[7] << 16));
+      qa[c] = make_uint4(h[0], h[1], h[2], h[3]);
     }
   }
 
@@ -1051,7 +1053,15 @@ int launch_partitions(const DecodeArgs& a, int max_parts) {
   const int cap = ctx_cap_of(a.max_context, a.max_blocks_per_seq, a.block_size);
   // KV-head major: the Hkv workgroups of one (partition, sequence) are adjacent
   const dim3 grid((unsigned)a.num_kv_heads, (unsigned)max_parts, (unsigned)a.num_seqs);
-  hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), 0, a.stream, a.out, acc, ml, a.q, a.k_pool,
+  // bf16 pools at head_dim 128: 14 KiB of unused dynamic LDS per workgroup
+  // (35 -> 49 KiB) keep three workgroups (not four) on a CU; with four, the
+  // partition kernel runs ~2% slower at configs[2], while the 1-byte kernels
+  // gain from four.
+#ifndef RKV_DECODE_LDS_PAD_16
+#define RKV_DECODE_LDS_PAD_16 14336
+#endif
+  const size_t pad = (a.dtype == RKV_BF16 && a.head_dim == 128) ? RKV_DECODE_LDS_PAD_16 : 0;
+  hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), pad, a.stream, a.out, acc, ml, a.q, a.k_pool,
                      a.v_pool, a.k_scale, a.v_scale, a.block_tables, a.max_blocks_per_seq,
                      a.ctx_lens, cap,
                      a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts);
