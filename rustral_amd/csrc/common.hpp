@@ -37,11 +37,13 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // fp32 -> bf16, round to nearest even; NaN keeps sign/payload with the quiet
 // bit set.  The oracle uses the same bit routine (oracle/rkv_oracle.c).
+// Written with a select, not an early return: a data-dependent branch per
+// element costs an exec-mask region in every caller.
 __device__ __forceinline__ uint32_t bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t nan = (u >> 16) | 0x40u;
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? nan : rounded;
 }
 
 // Packs two floats into one dword of bf16 (lo = a, hi = b).
