@@ -502,15 +502,22 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
       // element times a zero p would still be NaN).
       const int tbase = (lb0 + i) * BS;
       uint8_t* vb = s_vq[w];
+      if (full[i]) {  // wave-uniform: every row of the tile is valid, no selects
 #pragma unroll
-      for (int n = 0; n < NL; ++n) {
-        const bool keep = ok[i] & (tbase + n * TPL + slot < L);
-        uint4 vv = tile[n];
-        vv.x = keep ? vv.x : 0u;
-        vv.y = keep ? vv.y : 0u;
-        vv.z = keep ? vv.z : 0u;
-        vv.w = keep ? vv.w : 0u;
-        *reinterpret_cast<uint4*>(vb + ((i % VT) * BS + n * TPL + slot) * VROW + dl * 16) = vv;
+        for (int n = 0; n < NL; ++n)
+          *reinterpret_cast<uint4*>(vb + ((i % VT) * BS + n * TPL + slot) * VROW + dl * 16) =
+              tile[n];
+      } else {
+#pragma unroll
+        for (int n = 0; n < NL; ++n) {
+          const bool keep = ok[i] & (tbase + n * TPL + slot < L);
+          uint4 vv = tile[n];
+          vv.x = keep ? vv.x : 0u;
+          vv.y = keep ? vv.y : 0u;
+          vv.z = keep ? vv.z : 0u;
+          vv.w = keep ? vv.w : 0u;
+          *reinterpret_cast<uint4*>(vb + ((i % VT) * BS + n * TPL + slot) * VROW + dl * 16) = vv;
+        }
       }
       if constexpr (!QNT) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the tile's rows ...
