@@ -120,8 +120,7 @@ __device__ __forceinline__ void to_float_q(const uint4& w, float (&f)[16]) {
 }
 
 // 8 stored bytes (two dwords) as 8 bf16 values packed in a uint4; exact, since
-// int8 integers and e4m3 values have at most 8 significant bits (the bf16 is
-// the high half of the float).
+// int8 integers and e4m3 values have at most 8 significant bits.
 template <int FMT>
 __device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
   if constexpr (FMT == RKV_FP8) {
@@ -136,13 +135,13 @@ __device__ __forceinline__ uint4 to_bf16x8_q(uint32_t lo, uint32_t hi) {
     return make_uint4(__builtin_bit_cast(uint32_t, a0), __builtin_bit_cast(uint32_t, a1),
                       __builtin_bit_cast(uint32_t, b0), __builtin_bit_cast(uint32_t, b1));
   }
+  // int8: sign-extending byte converts, then one v_cvt_pk_bf16_f32 per pair
+  // (exact: |value| <= 128)
   float a[4], b[4];
   dword_values<FMT>(lo, a);
   dword_values<FMT>(hi, b);
-  auto pack = [](float x, float y) {
-    return (__float_as_uint(x) >> 16) | (__float_as_uint(y) & 0xffff0000u);
-  };
-  return make_uint4(pack(a[0], a[1]), pack(a[2], a[3]), pack(b[0], b[1]), pack(b[2], b[3]));
+  return make_uint4(cvt_bf16x2(a[0], a[1]), cvt_bf16x2(a[2], a[3]), cvt_bf16x2(b[0], b[1]),
+                    cvt_bf16x2(b[2], b[3]));
 }
 
 // The value of lane l + G within its 16-lane row, for the lanes l % 16 < G
