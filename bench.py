@@ -1,6 +1,6 @@
 """Paged-KV decode attention benchmark on one MI355X.
 
-Workload (the configuration the metric is quoted
+Workload (benchmark configs[2], the configuration the metric is quoted
 on): Llama-3-8B attention shape, batch 64, 32 query heads, 8 KV heads
 (GQA 4:1), head_dim 128, block size 16, bf16 KV pools with fp32
 accumulation, context lengths U[512, 4096] (seed 2), random block tables,
@@ -52,7 +52,7 @@ def parse():
                    choices=["config0", "config1", "config2", "config3", "config4", "prefill",
                             "decode_q", "device_step"],
                    help="config2 (default): the headline decode line; the others print "
-                        "their own line (BASELINE.json configs[0], [1], [3], [4])")
+                        "their own line (benchmark configs[0], [1], [3], [4])")
     return p.parse_args()
 
 
@@ -149,7 +149,7 @@ def traffic_from_profiles():
     return None
 
 
-# ---- other BASELINE configs (one JSON line each; not the headline) ---------------
+# ---- the other benchmark configs (one JSON line each; not the headline) -----------
 
 def _timed(torch, fn, reps):
     """Average ms of fn() over reps calls, HIP events on the current stream."""
@@ -574,7 +574,7 @@ def run_config4(torch, dev, args):
     appended in bulk (one launch for all layers) and run through causal
     prefill attention (one call per layer), then one decode token for every
     running sequence: append (one launch) + 32 decode-attention calls.
-    Hq = 32 (GQA 4:1) is assumed; BASELINE does not state it.  One untimed
+    Hq = 32 (GQA 4:1) is assumed; the benchmark configuration does not state it.  One untimed
     and four timed steps: every step replaces 10% of the sequences by
     128-token ones, so a longer run drifts away from the configuration's
     context distribution U[1, 8192]."""

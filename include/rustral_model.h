@@ -1,7 +1,7 @@
 /*
  * rustral_model.h -- the model glue around the paged-KV path in
  * librustral_kv.so: the TensorOps subset a decoder step needs on the device,
- * a greedy decoder built from them and the paged-KV
+ * a greedy decoder (benchmark configs[0]) built from them and the paged-KV
  * entry points of rustral_kv.h, and the seeded parameter generator.
  *
  * Conventions are those of rustral_kv.h (device pointers unless marked host,
@@ -80,7 +80,7 @@ int rkv_add(float* y, const float* a, const float* b, int64_t n, void* stream);
  * element i unless the current best is greater. */
 int rkv_argmax(int32_t* out, const float* x, int rows, int n, void* stream);
 
-/* ---- greedy decoder ------------------------------------
+/* ---- greedy decoder (benchmark configs[0]) ------------------------------------
  * Pre-LN causal decoder: x = E[id] + PE[pos]; per layer h = LN1(x),
  * q,k,v = h W^T + b, K/V appended to a paged fp32 pool (16-token blocks from
  * a host block manager), a = paged decode attention (rkv_decode_attention)

@@ -314,7 +314,7 @@ class DecoderConfig(C.Structure):
                 ("max_seq", C.c_int), ("eps", C.c_float)]
 
 
-# 2 layers, d_model 128, 4 heads (head_dim 32), MLP 512,
+# benchmark configs[0]: 2 layers, d_model 128, 4 heads (head_dim 32), MLP 512,
 # vocab 1000; 32 prompt ids + 64 greedy tokens = 96 positions.
 CONFIG0 = dict(vocab=1000, d_model=128, n_heads=4, n_kv_heads=4, d_ff=512, n_layers=2,
                max_seq=128, eps=1e-5)

@@ -1,5 +1,5 @@
 """The model glue around the paged-KV path: device TensorOps subset, the
-greedy decoder of BASELINE configs[0], and the seeded parameter generator
+greedy decoder of benchmark configs[0], and the seeded parameter generator
 (include/rustral_model.h, implemented in csrc/model_ops.hip and
 csrc/decoder.hip).
 """
@@ -21,7 +21,7 @@ class DecoderConfig(C.Structure):
                 ("max_seq", C.c_int), ("eps", C.c_float)]
 
 
-# 2 layers, d_model 128, 4 heads x 32, MLP 512, vocab 1000.
+# benchmark configs[0]: 2 layers, d_model 128, 4 heads x 32, MLP 512, vocab 1000.
 CONFIG0 = dict(vocab=1000, d_model=128, n_heads=4, n_kv_heads=4, d_ff=512, n_layers=2,
                max_seq=128, eps=1e-5)
 

@@ -1,4 +1,4 @@
-"""Model glue around the path: generator, oracle pins,
+"""Model glue around the path (benchmark configs[0]): generator, oracle pins,
 device ops and the end-to-end greedy decoder.
 
 CPU tests pin the oracle's decoder glue (oracle/rkv_oracle.c) against an
