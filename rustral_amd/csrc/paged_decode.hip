@@ -888,6 +888,13 @@ constexpr int kBS = 16;
 #ifndef RKV_DECODE_RING_LOADS_Q  // 1-byte pools (more registers per tile)
 #define RKV_DECODE_RING_LOADS_Q 8
 #endif
+// bf16 pools at head_dim 128: bytes of unused dynamic LDS per workgroup
+// (39 -> 53 KiB) so that three workgroups (not four) share a CU; with four,
+// the partition kernel runs ~2% slower at configs[2], while the 1-byte
+// kernels gain from four.
+#ifndef RKV_DECODE_LDS_PAD_16
+#define RKV_DECODE_LDS_PAD_16 14336
+#endif
 // 1-byte pools carry half the bytes per token: their own partition size and
 // waves per partition.
 #ifndef RKV_DECODE_P_Q
@@ -1059,13 +1066,6 @@ int launch_partitions(const DecodeArgs& a, int max_parts) {
   const int cap = ctx_cap_of(a.max_context, a.max_blocks_per_seq, a.block_size);
   // KV-head major: the Hkv workgroups of one (partition, sequence) are adjacent
   const dim3 grid((unsigned)a.num_kv_heads, (unsigned)max_parts, (unsigned)a.num_seqs);
-  // bf16 pools at head_dim 128: 14 KiB of unused dynamic LDS per workgroup
-  // (35 -> 49 KiB) keep three workgroups (not four) on a CU; with four, the
-  // partition kernel runs ~2% slower at configs[2], while the 1-byte kernels
-  // gain from four.
-#ifndef RKV_DECODE_LDS_PAD_16
-#define RKV_DECODE_LDS_PAD_16 14336
-#endif
   const size_t pad = (a.dtype == RKV_BF16 && a.head_dim == 128) ? RKV_DECODE_LDS_PAD_16 : 0;
   hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), pad, a.stream, a.out, acc, ml, a.q, a.k_pool,
                      a.v_pool, a.k_scale, a.v_scale, a.block_tables, a.max_blocks_per_seq,
