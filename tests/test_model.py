@@ -243,6 +243,28 @@ def test_gpu_layer_norm_add_embed_bit_exact(torch_dev):
 
 
 @pytest.mark.gpu
+def test_gpu_decoder_on_a_caller_stream(dev):
+    """The decoder built on a caller's (non-default) stream captures and
+    replays its launch sequence on that stream; tokens equal the CPU
+    decoder's on the first call (capture) and on later ones (replays)."""
+    import torch
+    from tests.gpu_util import say
+    say("decoder on a caller stream")
+    cfg = model.config()
+    params = model.init_params(cfg, seed=3, std=0.02)
+    rng = np.random.default_rng(4)
+    side = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(side):
+        dec = model.Decoder(cfg, params)
+        for _ in range(3):
+            prompt = rng.integers(0, 1000, 12).astype(np.int32)
+            got = dec.generate(prompt, 24)
+            want = oracle.decoder_generate(oracle.decoder_config(), params, prompt, 24)
+            assert got.tolist() == want.tolist()
+    torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("n,d,hq,hkv,dtype,ln,bias", [
     (1, 128, 4, 4, "f32", True, True),        # configs[0] decode row
     (300, 128, 4, 2, "f32", True, True),      # a prompt's rows, GQA
