@@ -352,7 +352,7 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
           s[hh][kb][r] = __builtin_amdgcn_exp2f(s[hh][kb][r] - mref);
           ls += s[hh][kb][r];
         }
-      l[hh] += xor48_sum(ls);
+      l[hh] += ls;  // this lane's keys of the row; the row's lanes are summed at the end
     }
 
     // ---- O^T += V^T P^T ----
@@ -476,6 +476,11 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   }
   for (; it < nit2; it += 2) pair(std::true_type{}, it);
 
+  // every lane kept its own keys' sum of the row (rescaled with the row's
+  // maximum like the accumulators): the row sum over its four lanes, with
+  // every lane of the wave still active for the swaps
+#pragma unroll
+  for (int hh = 0; hh < HW; ++hh) l[hh] = xor48_sum(l[hh]);
   if (!row_ok) return;
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) {
