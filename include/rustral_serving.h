@@ -172,7 +172,10 @@ int64_t rkv_sched_add_request(rkv_scheduler* s, const int32_t* prompt, int n_pro
                               int max_tokens, int priority);
 
 /* Scheduler::schedule (:248-296): retire finished requests (their blocks are
- * freed -- the reference keeps them), resume paused ones (re-allocating their
+ * freed -- the reference keeps them), pause a running request whose last
+ * update ran out of blocks and still finds none (the "should preempt" of
+ * :313-315; it resumes later by recompute, so no batch row ever has a table
+ * shorter than its sequence), resume paused ones (re-allocating their
  * blocks; they then recompute prompt + generated), admit pending ones
  * (allocating ceil(prompt / block_size) blocks), preempt a Low-priority
  * request under pressure, and build the batch.  The batch lists running
@@ -198,8 +201,9 @@ int rkv_sched_batch(const rkv_scheduler* s, int64_t* request_ids, int32_t* seq_l
 
 /* Scheduler::update (:299-322): appends each request's new token and grows
  * its block table to cover the new length.  RKV_ERR_OOM when the pool is
- * exhausted (the tokens before the failing one are applied, as in the
- * reference's loop). */
+ * exhausted: the tokens before the failing one are applied, as in the
+ * reference's loop, and the failing request keeps its token; the next
+ * rkv_sched_schedule pauses it if its table still cannot grow. */
 int rkv_sched_update(rkv_scheduler* s, const int64_t* request_ids, const int32_t* tokens, int n);
 
 /* Scheduler stats (:391-438): counts and tokens generated by completed

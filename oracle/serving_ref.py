@@ -111,6 +111,11 @@ class SchedulerRef:
             if self.running[rid].should_complete():
                 self.cache.free(rid)
                 self.completed.append(self.running.pop(rid))
+        for rid in sorted(self.running):                   # 1b. starved by an OOM update
+            r = self.running[rid]
+            if self.cache.reserve(rid, r.seq_len()) is None:   # :313-315 "should preempt"
+                self.cache.free(rid)
+                self.paused.append(self.running.pop(rid))
         while self.paused and len(self.running) < self.max_batch:  # 2. resume
             r = self.paused[0]
             if self.cache.reserve(r.id, r.seq_len()) is None:

@@ -204,8 +204,11 @@ extern "C" int rkv_engine_step(rkv_engine* e) {
       const int p = first[(size_t)r] + (int)i;
       if (p >= c.max_seq) return fail(RKV_ERR_INVALID_ARG, "rkv_engine_step: position >= max_seq");
       tok_pos[(size_t)t] = p;
-      const int32_t blk = tab[(size_t)r * mb + p / 16];
-      if (blk < 0) return fail(RKV_ERR_INVALID_ARG, "rkv_engine_step: position without a block");
+      // the scheduler hands out tables that cover every row's sequence; a
+      // position past the row's table is refused rather than read out of it
+      const int32_t blk = p / 16 < mb ? tab[(size_t)r * mb + p / 16] : -1;
+      if (blk < 0 || blk >= e->num_blocks)
+        return fail(RKV_ERR_OOM, "rkv_engine_step: position without a block (KV cache out of memory)");
       slots[(size_t)t] = (int64_t)blk * 16 + p % 16;
     }
   }

@@ -200,6 +200,22 @@ class Scheduler {
         ++it;
       }
     }
+    // 1b. a running request whose last update found no free block (its table
+    // no longer covers its sequence) retries the reservation; if the pool is
+    // still full it is paused like a preempted request and later resumes by
+    // recompute -- the "should preempt" of the reference's out-of-memory
+    // branch (continuous_batching.rs:313-315).  Ascending id.
+    for (auto it = running_.begin(); it != running_.end();) {
+      Request& r = it->second;
+      if (cache_.reserve(r.id, r.seq_len()) >= 0) {
+        ++it;
+        continue;
+      }
+      cache_.free_seq(r.id);
+      r.state = State::Paused;
+      paused_.push_back(std::move(r));
+      it = running_.erase(it);
+    }
     // 2. resume paused requests (in pause order) while there is room
     while (!paused_.empty() && (int)running_.size() < max_batch_) {
       Request& r = paused_.front();

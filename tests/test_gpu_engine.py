@@ -92,3 +92,29 @@ def test_engine_reports_pool_exhaustion(dev):
             if eng.step() == 0:
                 break
     assert e.value.code == RKV_ERR_OOM
+
+
+def test_engine_steps_on_after_an_out_of_memory_update(dev):
+    """An update that finds no free block raises RKV_ERR_OOM; the engine keeps
+    stepping: the starved request is paused (its blocks go back), the other
+    request's rows never read past a table, and the starved one resumes by
+    recompute.  Every request's tokens still equal the oracle's."""
+    say("engine: steps after an out-of-memory update")
+    cfg = model.config()
+    params = model.init_params(cfg, seed=0, std=0.02)
+    reqs = requests(4, [16, 30], [30, 20])
+    eng = model.Engine(cfg, params, num_blocks=5, max_batch_size=2)
+    ids = [eng.submit(p, m) for p, m in reqs]
+    ooms = 0
+    for _ in range(200):
+        try:
+            if eng.step() == 0:
+                break
+        except RkvError as e:
+            assert e.code == RKV_ERR_OOM
+            ooms += 1
+    assert ooms >= 1, "the scenario is meant to run out of blocks"
+    assert eng.scheduler.stats()["completed"] == len(reqs)
+    for rid, (p, m) in zip(ids, reqs):
+        want, _ = expected(params, p, m)
+        assert eng.generated(rid) == want, f"request {rid}"

@@ -206,9 +206,42 @@ def test_scheduler_matches_restatement(seed):
         except RuntimeError:
             ok = False
         assert ok == ok_ref
-        if not ok:
-            break
         assert s.stats() == ref.stats()
+        # after an out-of-memory update the run goes on: the next schedule
+        # pauses the starved request (both sides), so tables keep covering
+        # their sequences
+
+
+def test_update_oom_then_schedule_pauses_the_starved_request():
+    """An update that finds no free block keeps the token (the reference adds
+    it before allocating, continuous_batching.rs:301-316); the next schedule
+    must not hand out a row whose table is too short: the request is paused
+    and resumes by recompute once blocks are free."""
+    s, ref = Scheduler(3, 16, 4, 512), SchedulerRef(3, 16, 4, 512)
+    a = s.add_request([5] * 16, 8)
+    b = s.add_request([6] * 31, 8)
+    assert ref.add_request([5] * 16, 8) == a and ref.add_request([6] * 31, 8) == b
+    s.schedule(), ref.schedule()                   # a: 1 block, b: 2 blocks, pool empty
+    with pytest.raises(RuntimeError, match="out of memory"):
+        s.update({a: 7, b: 7})                     # a needs a second block
+    assert ref.update({a: 7, b: 7}) is False
+    bt = s.schedule()
+    rows = ref.schedule()
+    assert bt.request_ids == [x[0] for x in rows] == [b]
+    for i, x in enumerate(rows):
+        t = bt.block_tables[i]
+        assert t[t >= 0].tolist() == x[4] and len(x[4]) * 16 >= x[2]
+    assert s.stats() == ref.stats() and s.stats()["paused"] == 1
+    # b finishes; a resumes by recomputing prompt + its kept token
+    while True:
+        out = {rid: 4 for rid in bt.request_ids}
+        s.update(out), ref.update(out)
+        bt, rows = s.schedule(), ref.schedule()
+        if bt is None or a in bt.request_ids:
+            break
+    assert rows is not None and bt.request_ids == [x[0] for x in rows]
+    i = bt.request_ids.index(a)
+    assert bt.input_ids[i] == [5] * 16 + [7] == rows[i][1] and bt.positions[i] == 0
 
 
 # ---- compaction moves data the way copy_blocks does ----------------------------
