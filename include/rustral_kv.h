@@ -137,6 +137,27 @@ int rkv_decode_attention(float* out, const float* q, const void* k_pool, const v
                          int max_context, float scale, int dtype, int partition_size,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* rkv_decode_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: its
+ * attention allocates freely.  The split-K partials live in a 16 MiB array
+ * the library keeps on each GPU it runs on (rkv_decode_noalloc_max_bytes());
+ * a call whose partials (rkv_decode_workspace_bytes) exceed it fails with
+ * RKV_ERR_WORKSPACE.  The call allocates nothing: no hipMalloc, no library
+ * allocator.  The array is shared by every call on one GPU and keeps the
+ * last call's contents, so calls that overlap on one GPU (concurrent streams
+ * or threads) race; serialise them on one stream.  Same arguments and result
+ * as rkv_decode_attention otherwise. */
+int rkv_decode_attention_noalloc(float* out, const float* q, const void* k_pool,
+                                 const void* v_pool, const int32_t* block_tables,
+                                 int max_blocks_per_seq, const int32_t* ctx_lens, int num_seqs,
+                                 int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                                 int64_t num_blocks, int max_context, float scale, int dtype,
+                                 int partition_size, void* stream);
+
+/* Size in bytes of the per-GPU scratch of rkv_decode_attention_noalloc. */
+size_t rkv_decode_noalloc_max_bytes(void);
+
 /* The two passes of rkv_decode_attention as separate launches, for callers
  * that schedule them apart (and for per-kernel timing).  Same arguments;
  * pass 1 writes finished rows for single-partition sequences and partials

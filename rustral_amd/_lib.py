@@ -28,6 +28,9 @@ SIGNATURES = {
     "rkv_decode_partition_size": (_i, [_i, _i, _i]),
     "rkv_decode_attention": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64, _i, _f,
                                   _i, _i, _p, _sz, _p]),
+    "rkv_decode_attention_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,
+                                          _i, _f, _i, _i, _p]),
+    "rkv_decode_noalloc_max_bytes": (_sz, []),
     "rkv_decode_attention_partitions": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
                                              _i64, _i, _f, _i, _i, _p, _sz, _p]),
     "rkv_decode_attention_merge": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),

@@ -34,6 +34,8 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 namespace rkv {
@@ -1181,6 +1183,85 @@ extern "C" int rkv_decode_attention(float* out, const float* q, const void* k_po
   return rkv_decode_attention_merge(out, ctx_lens, max_blocks_per_seq, num_seqs, num_q_heads,
                                     head_dim, block_size, max_context, dtype, partition_size,
                                     workspace, workspace_bytes, stream);
+}
+
+// ---- the entry point that allocates nothing -----------------------------------
+// Callers that cannot allocate device memory (code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc) get the split-K
+// partials from a file-scope device array instead of a workspace argument.
+// Every GPU the library runs on holds its own copy until the process ends.
+// Its address on a device comes from hipGetSymbolAddress (the array's name in
+// host code is only a stand-in for the symbol), taken once per device with
+// that device current and kept.
+constexpr size_t kScratchBytes = size_t(16) << 20;  // 16 MiB
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's device address on the device that owns `stream`.
+int scratch_for(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  if (stream) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess)
+      return fail(RKV_ERR_HIP, "rkv_decode_attention_noalloc: hipStreamGetDevice failed");
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return fail(RKV_ERR_HIP, "rkv_decode_attention_noalloc: hipGetDevice failed");
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(RKV_ERR_UNSUPPORTED, "rkv_decode_attention_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess)
+      return fail(RKV_ERR_HIP, "rkv_decode_attention_noalloc: hipGetDevice failed");
+    if (cur != dev && hipSetDevice(dev) != hipSuccess)
+      return fail(RKV_ERR_HIP, "rkv_decode_attention_noalloc: hipSetDevice failed");
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return fail(RKV_ERR_HIP, std::string("rkv_decode_attention_noalloc: hipGetSymbolAddress: ") +
+                                   hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return RKV_OK;
+}
+}  // namespace
+
+extern "C" size_t rkv_decode_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int rkv_decode_attention_noalloc(float* out, const float* q, const void* k_pool,
+                                            const void* v_pool, const int32_t* block_tables,
+                                            int max_blocks_per_seq, const int32_t* ctx_lens,
+                                            int num_seqs, int num_q_heads, int num_kv_heads,
+                                            int head_dim, int block_size, int64_t num_blocks,
+                                            int max_context, float scale, int dtype,
+                                            int partition_size, void* stream) {
+  clear_error();
+  const int P = part_size(dtype);
+  if (partition_size > 0 && partition_size != P)
+    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
+  const int cap = ctx_cap_of(max_context < 0 ? 0 : max_context, max_blocks_per_seq < 0 ? 0 : max_blocks_per_seq,
+                             block_size);
+  const int max_parts = cap <= 0 ? 1 : (cap + P - 1) / P;
+  const size_t need = (num_seqs > 0 && num_q_heads > 0 && head_dim > 0)
+                          ? ws_bytes(num_seqs, num_q_heads, head_dim, max_parts)
+                          : 0;
+  if (need > kScratchBytes)
+    return fail(RKV_ERR_WORKSPACE,
+                "rkv_decode_attention_noalloc: split-K partials need " + std::to_string(need) +
+                    " bytes, above the 16 MiB scratch (use rkv_decode_attention with a workspace)");
+  void* ws = nullptr;
+  if (need > 0)
+    if (int rc = scratch_for(static_cast<hipStream_t>(stream), &ws)) return rc;
+  return rkv_decode_attention(out, q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
+                              num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                              num_blocks, max_context, scale, dtype, partition_size, ws,
+                              need > 0 ? kScratchBytes : 0, stream);
 }
 
 extern "C" int rkv_decode_attention_q(float* out, const float* q, const void* k_pool,

@@ -117,3 +117,15 @@ def test_linear_rejects_rows_too_wide_for_staging():
     L = _lib.lib()
     assert L.rkv_linear(16, 16, 16, None, 1, 8193, 4, None) == RKV_ERR_UNSUPPORTED
     assert "in_dim" in L.rkv_last_error().decode()
+
+
+def test_noalloc_decode_refuses_partials_above_its_scratch():
+    """rkv_decode_attention_noalloc checks the size on the host, before any
+    HIP call: partials above its fixed scratch are RKV_ERR_WORKSPACE."""
+    L = _lib.lib()
+    cap = L.rkv_decode_noalloc_max_bytes()
+    assert cap == 16 << 20
+    assert L.rkv_decode_workspace_bytes(4096, 32, 128, 4096, 0) > cap
+    rc = L.rkv_decode_attention_noalloc(16, 16, 16, 16, 16, 256, 16, 4096, 32, 8, 128, 16, 10,
+                                        4096, 0.1, RKV_BF16, 0, None)
+    assert rc == RKV_ERR_WORKSPACE and b"16 MiB" in L.rkv_last_error()
