@@ -296,6 +296,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     }
   }
 
+
+
   L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
   const int nparts = (L + P - 1) / P;
   if (L == 0) {
@@ -306,14 +308,17 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   if (part >= nparts) return;
 
   // Tile i of the partition is block lb0 + i.  A tile past the context, or
-  // with an invalid id, re-reads tile 0 (an L2 hit) and is masked.
-  const int32_t pb0 = (pb[0] >= 0 && pb[0] < num_blocks) ? pb[0] : 0;
+  // with an invalid id, re-reads tile 0 (an L2 hit) and is masked.  Block ids
+  // are int32, so validity is one unsigned compare against the pool size
+  // clamped to 2^31 - 1.
+  const uint32_t nb32 = num_blocks > 0x7fffffff ? 0x7fffffffu : (uint32_t)num_blocks;
+  const int32_t pb0 = (uint32_t)pb[0] < nb32 ? pb[0] : 0;
   int64_t base[NTW];  // wave-uniform element offset of each (block, head) tile
   bool ok[NTW], full[NTW];
 #pragma unroll
   for (int i = 0; i < NTW; ++i) {
     const int tbase = (lb0 + i) * BS;
-    ok[i] = tbase < L && pb[i] >= 0 && pb[i] < num_blocks;
+    ok[i] = tbase < L && (uint32_t)pb[i] < nb32;
     full[i] = ok[i] && tbase + BS <= L;
     base[i] = ((int64_t)(ok[i] ? pb[i] : pb0) * num_kv_heads + kh) * BS * D;
   }
@@ -331,7 +336,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     const int step = t < NTW ? KSTEP : VSTEP;
 #pragma unroll
     for (int n = 0; n < NL; ++n)
-      ring[t][n] = *reinterpret_cast<const uint4*>(pool + base[t % NTW] + n * step);
+      ring[t][n] = load_stream(pool + base[t % NTW] + n * step);
   }
 
   // 1-byte pools: the K scale of this lane's token in each K tile (MFMA column
@@ -352,8 +357,12 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     }
   }
 
-  // MFMA A operands: q split into bf16 hi + lo rows (after the ring loads
-  // are issued, so the conversion overlaps them), two values per
+  // q was requested before the ring and is converted after it: the barrier
+  // keeps the conversion (which waits for q) below the ring's requests --
+  // without it the scheduler interleaves the two and the first tile is not
+  // requested until q has arrived.
+  __builtin_amdgcn_sched_barrier(0);
+  // MFMA A operands: q split into bf16 hi + lo rows, two values per
   // v_cvt_pk_bf16_f32 (round to nearest even, no branch)
   uint4 qa[MFMA ? NC : 1];
   if constexpr (MFMA) {
@@ -405,7 +414,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
                                                           sacc, 0, 0, 0);
         }
         // dot * scale (the reference's order), then the token's K row scale
-        const float qs = QNT ? q_scale * ksc[i] : q_scale;
+        float qs = q_scale;
+        if constexpr (QNT) qs *= ksc[i];
         const int tp = i * BS + kt;  // token of this lane's column
         const bool valid = ok[i] && (tok0 + tp < L);
         if constexpr (G == 1) {
@@ -619,7 +629,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
       __builtin_amdgcn_s_setprio(3);
 #pragma unroll
       for (int n = 0; n < NL; ++n)
-        tile[n] = *reinterpret_cast<const uint4*>(pool + base[tn % NTW] + n * step);
+        tile[n] = load_stream(pool + base[tn % NTW] + n * step);
       __builtin_amdgcn_s_setprio(0);
     }
     // keep the ring a ring: the scheduler may not hoist later refills above
@@ -872,6 +882,93 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge_kernel(
   }
 }
 
+// Merge for calls with at most kMergeRowsMaxParts partitions per sequence
+// (max_context <= 8 partitions: configs[2] and most decode batches).  One
+// wave per (sequence, query head), four per workgroup, no LDS and no
+// barrier: lane l holds float4 c = l % (D/4) of partition rows
+// p = l / (D/4) + RPW j, and the rows meet through cross-lane reductions.
+// The length and every row the call could have written are requested
+// together (rows at or past the sequence's partition count hold stale bytes
+// from earlier calls and are removed by selects, never multiplied), so the
+// wave waits on memory once.
+constexpr int kMergeRowsMaxParts = 8;
+
+// Reduction over the RPW lanes l, l + V4, l + 2 V4, ... (same column c).
+template <int V4, bool MAX>
+__device__ __forceinline__ float rows_reduce(float x) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if constexpr (V4 <= 8) x = op(x, dpp<0x128>(x));  // lane l ^ 8 inside a 16-lane row
+  if constexpr (V4 <= 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_merge_rows_kernel(
+    float* __restrict__ out, const float* __restrict__ part_acc,
+    const float* __restrict__ part_ml, const int32_t* __restrict__ ctx_lens, int ctx_cap,
+    int num_q_heads, int P, int max_parts, int n_rows) {
+  constexpr int V4 = D / 4, RPW = 64 / V4, J = kMergeRowsMaxParts / RPW;
+  static_assert(RPW >= 2 && J >= 1, "head_dim 32, 64 or 128");
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);  // sequence * num_q_heads + head
+  if (row >= n_rows) return;
+  const int b = row / num_q_heads;
+  int L = ctx_lens[b];
+  const int r = lane / V4, c = lane % V4;
+  const int64_t row0 = (int64_t)row * max_parts;
+  float4 a[J];
+  float2 ml[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int p = r + RPW * j;
+    if (p < max_parts) {
+      a[j] = *reinterpret_cast<const float4*>(part_acc + (row0 + p) * D + 4 * c);
+      ml[j] = *reinterpret_cast<const float2*>(part_ml + (row0 + p) * 2);
+    } else {
+      a[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      ml[j] = make_float2(-INFINITY, 0.0f);
+    }
+  }
+  L = L < 0 ? 0 : (L > ctx_cap ? ctx_cap : L);
+  const int np = (L + P - 1) / P;
+  if (np <= 1) return;  // finished by the partition pass
+  float m[J], M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    m[j] = r + RPW * j < np ? ml[j].x : -INFINITY;
+    M = fmaxf(M, m[j]);
+  }
+  M = rows_reduce<V4, true>(M);
+  float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float den = 0.0f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const bool use = m[j] != -INFINITY;  // a written row of a partition with a valid token
+    const float w = use ? exp2f(m[j] - M) : 0.0f;
+    const float4 x = use ? a[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    num.x = fmaf(w, x.x, num.x);
+    num.y = fmaf(w, x.y, num.y);
+    num.z = fmaf(w, x.z, num.z);
+    num.w = fmaf(w, x.w, num.w);
+    den = fmaf(w, use ? ml[j].y : 0.0f, den);
+  }
+  num.x = rows_reduce<V4, false>(num.x);
+  num.y = rows_reduce<V4, false>(num.y);
+  num.z = rows_reduce<V4, false>(num.z);
+  num.w = rows_reduce<V4, false>(num.w);
+  den = rows_reduce<V4, false>(den);
+  if (r == 0) {
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    *reinterpret_cast<float4*>(out + (int64_t)row * D + 4 * c) =
+        den > 0.0f ? make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
 // ---- dispatch ----------------------------------------------------------------
 
 constexpr int kBS = 16;
@@ -890,12 +987,12 @@ constexpr int kBS = 16;
 #ifndef RKV_DECODE_RING_LOADS_Q  // 1-byte pools (more registers per tile)
 #define RKV_DECODE_RING_LOADS_Q 8
 #endif
-// bf16 pools at head_dim 128: bytes of unused dynamic LDS per workgroup
-// (39 -> 53 KiB) so that three workgroups (not four) share a CU; with four,
-// the partition kernel runs ~2% slower at configs[2], while the 1-byte
-// kernels gain from four.
+// bf16 pools at head_dim 128: bytes of unused dynamic LDS per workgroup,
+// a knob on how many workgroups share a CU (39 KiB each: four).  With the
+// streaming (nontemporal) K/V loads, four per CU beat three (14 KiB of
+// padding) by ~2% at configs[2]; with ordinary loads it was the reverse.
 #ifndef RKV_DECODE_LDS_PAD_16
-#define RKV_DECODE_LDS_PAD_16 14336
+#define RKV_DECODE_LDS_PAD_16 0
 #endif
 // 1-byte pools carry half the bytes per token: their own partition size and
 // waves per partition.
@@ -1081,6 +1178,25 @@ int launch_merge(float* out, const int32_t* ctx_lens, int num_seqs, int num_q_he
   if (max_parts <= 1 || num_seqs == 0) return RKV_OK;
   float *acc = nullptr, *ml = nullptr;
   split_ws(ws, num_seqs, num_q_heads, head_dim, max_parts, acc, ml);
+  if (max_parts <= kMergeRowsMaxParts && (int64_t)num_seqs * num_q_heads <= (1 << 28)) {
+    const int n_rows = num_seqs * num_q_heads;
+    const unsigned nwg = (unsigned)((n_rows + 3) / 4);
+    switch (head_dim) {
+      case 32:
+        decode_merge_rows_kernel<32><<<nwg, 256, 0, stream>>>(out, acc, ml, ctx_lens, cap,
+                                                              num_q_heads, P, max_parts, n_rows);
+        break;
+      case 64:
+        decode_merge_rows_kernel<64><<<nwg, 256, 0, stream>>>(out, acc, ml, ctx_lens, cap,
+                                                              num_q_heads, P, max_parts, n_rows);
+        break;
+      default:
+        decode_merge_rows_kernel<128><<<nwg, 256, 0, stream>>>(out, acc, ml, ctx_lens, cap,
+                                                               num_q_heads, P, max_parts, n_rows);
+        break;
+    }
+    return check_launch("decode_merge_rows_kernel");
+  }
   dim3 grid((unsigned)num_q_heads, (unsigned)num_seqs);
   const size_t lds = (size_t)max_parts * sizeof(float);
   switch (head_dim) {
