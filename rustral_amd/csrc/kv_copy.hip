@@ -12,29 +12,63 @@
 namespace rkv {
 namespace {
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// Load / store policy: 1 = nontemporal (streaming) hint.  Measured on
+// configs[1]-sized calls (65,536-block pools, GB/s of algorithmic bytes):
+//   gather bf16 -> bf16: plain 5155, nt loads 5387, nt stores 5705, both 6066
+//   gather bf16 -> fp32: plain 4972, nt loads 5197, nt stores 3536 (the two
+//                        16-byte stores of a lane's 8 floats are not a
+//                        contiguous wave store; as streaming stores they lose
+//                        the L2 write combining)
+//   gather fp32 -> fp32: plain 5344, nt loads 5114, both 5277
+//   copy_blocks: 5082 - 5177 for every policy
+// so the gather streams its loads for 16-bit pools and its stores for
+// 16-bit outputs (RKV_GATHER_NT = 0 turns both off), and copy_blocks streams
+// both.
+#ifndef RKV_GATHER_NT
+#define RKV_GATHER_NT 1
+#endif
+#ifndef RKV_COPY_NTL
+#define RKV_COPY_NTL 1
+#endif
+#ifndef RKV_COPY_NTS
+#define RKV_COPY_NTS 1
+#endif
+#ifndef RKV_APPEND_NTL
+#define RKV_APPEND_NTL 0
+#endif
+#ifndef RKV_APPEND_NTS
+#define RKV_APPEND_NTS 0
+#endif
 
-// 16-byte store of the bits of v (any 16-byte trivially copyable type).
-// (Non-temporal stores were measured: +3% on the bf16 gather, -34% on the
-// fp32-output gather; plain stores are kept.)
-template <typename V>
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  if constexpr (NT) return load_stream(p);
+  else return *static_cast<const uint4*>(p);
+}
+
+// 16-byte store of the bits of v (any 16-byte trivially copyable type),
+// optionally with the nontemporal hint.
+template <bool NT = false, typename V>
 __device__ __forceinline__ void store16(void* p, const V& v) {
   static_assert(sizeof(V) == 16, "16-byte store");
-  *static_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
+  if constexpr (NT) __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), static_cast<u32x4_t*>(p));
+  else *static_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
 }
 
 struct alignas(16) F8 {  // 8 floats = 32 bytes
   float4 a, b;
 };
 
+template <bool NT = false>
 __device__ __forceinline__ F8 load_f8(const float* p) {
-  const float4* v = reinterpret_cast<const float4*>(p);
-  return F8{v[0], v[1]};
+  const uint4 a = ld16<NT>(p), b = ld16<NT>(p + 4);
+  return F8{__builtin_bit_cast(float4, a), __builtin_bit_cast(float4, b)};
 }
 
+template <bool NT = false>
 __device__ __forceinline__ void store_f8(float* p, const F8& x) {
-  store16(p, x.a);
-  store16(p + 4, x.b);
+  store16<NT>(p, x.a);
+  store16<NT>(p + 4, x.b);
 }
 
 __device__ __forceinline__ uint4 f8_to_bf16x8(const F8& x) {
@@ -72,18 +106,18 @@ __global__ __launch_bounds__(256) void append_kernel(
     const int64_t dst =
         layer * pool_layer_stride + ((blk * num_kv_heads + h) * block_size + row) * head_dim + c * 8;
     if constexpr (BF16) {
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(k_pool) + dst) = f8_to_bf16x8(k);
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(v_pool) + dst) = f8_to_bf16x8(v);
+      store16<RKV_APPEND_NTS>(static_cast<uint16_t*>(k_pool) + dst, f8_to_bf16x8(k));
+      store16<RKV_APPEND_NTS>(static_cast<uint16_t*>(v_pool) + dst, f8_to_bf16x8(v));
     } else {
-      store_f8(static_cast<float*>(k_pool) + dst, k);
-      store_f8(static_cast<float*>(v_pool) + dst, v);
+      store_f8<RKV_APPEND_NTS>(static_cast<float*>(k_pool) + dst, k);
+      store_f8<RKV_APPEND_NTS>(static_cast<float*>(v_pool) + dst, v);
     }
   };
   const int u0 = threadIdx.x;
   F8 k0, v0;
   if (u0 < units) {
-    k0 = load_f8(k_new + src_of(u0));
-    v0 = load_f8(v_new + src_of(u0));
+    k0 = load_f8<RKV_APPEND_NTL>(k_new + src_of(u0));
+    v0 = load_f8<RKV_APPEND_NTL>(v_new + src_of(u0));
   }
   const int64_t slot = slot_mapping[t];
   if (slot < 0 || slot >= num_slots) return;  // padding or out-of-range slot
@@ -91,8 +125,8 @@ __global__ __launch_bounds__(256) void append_kernel(
   const int64_t row = slot - blk * block_size;
   if (u0 < units) put(u0, blk, row, k0, v0);
   for (int u = u0 + blockDim.x; u < units; u += blockDim.x) {
-    const F8 k = load_f8(k_new + src_of(u));
-    const F8 v = load_f8(v_new + src_of(u));
+    const F8 k = load_f8<RKV_APPEND_NTL>(k_new + src_of(u));
+    const F8 v = load_f8<RKV_APPEND_NTL>(v_new + src_of(u));
     put(u, blk, row, k, v);
   }
 }
@@ -139,6 +173,8 @@ __global__ __launch_bounds__(256) void gather_kernel(
   // before the first store, so a thread keeps UNR loads in flight.
   constexpr int UNR = 8;
   using In = typename std::conditional<sizeof(TIn) == 2, uint4, F8>::type;
+  constexpr bool NTL = RKV_GATHER_NT && sizeof(TIn) == 2;
+  constexpr bool NTS = RKV_GATHER_NT && sizeof(TIn) == 2 && sizeof(TOut) == 2;
   for (int u0 = threadIdx.x; u0 < units; u0 += UNR * blockDim.x) {
     In x[UNR];
 #pragma unroll
@@ -148,9 +184,9 @@ __global__ __launch_bounds__(256) void gather_kernel(
         const int h = u / per_head, r = u - h * per_head;
         const TIn* s = src_pool + ((int64_t)blk * num_kv_heads + h) * block_size * head_dim + r * 8;
         if constexpr (sizeof(TIn) == 2)
-          x[k] = *reinterpret_cast<const uint4*>(s);
+          x[k] = ld16<NTL>(s);
         else
-          x[k] = load_f8(reinterpret_cast<const float*>(s));
+          x[k] = load_f8<false>(reinterpret_cast<const float*>(s));
       }
     }
 #pragma unroll
@@ -160,11 +196,11 @@ __global__ __launch_bounds__(256) void gather_kernel(
         const int h = u / per_head, r = u - h * per_head;
         TOut* d = dst_all + seq_base + ((int64_t)h * row_stride + p0) * head_dim + r * 8;
         if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 2)
-          store16(d, x[k]);
+          store16<NTS>(d, x[k]);
         else if constexpr (sizeof(TIn) == 2)
-          store_f8(reinterpret_cast<float*>(d), bf16x8_to_f8(x[k]));
+          store_f8<false>(reinterpret_cast<float*>(d), bf16x8_to_f8(x[k]));
         else
-          store_f8(reinterpret_cast<float*>(d), x[k]);
+          store_f8<false>(reinterpret_cast<float*>(d), x[k]);
       }
     }
   }
@@ -188,12 +224,12 @@ __global__ __launch_bounds__(256) void copy_blocks_kernel(
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
       const int64_t u = u0 + k * blockDim.x;
-      if (u < n) x[k] = s[u];
+      if (u < n) x[k] = ld16<RKV_COPY_NTL>(s + u);
     }
 #pragma unroll
     for (int k = 0; k < UNR; ++k) {
       const int64_t u = u0 + k * blockDim.x;
-      if (u < n) store16(d + u, x[k]);
+      if (u < n) store16<RKV_COPY_NTS>(d + u, x[k]);
     }
   }
 }
