@@ -154,6 +154,43 @@ int rkv_decoder_load_safetensors(const rkv_decoder_config* cfg, const char* path
 int rkv_decoder_save_safetensors(const rkv_decoder_config* cfg, const float* host_params,
                                  int64_t n_params, const char* path);
 
+/* The same strict load straight into a decoder's device parameters (one
+ * host-to-device copy per tensor from the memory-mapped file, on the
+ * decoder's stream; returns once they are done).  On an error the decoder's
+ * parameters are unchanged unless the failure is a HIP copy error. */
+int rkv_decoder_load_safetensors_device(rkv_decoder* dec, const char* path);
+
+/* rkv_decoder_create with the parameters read from a safetensors file
+ * straight into device memory (no host parameter array).  NULL on failure
+ * (rkv_last_error carries load_model's message). */
+rkv_decoder* rkv_decoder_create_from_safetensors(const rkv_decoder_config* cfg,
+                                                 const char* path, void* stream);
+
+/* ---- any named-parameter model in a safetensors file --------------------------
+ * The reference's load_model (crates/runtime/src/model_io.rs:36-105) loads
+ * every NamedParameters model the same way; these calls give a caller (the
+ * Rust backend, a Llama layer's projections) that load for its own list of
+ * names, shapes and destinations.  rkv_st_open maps the file read-only and
+ * checks its header (JSON object; every entry with a dtype string, integer
+ * shape, data_offsets inside the data section and matching the element count
+ * for the known dtypes); NULL on failure. */
+typedef struct rkv_st_file rkv_st_file;
+rkv_st_file* rkv_st_open(const char* path);
+void rkv_st_close(rkv_st_file* f);
+int64_t rkv_st_num_tensors(const rkv_st_file* f);
+/* Entry i in header order: name and dtype strings (valid until rkv_st_close),
+ * number of dimensions, and up to max_dims sizes. */
+int rkv_st_tensor(const rkv_st_file* f, int64_t i, const char** name, const char** dtype,
+                  int* ndim, int64_t* shape, int max_dims);
+/* load_model's strict load: n tensors names[i] with ndims[i] dimensions
+ * (shapes concatenated in order), each F32, copied into dsts[i] -- device
+ * pointers when dst_on_device (hipMemcpyAsync on stream, finished before the
+ * call returns), else host pointers.  Missing keys, keys of the file not in
+ * the list, a shape mismatch or another dtype are RKV_ERR_INVALID_ARG with
+ * the reference's message. */
+int rkv_st_load(const rkv_st_file* f, int n, const char* const* names, const int* ndims,
+                const int64_t* shapes, void* const* dsts, int dst_on_device, void* stream);
+
 /* ---- serving engine (continuous batching over the decoder) ----------------------
  * Replaces ServingEngine (crates/nn/src/continuous_batching.rs:493-537).  The
  * reference's step emits a dummy token for every scheduled request

@@ -90,6 +90,14 @@ SIGNATURES = {
     "rkv_decoder_generate": (_i, [_p, _p, _i, _i, _p, _p]),
     "rkv_decoder_load_safetensors": (_i, [_p, C.c_char_p, _p, _i64]),
     "rkv_decoder_save_safetensors": (_i, [_p, _p, _i64, C.c_char_p]),
+    "rkv_decoder_load_safetensors_device": (_i, [_p, C.c_char_p]),
+    "rkv_decoder_create_from_safetensors": (_p, [_p, C.c_char_p, _p]),
+    "rkv_st_open": (_p, [C.c_char_p]),
+    "rkv_st_close": (None, [_p]),
+    "rkv_st_num_tensors": (_i64, [_p]),
+    "rkv_st_tensor": (_i, [_p, _i64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p),
+                           C.POINTER(C.c_int), _p, _i]),
+    "rkv_st_load": (_i, [_p, _i, _p, _p, _p, _p, _i, _p]),
     "rkv_engine_create": (_p, [_p, _p, _i64, _i64, _i, _p]),
     "rkv_engine_destroy": (None, [_p]),
     "rkv_engine_submit": (_i64, [_p, _p, _i, _i, _i]),

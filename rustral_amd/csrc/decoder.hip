@@ -22,6 +22,7 @@
 #include "../../include/rustral_serving.h"
 #include "model_layout.hpp"
 #include "model_ops.hpp"
+#include "safetensors.hpp"
 
 // ---- generator -------------------------------------------------------------------
 
@@ -168,6 +169,19 @@ void release(rkv_decoder* dec) {
 
 extern "C" void rkv_decoder_destroy(rkv_decoder* dec) { release(dec); }
 
+namespace rkv {
+int copy_tensors(const st::File& f, const std::vector<const st::Tensor*>& found,
+                 const std::vector<void*>& dsts, bool on_device, hipStream_t stream,
+                 const char* what);
+}  // namespace rkv
+
+namespace {
+// Allocates a decoder; uploads host_params unless it is NULL (the caller then
+// fills dec->params itself, as the safetensors loader does).
+rkv_decoder* create(const rkv_decoder_config* cfg, const float* host_params, int64_t n_params,
+                    void* stream);
+}  // namespace
+
 extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const float* host_params,
                                            int64_t n_params, void* stream) {
   clear_error();
@@ -175,6 +189,45 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
     set_error("rkv_decoder_create: bad configuration or null parameters");
     return nullptr;
   }
+  return create(cfg, host_params, n_params, stream);
+}
+
+extern "C" int rkv_decoder_load_safetensors_device(rkv_decoder* dec, const char* path) {
+  clear_error();
+  if (!dec || !path) return fail(RKV_ERR_INVALID_ARG, "rkv_decoder_load_safetensors_device: bad argument");
+  std::string err;
+  std::unique_ptr<st::File> f = st::open(path, err);
+  if (!f) return fail(RKV_ERR_INVALID_ARG, err);
+  std::vector<int64_t> offsets;
+  const std::vector<st::Want> want = st::decoder_layout(dec->cfg, &offsets);
+  std::vector<const st::Tensor*> found;
+  if (!st::match(*f, want, found, err)) return fail(RKV_ERR_INVALID_ARG, err);
+  std::vector<void*> dst(want.size());
+  for (size_t i = 0; i < want.size(); ++i) dst[i] = dec->params + offsets[i];
+  return copy_tensors(*f, found, dst, true, dec->stream, "rkv_decoder_load_safetensors_device");
+}
+
+extern "C" rkv_decoder* rkv_decoder_create_from_safetensors(const rkv_decoder_config* cfg,
+                                                            const char* path, void* stream) {
+  clear_error();
+  if (!config_ok(cfg) || !path) {
+    set_error("rkv_decoder_create_from_safetensors: bad configuration or null path");
+    return nullptr;
+  }
+  rkv_decoder* dec = create(cfg, nullptr, param_count(*cfg), stream);
+  if (!dec) return nullptr;
+  if (rkv_decoder_load_safetensors_device(dec, path) != RKV_OK) {
+    const std::string msg = rkv_last_error();
+    release(dec);
+    set_error(msg);
+    return nullptr;
+  }
+  return dec;
+}
+
+namespace {
+rkv_decoder* create(const rkv_decoder_config* cfg, const float* host_params, int64_t n_params,
+                    void* stream) {
   const rkv_decoder_config c = *cfg;
   const int dh = c.d_model / c.n_heads;
   if ((dh != 32 && dh != 64 && dh != 128) || (c.n_heads / c.n_kv_heads > 8)) {
@@ -228,8 +281,8 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
     ctx[p] = (int32_t)(p + 1);
   }
   hipStream_t s = dec->stream;
-  ok = hipMemcpyAsync(dec->params, host_params, (size_t)n_params * sizeof(float),
-                      hipMemcpyHostToDevice, s) == hipSuccess &&
+  ok = (!host_params || hipMemcpyAsync(dec->params, host_params, (size_t)n_params * sizeof(float),
+                                       hipMemcpyHostToDevice, s) == hipSuccess) &&
        hipMemcpyAsync(dec->pe, pe.data(), pe.size() * sizeof(float), hipMemcpyHostToDevice, s) ==
            hipSuccess &&
        hipMemcpyAsync(dec->pos, pos.data(), S * sizeof(int32_t), hipMemcpyHostToDevice, s) ==
@@ -245,6 +298,7 @@ extern "C" rkv_decoder* rkv_decoder_create(const rkv_decoder_config* cfg, const 
   }
   return dec;
 }
+}  // namespace
 
 namespace {
 

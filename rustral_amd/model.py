@@ -77,18 +77,98 @@ def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
     return out
 
 
-class Decoder:
-    """Greedy decoder on the current device (rkv_decoder_*)."""
+class SafetensorsFile:
+    """A memory-mapped safetensors file (rkv_st_*): its entries, and the
+    strict load of the reference's load_model into host arrays or device
+    tensors."""
 
-    def __init__(self, cfg: DecoderConfig, params: np.ndarray, device=None):
-        params = np.ascontiguousarray(params, np.float32)
-        dev = torch.device("cuda:0") if device is None else torch.device(device)
-        self._stream = torch.cuda.current_stream(dev).cuda_stream
-        self.cfg = cfg
-        h = lib().rkv_decoder_create(C.byref(cfg), _p(params), params.size, self._stream)
+    def __init__(self, path):
+        h = lib().rkv_st_open(str(path).encode())
         if not h:
             raise RkvError(-1, lib().rkv_last_error().decode())
         self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().rkv_st_close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def entries(self) -> dict:
+        """name -> (dtype, shape) in header order."""
+        out = {}
+        for i in range(lib().rkv_st_num_tensors(self._h)):
+            name, dt, nd = C.c_char_p(), C.c_char_p(), C.c_int()
+            shape = (C.c_int64 * 8)()
+            check(lib().rkv_st_tensor(self._h, i, C.byref(name), C.byref(dt), C.byref(nd),
+                                      C.cast(shape, C.c_void_p), 8))
+            out[name.value.decode()] = (dt.value.decode(), tuple(shape[:nd.value]))
+        return out
+
+    def load(self, dsts: dict) -> None:
+        """Strict load (every name of the file, F32, equal shapes) into the
+        given destinations: name -> float32 numpy array (host) or contiguous
+        float32 device tensor; all of one kind."""
+        names = list(dsts)
+        on_dev = [isinstance(dsts[n], torch.Tensor) for n in names]
+        if any(on_dev) and not all(on_dev):
+            raise ValueError("destinations must be all host arrays or all device tensors")
+        dev = bool(names) and on_dev[0]
+        ptrs, dims, shapes = [], [], []
+        for n in names:
+            t = dsts[n]
+            if dev:
+                _dev(t, n, torch.float32)
+                ptrs.append(t.data_ptr())
+            else:
+                if t.dtype != np.float32 or not t.flags["C_CONTIGUOUS"] or not t.flags["WRITEABLE"]:
+                    raise ValueError(f"{n}: host destination must be a writable contiguous float32 array")
+                ptrs.append(t.ctypes.data)
+            dims.append(t.dim() if dev else t.ndim)
+            shapes.extend(int(x) for x in t.shape)
+        c_names = (C.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+        c_dims = (C.c_int * max(1, len(dims)))(*dims)
+        c_shapes = (C.c_int64 * max(1, len(shapes)))(*shapes)
+        c_ptrs = (C.c_void_p * max(1, len(ptrs)))(*ptrs)
+        stream = torch.cuda.current_stream(dsts[names[0]].device).cuda_stream if dev else None
+        check(lib().rkv_st_load(self._h, len(names), C.cast(c_names, C.c_void_p),
+                                C.cast(c_dims, C.c_void_p), C.cast(c_shapes, C.c_void_p),
+                                C.cast(c_ptrs, C.c_void_p), int(dev), stream))
+
+
+class Decoder:
+    """Greedy decoder on the current device (rkv_decoder_*)."""
+
+    def __init__(self, cfg: DecoderConfig, params: np.ndarray | None = None, device=None, *,
+                 path=None):
+        """params: the packed host parameter array; or path: a safetensors file
+        loaded strictly straight into device memory."""
+        if (params is None) == (path is None):
+            raise ValueError("give exactly one of params and path")
+        dev = torch.device("cuda:0") if device is None else torch.device(device)
+        self._stream = torch.cuda.current_stream(dev).cuda_stream
+        self.cfg = cfg
+        if path is not None:
+            h = lib().rkv_decoder_create_from_safetensors(C.byref(cfg), str(path).encode(),
+                                                          self._stream)
+        else:
+            params = np.ascontiguousarray(params, np.float32)
+            h = lib().rkv_decoder_create(C.byref(cfg), _p(params), params.size, self._stream)
+        if not h:
+            raise RkvError(-1, lib().rkv_last_error().decode())
+        self._h = h
+
+    def load_safetensors(self, path) -> None:
+        """Replaces the parameters with a safetensors file's (strict load
+        straight into the decoder's device memory)."""
+        check(lib().rkv_decoder_load_safetensors_device(self._h, str(path).encode()))
 
     def __del__(self):
         if getattr(self, "_h", None):

@@ -14,10 +14,8 @@ CFG = dict(vocab=50, d_model=64, n_heads=4, n_kv_heads=2, d_ff=96, n_layers=2, m
 def named(cfg, params):
     """The name -> array view of a packed parameter array, from the names and
     shapes the header documents (an independent walk of the layout)."""
-    c = dict(model.CONFIG0)
-    c.update(CFG)
-    d, V, f, L = c["d_model"], c["vocab"], c["d_ff"], c["n_layers"]
-    kvd = c["n_kv_heads"] * (d // c["n_heads"])
+    d, V, f, L = cfg.d_model, cfg.vocab, cfg.d_ff, cfg.n_layers
+    kvd = cfg.n_kv_heads * (d // cfg.n_heads)
     order = [("token_embedding.weight", (V, d))]
     for i in range(L):
         p = f"layers.{i}."
@@ -107,3 +105,67 @@ def test_loader_rejects_truncated_and_missing_files(cfg, tmp_path):
         model.load_safetensors(cfg, junk)
     with pytest.raises(RkvError, match="cannot open"):
         model.load_safetensors(cfg, tmp_path / "absent.safetensors")
+
+
+# ---- the generic reader (rkv_st_*): any named-parameter model -----------------
+
+def test_reader_lists_entries_like_the_safetensors_package(tmp_path):
+    import torch
+    from safetensors.torch import save_file as save_torch
+    t = {"a.weight": torch.randn(3, 5), "b.half": torch.randn(7).half(),
+         "c.bf16": torch.randn(2, 2, 2).bfloat16(), "d.ids": torch.arange(6, dtype=torch.int64),
+         "e.scalar": torch.tensor(1.5)}
+    path = tmp_path / "mixed.safetensors"
+    save_torch(t, str(path), metadata={"k": "v"})
+    want = {"a.weight": ("F32", (3, 5)), "b.half": ("F16", (7,)), "c.bf16": ("BF16", (2, 2, 2)),
+            "d.ids": ("I64", (6,)), "e.scalar": ("F32", ())}
+    with model.SafetensorsFile(path) as f:
+        assert f.entries() == want
+
+
+def test_generic_load_is_strict_and_exact(tmp_path):
+    rng = np.random.default_rng(0)
+    t = {"model.layers.0.self_attn.q_proj.weight": rng.standard_normal((8, 16), np.float32),
+         "model.layers.0.self_attn.k_proj.weight": rng.standard_normal((4, 16), np.float32),
+         "model.norm.weight": rng.standard_normal(16, np.float32)}
+    path = tmp_path / "layer.safetensors"
+    save_file(t, str(path))
+    with model.SafetensorsFile(path) as f:
+        dst = {k: np.empty_like(v) for k, v in t.items()}
+        f.load(dst)
+        for k in t:
+            assert np.array_equal(dst[k], t[k]), k
+        with pytest.raises(RkvError, match="unexpected extra keys: model.norm.weight"):
+            f.load({k: np.empty_like(v) for k, v in t.items() if k != "model.norm.weight"})
+        with pytest.raises(RkvError, match="missing keys: lm_head.weight"):
+            f.load({**{k: np.empty_like(v) for k, v in t.items()},
+                    "lm_head.weight": np.empty(3, np.float32)})
+        bad = {k: np.empty_like(v) for k, v in t.items()}
+        bad["model.norm.weight"] = np.empty((4, 4), np.float32)
+        with pytest.raises(RkvError, match=r"shape mismatch for 'model.norm.weight': "
+                                           r"expected \[4, 4\], got \[16\]"):
+            f.load(bad)
+
+
+def test_reader_rejects_malformed_headers(tmp_path):
+    def write(header: bytes, body: bytes = b"", name="m.safetensors"):
+        p = tmp_path / name
+        p.write_bytes(len(header).to_bytes(8, "little") + header + body)
+        return p
+    cases = [
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,4]}}', b"\0" * 8, "bad data_offsets"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}', b"\0" * 4, "bad data_offsets"),
+        (b'{"a":{"dtype":"F32","shape":[-2],"data_offsets":[0,8]}}', b"\0" * 8, "bad shape"),
+        (b'{"a":{"dtype":"F32","shape":[2.5],"data_offsets":[0,8]}}', b"\0" * 8, "bad shape"),
+        (b'{"a":{"dtype":"F32","shape":[2]}}', b"\0" * 8, "malformed entry"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]},'
+         b'"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}', b"\0" * 8, "duplicate entry"),
+        (b'[1,2]', b"", "not a JSON object"),
+    ]
+    for i, (h, body, msg) in enumerate(cases):
+        with pytest.raises(RkvError, match=msg):
+            model.SafetensorsFile(write(h, body, f"m{i}.safetensors"))
+    short = tmp_path / "short.safetensors"
+    short.write_bytes(b"\x01\x02")
+    with pytest.raises(RkvError, match="shorter than 8 bytes"):
+        model.SafetensorsFile(short)
