@@ -1,0 +1,194 @@
+"""The Rust crate that binds the library for rustral (rust/rustral-rocm-backend)
+against the C headers, on the CPU (no Rust toolchain here):
+
+* src/ffi.rs declares every function of include/*.h with the same name,
+  arity, integer / float widths and pointer structure (constness and depth,
+  pointee type), and nothing else;
+* build.rs compiles every source the functions are defined in (all .hip and
+  .cpp files of rustral_amd/csrc) with the flags of rustral_amd/build.py;
+* every ffi function the crate calls is declared.
+
+The header parser here is independent of how ffi.rs was written.
+"""
+import os
+import re
+
+import pytest
+
+from rustral_amd import build as B
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CRATE = os.path.join(ROOT, "rust", "rustral-rocm-backend")
+INCLUDE = os.path.join(ROOT, "include")
+
+C_BASE = {"int": "i32", "int32_t": "i32", "int64_t": "i64", "uint64_t": "u64", "size_t": "usize",
+          "float": "f32", "double": "f64", "char": "i8", "void": "void"}
+RUST_BASE = {"c_int": "i32", "i32": "i32", "i64": "i64", "u64": "u64", "usize": "usize", "f32": "f32",
+             "f64": "f64", "c_char": "i8", "c_void": "void"}
+
+
+def camel(c_name: str) -> str:
+    return "".join(p.capitalize() for p in c_name.split("_"))
+
+
+def c_type(text: str):
+    """Canonical form of a C type: (base, [pointee constness, outer first])."""
+    t = text.replace("struct ", "").replace("*", " * ").split()
+    quals, base, const = [], None, False
+    for tok in t:
+        if tok == "const":
+            const = True
+        elif tok == "*":
+            quals.append(const)      # constness of what this pointer points to
+            const = False            # a const after '*' qualifies the pointer itself
+        else:
+            base = tok
+    if base in C_BASE:
+        b = C_BASE[base]
+    else:
+        b = "struct:" + camel(base)
+    return b, list(reversed(quals))
+
+
+def rust_type(text: str):
+    text = text.strip()
+    if text == "Stream":
+        return "void", [False]
+    quals = []
+    while text.startswith("*"):
+        m = re.match(r"\*(const|mut)\s+(.*)", text)
+        assert m, text
+        quals.append(m.group(1) == "const")
+        text = m.group(2).strip()
+    b = RUST_BASE.get(text, "struct:" + text)
+    return b, quals
+
+
+def header_protos():
+    out = {}
+    for f in sorted(os.listdir(INCLUDE)):
+        if not f.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, f)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"^\s*#.*$", "", text, flags=re.M)
+        for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(rkv_\w+)\s*\(([^;{)]*)\)\s*;", text):
+            ret, name, args = m.group(1), m.group(2), m.group(3).strip()
+            params = []
+            if args and args != "void":
+                for a in args.split(","):
+                    a = " ".join(a.split())
+                    pm = re.match(r"(.*?)(\w+)$", a)
+                    params.append((pm.group(2), c_type(pm.group(1))))
+            out[name] = (c_type(ret), params)
+    return out
+
+
+def ffi_protos():
+    text = open(os.path.join(CRATE, "src", "ffi.rs")).read()
+    block = text[text.index('extern "C" {'):text.index("pub mod hip")]
+    out = {}
+    for m in re.finditer(r"pub fn (rkv_\w+)\s*\((.*?)\)\s*(->\s*([^;]+))?;", block, re.S):
+        name, args, ret = m.group(1), m.group(2), m.group(4)
+        params = []
+        for a in [x.strip() for x in args.split(",") if x.strip()]:
+            pn, ty = a.split(":", 1)
+            params.append((pn.strip().rstrip("_"), rust_type(ty)))
+        out[name] = (rust_type(ret) if ret else ("void", []), params)
+    return out
+
+
+def test_parsers_read_every_declaration():
+    h, r = header_protos(), ffi_protos()
+    assert len(h) >= 76 and len(r) >= 76
+    assert c_type("const char* const*") == ("i8", [True, True])
+    assert c_type("void* const*") == ("void", [True, False])
+    assert c_type("const char**") == ("i8", [False, True])
+    assert rust_type("*mut *const c_char") == ("i8", [False, True])
+
+
+def test_ffi_declares_every_header_function_with_matching_types():
+    h, r = header_protos(), ffi_protos()
+    assert sorted(h) == sorted(r), (sorted(set(h) - set(r)), sorted(set(r) - set(h)))
+    for name, (ret, params) in h.items():
+        rret, rparams = r[name]
+        assert ret == rret, f"{name}: return {ret} vs {rret}"
+        assert len(params) == len(rparams), f"{name}: arity {len(params)} vs {len(rparams)}"
+        for (pn, pt), (rn, rt) in zip(params, rparams):
+            assert pn == rn, f"{name}: parameter {pn} vs {rn}"
+            assert pt == rt, f"{name}({pn}): C {pt} vs Rust {rt}"
+
+
+def test_ffi_constants_and_config_struct_match_the_headers():
+    text = open(os.path.join(CRATE, "src", "ffi.rs")).read()
+    consts = dict(re.findall(r"pub const (RKV_\w+): \w+ = (-?\d+);", text))
+    hdr = ""
+    for f in os.listdir(INCLUDE):
+        hdr += open(os.path.join(INCLUDE, f)).read()
+    defs = dict(re.findall(r"#define (RKV_\w+) \(?(-?\d+)\)?", hdr))
+    assert defs and set(defs) == set(consts), set(defs) ^ set(consts)
+    for k, v in defs.items():
+        assert consts[k] == v, k
+    fields = re.findall(r"pub (\w+): (c_int|f32),", text[text.index("pub struct RkvDecoderConfig"):])
+    assert [f for f, _ in fields] == ["vocab", "d_model", "n_heads", "n_kv_heads", "d_ff", "n_layers",
+                                      "max_seq", "eps"]
+
+
+def _definitions():
+    """function name -> defining source file of rustral_amd/csrc."""
+    out = {}
+    for f in os.listdir(B.CSRC):
+        text = open(os.path.join(B.CSRC, f)).read()
+        for m in re.finditer(r'extern "C"[^;{(]*?\b(rkv_\w+)\s*\(', text):
+            out[m.group(1)] = f
+    return out
+
+
+def test_build_rs_compiles_every_defining_source_with_the_library_flags():
+    text = open(os.path.join(CRATE, "build.rs")).read()
+    # the source set: every .hip and .cpp file of the directory
+    assert re.search(r'Some\("hip"\)\s*\|\s*Some\("cpp"\)', text)
+    defs = _definitions()
+    for name in header_protos():
+        assert name in defs, f"{name} is not defined in rustral_amd/csrc"
+        assert defs[name].endswith((".hip", ".cpp")), defs[name]
+    assert set(B.sources()) == {os.path.join(B.CSRC, f) for f in os.listdir(B.CSRC)
+                                if f.endswith((".hip", ".cpp"))}
+    # the same device flags as rustral_amd/build.py
+    assert 'const ARCH: &str = "gfx950";' in text
+    for flag in ("-O3", "-std=c++17", "-fPIC"):
+        assert f'"{flag}"' in text and flag in B.HIPCC_FLAGS
+    assert '"-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"' in text
+    for flag in B.CXX_FLAGS:
+        assert f'"{flag}"' in text, flag
+    assert "cargo:rustc-link-lib=dylib=rustral_kv" in text
+
+
+def test_crate_calls_only_declared_functions_and_balances_delimiters():
+    declared = set(ffi_protos())
+    used = set()
+    for root, _, files in os.walk(CRATE):
+        for f in files:
+            if not f.endswith(".rs"):
+                continue
+            text = open(os.path.join(root, f)).read()
+            used |= set(re.findall(r"ffi::(rkv_\w+)", text))
+            code = re.sub(r"//[^\n]*", "", text)
+            code = re.sub(r'"(\\.|[^"\\])*"', '""', code)
+            for a, b in ("()", "[]", "{}"):
+                assert code.count(a) == code.count(b), f"{f}: unbalanced {a}{b}"
+    assert used and used <= declared, used - declared
+
+
+@pytest.mark.parametrize("trait_method", [
+    "fn shape", "fn tensor_from_vec", "fn zeros", "fn matmul", "fn transpose", "fn add",
+    "fn add_row_vector", "fn relu", "fn softmax", "fn log_softmax", "fn argmax", "fn gather_rows",
+    "fn linear", "fn sigmoid", "fn tanh", "fn gelu", "fn mul", "fn dropout", "fn concat", "fn slice",
+    "fn reshape", "fn add_scalar", "fn mul_scalar", "fn broadcast", "fn neg", "fn sub", "fn sqrt",
+    "fn div", "fn exp", "fn log", "fn maximum", "fn gt_scalar", "fn sum_all", "fn sum_dim0",
+    "fn tensor_to_vec", "fn tensor_element"])
+def test_tensor_ops_implements_every_required_method(trait_method):
+    """The 36 required methods of TensorOps (crates/core/src/backend.rs:212-399)."""
+    text = open(os.path.join(CRATE, "src", "ops.rs")).read()
+    impl = text[text.index("impl TensorOps<RocmBackend> for RocmOps"):text.index("impl AttentionOps")]
+    assert re.search(rf"\b{trait_method}\(", impl), trait_method
