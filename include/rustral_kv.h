@@ -107,18 +107,23 @@ int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int 
 
 /* Workspace (bytes) rkv_decode_attention needs for split-K partials.
  * max_context: host-side upper bound on every ctx_lens[b] (for example
- * max_blocks_per_seq*block_size).  partition_size: the size
- * rkv_decode_partition_size returns for the pool dtype, or <= 0 for the
- * smallest partition size of the library (enough for every dtype). */
+ * max_blocks_per_seq*block_size).  partition_size: the size the call will
+ * use (rkv_decode_partition_size), or <= 0 for the library's default at this
+ * max_context (enough for every pool dtype). */
 size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_context,
                                   int partition_size);
 
-/* Partition size (tokens) rkv_decode_attention uses for pools of dtype, for a
- * request of partition_size (<= 0: the library default). */
-int rkv_decode_partition_size(int partition_size, int head_dim, int dtype);
+/* Partition size (tokens) rkv_decode_attention uses for pools of dtype and
+ * this max_context, for a request of partition_size: the request itself when
+ * it is a multiple of 64 tokens (16 tokens x 4 waves) up to 640; for
+ * partition_size <= 0 the default -- 640, and 512 for fp32 / bf16 pools when
+ * max_context exceeds 8192 (long contexts run ~3% faster with 512-token
+ * partitions).  RKV_ERR_UNSUPPORTED for other requests. */
+int rkv_decode_partition_size(int partition_size, int head_dim, int dtype, int max_context);
 
 /* Single-token paged decode attention with GQA (two passes: partitions of
- * partition_size tokens, then a merge; one partition skips the merge).
+ * partition_size tokens -- see rkv_decode_partition_size; <= 0 for the
+ * default -- then a merge; one partition skips the merge).
  * Replaces the per-head recipe of TapeMultiHeadAttention
  * (crates/nn/src/tape_transformer.rs:87-139), for one query token per
  * sequence attending to its whole cache, and AttentionOps

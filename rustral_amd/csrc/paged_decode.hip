@@ -33,6 +33,7 @@
 // softmax uses exp2 (v_exp_f32) directly.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <string>
@@ -160,8 +161,10 @@ __device__ __forceinline__ float lo_col(float x) {
 }
 
 // ---- streaming variant ---------------------------------------------------------
-// SPLIT 64-lane waves own one (partition of NTILE blocks, KV head, sequence)
-// item; wave w streams the NTW = NTILE / SPLIT tiles of its slice -- the K
+// SPLIT 64-lane waves own one (partition, KV head, sequence) item; a
+// partition is SPLIT * tw blocks (tw = tiles_per_wave <= NTW = NTILE / SPLIT,
+// chosen at launch), and wave w streams the tw tiles of its slice (the
+// static loop runs over NTW slots; slots past tw are masked) -- the K
 // tiles, then the V tiles -- through a ring of R register tiles: the loads of
 // tile t + R are issued as soon as tile t has been consumed, so a wave always
 // has R tiles (R KiB x 4 for bf16 D=128) in flight and its arithmetic overlaps
@@ -191,15 +194,16 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     const void* __restrict__ v_pool_, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens, int ctx_cap, int num_kv_heads,
-    int64_t num_blocks, float q_scale, int max_parts) {
+    int64_t num_blocks, float q_scale, int max_parts, int tiles_per_wave) {
   const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
   const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
   constexpr int E = Traits<T>::E;
   constexpr int LPT = D / E;     // lanes per token row
   constexpr int TPL = 64 / LPT;  // token rows per wave-load
   constexpr int NL = BS / TPL;   // wave-loads per tile
-  constexpr int P = NTILE * BS;  // tokens per partition
-  constexpr int NTW = NTILE / SPLIT;  // tiles of the partition this wave streams
+  constexpr int NTW = NTILE / SPLIT;  // tile slots of this wave's slice
+  const int tw = tiles_per_wave;      // tiles of the slice (1 .. NTW)
+  const int P = tw * SPLIT * BS;      // tokens per partition
   constexpr int NT = 2 * NTW;    // tiles streamed: K then V
   static_assert(D % E == 0 && 64 % LPT == 0 && BS % TPL == 0 && R >= 1 && R <= NT,
                 "unsupported tile shape");
@@ -227,7 +231,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 
   // Requests that do not depend on the context length go out first.
   int L = ctx_lens[b];
-  const int lb0 = part * NTILE + sub * NTW;  // first tile (block index) of this wave
+  const int lb0 = (part * SPLIT + sub) * tw;  // first tile (block index) of this wave
   const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
   int32_t pb[NTW];
 #pragma unroll
@@ -318,25 +322,30 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 #pragma unroll
   for (int i = 0; i < NTW; ++i) {
     const int tbase = (lb0 + i) * BS;
-    ok[i] = tbase < L && (uint32_t)pb[i] < nb32;
+    ok[i] = i < tw && tbase < L && (uint32_t)pb[i] < nb32;
     full[i] = ok[i] && tbase + BS <= L;
     base[i] = ((int64_t)(ok[i] ? pb[i] : pb0) * num_kv_heads + kh) * BS * D;
   }
-  // this lane's first element in a tile, and the stride between its loads
-  const T* __restrict__ kl = MFMA ? k_pool + kt * D + (QNT ? (D / 4) * kq : 8 * kq)
-                                  : k_pool + slot * D + dl * E;
-  const T* __restrict__ vl = v_pool + slot * D + dl * E;
-  constexpr int KSTEP = MFMA ? (QNT ? 16 : 32) : TPL * D;
-  constexpr int VSTEP = TPL * D;
+  // This lane's byte offset in a (block, head) tile and the stride between
+  // its loads.  A masked tile re-reads the wave's tile 0 (its streaming
+  // re-reads add ~2% to FETCH_SIZE; masking them with an empty buffer
+  // resource instead removed that traffic but made the kernel ~4% slower).
+  const uint32_t koff = (MFMA ? kt * D + (QNT ? (D / 4) * kq : 8 * kq) : slot * D + dl * E) * sizeof(T);
+  const uint32_t voff = (slot * D + dl * E) * sizeof(T);
+  constexpr uint32_t KSTEP = (MFMA ? (QNT ? 16 : 32) : TPL * D) * sizeof(T);
+  constexpr uint32_t VSTEP = TPL * D * sizeof(T);
+  auto tile_load = [&](int t, int n) __attribute__((always_inline)) {
+    const bool is_k = t < NTW;
+    const int i = t % NTW;
+    return load_stream(reinterpret_cast<const char*>((is_k ? k_pool : v_pool) + base[i]) +
+                       (is_k ? koff : voff) + n * (is_k ? KSTEP : VSTEP));
+  };
 
   uint4 ring[R][NL];
 #pragma unroll
   for (int t = 0; t < R; ++t) {
-    const T* pool = t < NTW ? kl : vl;
-    const int step = t < NTW ? KSTEP : VSTEP;
 #pragma unroll
-    for (int n = 0; n < NL; ++n)
-      ring[t][n] = load_stream(pool + base[t % NTW] + n * step);
+    for (int n = 0; n < NL; ++n) ring[t][n] = tile_load(t, n);
   }
 
   // 1-byte pools: the K scale of this lane's token in each K tile (MFMA column
@@ -622,14 +631,11 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     }
     if constexpr (t + R < NT) {  // refill the slot just consumed
       constexpr int tn = t + R;
-      const T* pool = tn < NTW ? kl : vl;
-      constexpr int step = tn < NTW ? KSTEP : VSTEP;
       // the refill's loads issue at raised wave priority, ahead of the other
       // waves' arithmetic on the SIMD (about 1% at configs[2])
       __builtin_amdgcn_s_setprio(3);
 #pragma unroll
-      for (int n = 0; n < NL; ++n)
-        tile[n] = load_stream(pool + base[tn % NTW] + n * step);
+      for (int n = 0; n < NL; ++n) tile[n] = tile_load(tn, n);
       __builtin_amdgcn_s_setprio(0);
     }
     // keep the ring a ring: the scheduler may not hoist later refills above
@@ -1004,70 +1010,108 @@ constexpr int kBS = 16;
 #endif
 constexpr int kP = RKV_DECODE_P;
 constexpr int kPQ = RKV_DECODE_P_Q;
-constexpr int kPMin = kP < kPQ ? kP : kPQ;
 template <typename T>
 constexpr int part_of() { return sizeof(T) == 1 ? kPQ : kP; }
 template <typename T>
 constexpr int split_of() { return sizeof(T) == 1 ? RKV_DECODE_SPLIT_Q : RKV_DECODE_SPLIT; }
-// tokens per partition of a pool dtype
-inline int part_size(int dtype) { return (dtype == RKV_I8 || dtype == RKV_FP8) ? kPQ : kP; }
+
+// Partition sizes.  A call's partition size P (tokens) is any multiple of
+// 16 * SPLIT up to the build's largest (640); its waves stream
+// tw = P / (16 * SPLIT) tiles each.  The kernels are built for two slice
+// lengths: the largest, and for 16-bit and fp32 pools also 512 tokens, so
+// that long-context calls run 512-token partitions without masked slots (at
+// configs[3] 512-token partitions measured ~3% faster than 640); other sizes
+// run on the smallest build that holds them, the extra slots masked.
+// Default: 640, and 512 for 16-bit / fp32 pools once max_context exceeds
+// kLongContext.
+constexpr int kSmallP = 512;
+constexpr int kLongContext = 8192;
+static_assert(kSmallP <= kP && kSmallP % (16 * RKV_DECODE_SPLIT) == 0, "small partition build");
+
+inline bool one_byte(int dtype) { return dtype == RKV_I8 || dtype == RKV_FP8; }
+
+int default_part(int dtype, int max_context) {
+  if (one_byte(dtype)) return kPQ;
+  return max_context > kLongContext ? kSmallP : kP;
+}
+
+// The partition size a call uses: the request when it is > 0 (a multiple of
+// 16 * SPLIT, at most the largest build), else the default; a negative
+// status for an unsupported request.
+int resolve_part(int requested, int dtype, int max_context) {
+  if (requested <= 0) return default_part(dtype, max_context);
+  const int split = one_byte(dtype) ? RKV_DECODE_SPLIT_Q : RKV_DECODE_SPLIT;
+  const int maxp = one_byte(dtype) ? kPQ : kP;
+  if (requested % (16 * split) != 0 || requested > maxp) return RKV_ERR_UNSUPPORTED;
+  return requested;
+}
 
 struct Launch {
   int nw = 0;
   void (*kernel)(float*, float*, float*, const float*, const void*, const void*, const float*,
                  const float*, const int32_t*, int, const int32_t*, int, int, int64_t, float,
-                 int) = nullptr;
+                 int, int) = nullptr;
 };
 
 // Ring depth: RKV_DECODE_RING_LOADS 16-byte loads per lane in flight, at most
 // every tile of the wave's slice.
-template <typename T, int D>
+template <typename T, int D, int NTILE>
 constexpr int ring_for() {
   constexpr int nl = kBS / (64 / (D / Traits<T>::E));
   constexpr int r = (sizeof(T) == 1 ? RKV_DECODE_RING_LOADS_Q : RKV_DECODE_RING_LOADS) / nl;
-  constexpr int nt = 2 * (part_of<T>() / kBS) / split_of<T>();
+  constexpr int nt = 2 * NTILE / split_of<T>();
   return r < 1 ? 1 : (r > nt ? nt : r);
 }
 
-template <typename T, int D, int G, int FMT>
+template <typename T, int D, int G, int FMT, int NTILE>
 Launch make_launch() {
   Launch l;
   l.nw = split_of<T>();
-  l.kernel = &decode_stream_kernel<T, D, G, kBS, part_of<T>() / kBS, ring_for<T, D>(),
-                                   split_of<T>(), FMT>;
+  l.kernel = &decode_stream_kernel<T, D, G, kBS, NTILE, ring_for<T, D, NTILE>(), split_of<T>(),
+                                   FMT>;
   return l;
 }
 
+// The build for partitions of P tokens: the 512-token build when it holds
+// them (16-bit and fp32 pools), else the largest.
+template <typename T, int D, int G, int FMT>
+Launch pick_p(int P) {
+  if constexpr (sizeof(T) != 1 && kSmallP < kP) {
+    if (P <= kSmallP) return make_launch<T, D, G, FMT, kSmallP / kBS>();
+  }
+  return make_launch<T, D, G, FMT, part_of<T>() / kBS>();
+}
+
 template <typename T, int D, int FMT>
-Launch pick_g(int G) {
+Launch pick_g(int G, int P) {
   switch (G) {
-    case 1: return make_launch<T, D, 1, FMT>();
-    case 2: return make_launch<T, D, 2, FMT>();
-    case 4: return make_launch<T, D, 4, FMT>();
-    case 8: return make_launch<T, D, 8, FMT>();
+    case 1: return pick_p<T, D, 1, FMT>(P);
+    case 2: return pick_p<T, D, 2, FMT>(P);
+    case 4: return pick_p<T, D, 4, FMT>(P);
+    case 8: return pick_p<T, D, 8, FMT>(P);
     default: return Launch{};
   }
 }
 
 // 16-bit and fp32 pools: head_dim 32, 64, 128; 1-byte pools: 64, 128.
 template <typename T, int FMT>
-Launch pick_d(int D, int G) {
+Launch pick_d(int D, int G, int P) {
   switch (D) {
     case 32:
       if constexpr (sizeof(T) == 1) return Launch{};
-      else return pick_g<T, 32, FMT>(G);
-    case 64: return pick_g<T, 64, FMT>(G);
-    case 128: return pick_g<T, 128, FMT>(G);
+      else return pick_g<T, 32, FMT>(G, P);
+    case 64: return pick_g<T, 64, FMT>(G, P);
+    case 128: return pick_g<T, 128, FMT>(G, P);
     default: return Launch{};
   }
 }
 
-Launch pick(int dtype, int D, int G) {
+Launch pick(int dtype, int D, int G, int P) {
   switch (dtype) {
-    case RKV_F32: return pick_d<float, RKV_F32>(D, G);
-    case RKV_BF16: return pick_d<uint16_t, RKV_BF16>(D, G);
-    case RKV_I8: return pick_d<uint8_t, RKV_I8>(D, G);
-    case RKV_FP8: return pick_d<uint8_t, RKV_FP8>(D, G);
+    case RKV_F32: return pick_d<float, RKV_F32>(D, G, P);
+    case RKV_BF16: return pick_d<uint16_t, RKV_BF16>(D, G, P);
+    case RKV_I8: return pick_d<uint8_t, RKV_I8>(D, G, P);
+    case RKV_FP8: return pick_d<uint8_t, RKV_FP8>(D, G, P);
     default: return Launch{};
   }
 }
@@ -1105,7 +1149,7 @@ int ctx_cap_of(int max_context, int max_blocks_per_seq, int block_size) {
   return (int)(max_context < cap ? max_context : cap);
 }
 
-int validate(const DecodeArgs& a, int& max_parts) {
+int validate(const DecodeArgs& a, int& max_parts, int& P) {
   if (a.num_seqs < 0 || a.max_blocks_per_seq < 0 || a.num_blocks < 0)
     return fail(RKV_ERR_INVALID_ARG, "negative size argument");
   if (a.num_q_heads <= 0 || a.num_kv_heads <= 0 || a.num_q_heads % a.num_kv_heads)
@@ -1121,9 +1165,10 @@ int validate(const DecodeArgs& a, int& max_parts) {
   const int G = a.num_q_heads / a.num_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8)
     return fail(RKV_ERR_UNSUPPORTED, "num_q_heads / num_kv_heads must be 1, 2, 4 or 8");
-  const int P = part_size(a.dtype);
-  if (a.partition_size > 0 && a.partition_size != P)
-    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
+  P = resolve_part(a.partition_size, a.dtype, a.max_context);
+  if (P < 0)
+    return fail(RKV_ERR_UNSUPPORTED,
+                "partition_size must be a multiple of 64 tokens up to 640 (or <= 0 for the default)");
   if (a.num_seqs > 65535 || a.num_kv_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_kv_heads must be <= 65535");
   if (a.max_context < 0) return fail(RKV_ERR_INVALID_ARG, "max_context must be >= 0");
@@ -1155,10 +1200,10 @@ void split_ws(void* ws, int B, int Hq, int D, int max_parts, float*& acc, float*
   ml = reinterpret_cast<float*>(static_cast<char*>(ws) + acc_pad);
 }
 
-int launch_partitions(const DecodeArgs& a, int max_parts) {
+int launch_partitions(const DecodeArgs& a, int max_parts, int P) {
   const int G = a.num_q_heads / a.num_kv_heads;
 
-  Launch l = pick(a.dtype, a.head_dim, G);
+  Launch l = pick(a.dtype, a.head_dim, G, P);
   if (!l.kernel) return fail(RKV_ERR_UNSUPPORTED, "no decode kernel for this shape");
   float *acc = nullptr, *ml = nullptr;
   if (max_parts > 1) split_ws(a.workspace, a.num_seqs, a.num_q_heads, a.head_dim, max_parts, acc, ml);
@@ -1169,7 +1214,8 @@ int launch_partitions(const DecodeArgs& a, int max_parts) {
   hipLaunchKernelGGL(l.kernel, grid, dim3(l.nw * 64), pad, a.stream, a.out, acc, ml, a.q, a.k_pool,
                      a.v_pool, a.k_scale, a.v_scale, a.block_tables, a.max_blocks_per_seq,
                      a.ctx_lens, cap,
-                     a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts);
+                     a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts,
+                     P / (kBS * l.nw));
   return check_launch("decode_stream_kernel");
 }
 
@@ -1224,17 +1270,24 @@ using namespace rkv;
 extern "C" size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim,
                                              int max_context, int partition_size) {
   if (num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_context <= 0) return 0;
-  // a given partition size (one of the library's), else the smallest one:
-  // enough for every pool dtype
-  const int P = partition_size > 0 ? partition_size : kPMin;
+  // a given partition size, else the smaller of the 16-bit and 1-byte
+  // defaults for this max_context: enough for every pool dtype
+  const int dflt = std::min(default_part(RKV_BF16, max_context), default_part(RKV_I8, max_context));
+  const int P = partition_size > 0 ? partition_size : dflt;
   const int max_parts = (max_context + P - 1) / P;
   return ws_bytes(num_seqs, num_q_heads, head_dim, max_parts);
 }
 
-extern "C" int rkv_decode_partition_size(int partition_size, int head_dim, int dtype) {
-  (void)partition_size;
+extern "C" int rkv_decode_partition_size(int partition_size, int head_dim, int dtype,
+                                         int max_context) {
+  clear_error();
   (void)head_dim;
-  return part_size(dtype);
+  if (dtype != RKV_F32 && dtype != RKV_BF16 && !one_byte(dtype))
+    return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_F32, RKV_BF16, RKV_I8 or RKV_FP8");
+  const int P = resolve_part(partition_size, dtype, max_context);
+  if (P < 0)
+    return fail(P, "partition_size must be a multiple of 64 tokens up to 640 (or <= 0)");
+  return P;
 }
 
 extern "C" int rkv_decode_attention_partitions(
@@ -1248,10 +1301,10 @@ extern "C" int rkv_decode_attention_partitions(
                num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context, scale,
                dtype, partition_size, workspace, workspace_bytes,
                static_cast<hipStream_t>(stream)};
-  int max_parts = 1;
-  if (int rc = validate(a, max_parts)) return rc;
+  int max_parts = 1, P = 0;
+  if (int rc = validate(a, max_parts, P)) return rc;
   if (num_seqs == 0) return RKV_OK;
-  return launch_partitions(a, max_parts);
+  return launch_partitions(a, max_parts, P);
 }
 
 extern "C" int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens,
@@ -1260,14 +1313,15 @@ extern "C" int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens,
                                           int dtype, int partition_size, const void* workspace,
                                           size_t workspace_bytes, void* stream) {
   clear_error();
-  const int P = part_size(dtype);
   if (num_seqs < 0 || num_q_heads <= 0 || max_blocks_per_seq < 0 || max_context < 0)
     return fail(RKV_ERR_INVALID_ARG, "bad size argument");
   if (block_size != kBS) return fail(RKV_ERR_UNSUPPORTED, "block_size must be 16");
   if (head_dim != 32 && head_dim != 64 && head_dim != 128)
     return fail(RKV_ERR_UNSUPPORTED, "head_dim must be 32, 64 or 128");
-  if (partition_size > 0 && partition_size != P)
-    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
+  const int P = resolve_part(partition_size, dtype, max_context);
+  if (P < 0)
+    return fail(RKV_ERR_UNSUPPORTED,
+                "partition_size must be a multiple of 64 tokens up to 640 (or <= 0 for the default)");
   if (num_seqs > 65535 || num_q_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_q_heads must be <= 65535");
   const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
@@ -1358,9 +1412,10 @@ extern "C" int rkv_decode_attention_noalloc(float* out, const float* q, const vo
                                             int max_context, float scale, int dtype,
                                             int partition_size, void* stream) {
   clear_error();
-  const int P = part_size(dtype);
-  if (partition_size > 0 && partition_size != P)
-    return fail(RKV_ERR_UNSUPPORTED, "partition_size must be the library's (or <= 0 for it)");
+  const int P = resolve_part(partition_size, dtype, max_context);
+  if (P < 0)
+    return fail(RKV_ERR_UNSUPPORTED,
+                "partition_size must be a multiple of 64 tokens up to 640 (or <= 0 for the default)");
   const int cap = ctx_cap_of(max_context < 0 ? 0 : max_context, max_blocks_per_seq < 0 ? 0 : max_blocks_per_seq,
                              block_size);
   const int max_parts = cap <= 0 ? 1 : (cap + P - 1) / P;
@@ -1396,11 +1451,11 @@ extern "C" int rkv_decode_attention_q(float* out, const float* q, const void* k_
                num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context, scale,
                dtype, partition_size, workspace, workspace_bytes,
                static_cast<hipStream_t>(stream), k_scale, v_scale};
-  int max_parts = 1;
-  if (int rc = validate(a, max_parts)) return rc;
+  int max_parts = 1, P = 0;
+  if (int rc = validate(a, max_parts, P)) return rc;
   if (num_seqs == 0) return RKV_OK;
-  if (int rc = launch_partitions(a, max_parts)) return rc;
+  if (int rc = launch_partitions(a, max_parts, P)) return rc;
   const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
-  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, part_size(dtype),
-                      max_parts, workspace, a.stream);
+  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim, cap, P, max_parts,
+                      workspace, a.stream);
 }

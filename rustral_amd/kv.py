@@ -121,19 +121,30 @@ def copy_blocks(k_pool: torch.Tensor, v_pool: torch.Tensor, pairs: torch.Tensor)
                                 _stream(k_pool)))
 
 
-def workspace_bytes(num_seqs: int, num_q_heads: int, head_dim: int, max_context: int) -> int:
-    return int(lib().rkv_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_context, 0))
+def workspace_bytes(num_seqs: int, num_q_heads: int, head_dim: int, max_context: int,
+                    partition_size: int = 0) -> int:
+    return int(lib().rkv_decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_context,
+                                                partition_size))
+
+
+def partition_size(dtype_code: int, max_context: int, requested: int = 0, head_dim: int = 128) -> int:
+    """The partition size a decode call uses (a request <= 0: the default)."""
+    p = lib().rkv_decode_partition_size(requested, head_dim, dtype_code, max_context)
+    check(min(p, 0))
+    return int(p)
 
 
 def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                      block_tables: torch.Tensor, ctx_lens: torch.Tensor,
                      scale: float | None = None, *, max_context: int | None = None,
                      out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-                     passes: str = "both") -> torch.Tensor:
+                     passes: str = "both", partition_size: int = 0) -> torch.Tensor:
     """Paged GQA decode attention: q [B, Hq, D] fp32 -> out [B, Hq, D] fp32.
 
     passes: "both" (default), "partitions" or "merge" (the two launches of
     the split-K algorithm, for callers that time or schedule them apart).
+    partition_size: tokens per split-K partition (a multiple of 64 up to
+    640; 0: the library's default for max_context).
     """
     _dev(q, "q", torch.float32), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
     _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
@@ -148,7 +159,7 @@ def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
         scale = 1.0 / math.sqrt(d)
     if out is None:
         out = torch.empty_like(q)
-    need = workspace_bytes(B, hq, d, max_context)
+    need = workspace_bytes(B, hq, d, max_context, partition_size)
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
@@ -159,10 +170,11 @@ def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
         fn = lib().rkv_decode_attention if passes == "both" else lib().rkv_decode_attention_partitions
         check(fn(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
                  block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), B, hq, hkv, d, bs, nb,
-                 max_context, float(scale), dt, 0, ws_ptr, ws_len, s))
+                 max_context, float(scale), dt, partition_size, ws_ptr, ws_len, s))
     elif passes == "merge":
         check(lib().rkv_decode_attention_merge(out.data_ptr(), ctx_lens.data_ptr(), mbs, B, hq, d,
-                                               bs, max_context, dt, 0, ws_ptr, ws_len, s))
+                                               bs, max_context, dt, partition_size, ws_ptr, ws_len,
+                                               s))
     else:
         raise ValueError(f"passes={passes!r}")
     return out
@@ -224,7 +236,7 @@ def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tens
                        k_scale: torch.Tensor, v_scale: torch.Tensor, block_tables: torch.Tensor,
                        ctx_lens: torch.Tensor, scale: float | None = None, fmt: str = "int8", *,
                        max_context: int | None = None, out: torch.Tensor | None = None,
-                       workspace: torch.Tensor | None = None) -> torch.Tensor:
+                       workspace: torch.Tensor | None = None, partition_size: int = 0) -> torch.Tensor:
     """decode_attention over 1-byte pools with per-row scales."""
     _dev(q, "q", torch.float32), _dev(k_pool, "k_pool", torch.uint8)
     _dev(v_pool, "v_pool", torch.uint8), _dev(k_scale, "k_scale", torch.float32)
@@ -239,7 +251,7 @@ def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tens
         scale = 1.0 / math.sqrt(d)
     if out is None:
         out = torch.empty_like(q)
-    need = workspace_bytes(B, hq, d, max_context)
+    need = workspace_bytes(B, hq, d, max_context, partition_size)
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
@@ -247,8 +259,8 @@ def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tens
     check(lib().rkv_decode_attention_q(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(),
                                        v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
                                        block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), B, hq,
-                                       hkv, d, bs, nb, max_context, float(scale), _qcode(fmt), 0,
-                                       ws_ptr, ws_len, _stream(q)))
+                                       hkv, d, bs, nb, max_context, float(scale), _qcode(fmt),
+                                       partition_size, ws_ptr, ws_len, _stream(q)))
     return out
 
 

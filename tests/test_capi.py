@@ -53,7 +53,8 @@ def _decode(**kw):
     (dict(q=None), RKV_ERR_INVALID_ARG),
     (dict(out=8), RKV_ERR_INVALID_ARG),           # misaligned
     (dict(maxc=1000, mbs=100), RKV_ERR_WORKSPACE),  # needs split-K partials
-    (dict(ps=128), RKV_ERR_UNSUPPORTED),
+    (dict(ps=100), RKV_ERR_UNSUPPORTED),            # not a multiple of 64 tokens
+    (dict(ps=704), RKV_ERR_UNSUPPORTED),            # above the largest build
 ])
 def test_decode_rejects_bad_arguments(kw, code):
     assert _decode(**kw) == code
@@ -67,18 +68,29 @@ def test_decode_zero_sequences_is_a_no_op():
 
 def test_workspace_size():
     L = _lib.lib()
-    P = L.rkv_decode_partition_size(0, 128, RKV_BF16)
+    P = L.rkv_decode_partition_size(0, 128, RKV_BF16, 4096)
     assert P == 640
     assert L.rkv_decode_workspace_bytes(64, 32, 128, P, 0) == 0  # one partition
     ws = L.rkv_decode_workspace_bytes(64, 32, 128, 4096, 0)
     rows = 64 * 32 * -(-4096 // P)
     assert ws >= rows * (128 + 2) * 4
-    # each pool dtype has its partition size; the default workspace (partition
-    # size 0) covers every one of them
-    for dt in (RKV_F32, RKV_BF16, RKV_I8, RKV_FP8):
-        Pd = L.rkv_decode_partition_size(0, 128, dt)
-        assert Pd > 0 and Pd % 16 == 0
-        assert ws >= L.rkv_decode_workspace_bytes(64, 32, 128, 4096, Pd)
+    # each pool dtype has its default partition size at a max_context; the
+    # default workspace (partition size 0) covers every one of them
+    for maxc in (4096, 65536):
+        ws = L.rkv_decode_workspace_bytes(8, 32, 128, maxc, 0)
+        for dt in (RKV_F32, RKV_BF16, RKV_I8, RKV_FP8):
+            Pd = L.rkv_decode_partition_size(0, 128, dt, maxc)
+            assert Pd > 0 and Pd % 64 == 0
+            assert ws >= L.rkv_decode_workspace_bytes(8, 32, 128, maxc, Pd)
+    # long contexts default to 512-token partitions for 16-bit / fp32 pools
+    assert L.rkv_decode_partition_size(0, 128, RKV_BF16, 65536) == 512
+    assert L.rkv_decode_partition_size(0, 128, RKV_F32, 65536) == 512
+    assert L.rkv_decode_partition_size(0, 128, RKV_I8, 65536) == 640
+    # a request is honoured when it is a multiple of 64 up to 640
+    for req in (64, 128, 320, 512, 576, 640):
+        assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == req
+    for req in (100, 704, 1024):
+        assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == RKV_ERR_UNSUPPORTED
 
 
 def test_copy_kernels_reject_bad_arguments():

@@ -262,3 +262,21 @@ def test_decode_graph_replay_matches_eager(dev):
         torch.cuda.synchronize()
         for o, e in zip(outs, eager):
             assert torch.equal(o, e), f"replay {rep}"
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("P", [64, 192, 320, 512, 576, 640])
+def test_decode_caller_partition_sizes(dev, dtype, P):
+    """Every accepted partition size (multiples of 64 tokens up to 640) gives
+    the oracle's result: sizes up to 512 run on the 512-token build, larger
+    ones on the 640-token build, with the slots past the size masked; the
+    contexts straddle the partition and block boundaries."""
+    ctx = np.array([1, 63, 64, 65, 511, 512, 513, 575, 577, 640, 641, 1300, 2048, 3333], np.int32)
+    say(f"decode partition_size={P} dtype={dtype}")
+    q, kp, vp, kf, vf, tables = case(P + 7, len(ctx), 32, 8, 128, ctx, dtype)
+    scale = float(np.float32(1.0 / math.sqrt(128)))
+    out = kv.decode_attention(to_dev(q, dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(tables, dev),
+                              to_dev(ctx, dev), scale, partition_size=P)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, kp, vp, tables, ctx, scale)
+    assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"partition {P} vs oracle")

@@ -167,3 +167,25 @@ def test_decode_q_quantization_error_is_small(dev):
         err = np.abs(got - want).max()
         say(f"{fmt}: max |decode_q - fp32 decode| = {err:.3e}")
         assert err < tol
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+@pytest.mark.parametrize("P", [128, 384])
+def test_decode_q_caller_partition_sizes(dev, fmt, P):
+    """1-byte pools at requested partition sizes (the 640-token build with the
+    slots past the size masked), against the oracle on the dequantized pool."""
+    say(f"decode_q partition_size={P} fmt={fmt}")
+    rng = np.random.default_rng(P)
+    ctx = np.array([1, 100, 128, 129, 384, 385, 1000, 2500], np.int32)
+    nb, hkv, bs, d = 360, 8, 16, 128
+    kp, vp, ks, vs = quant_case(P, nb, hkv, bs, d, fmt)
+    tables = make_tables(rng, ctx, bs, nb)
+    q = rng.standard_normal((len(ctx), 32, d)).astype(np.float32)
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    out = kv.decode_attention_q(to_dev(q, dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(ks, dev),
+                                to_dev(vs, dev), to_dev(tables, dev), to_dev(ctx, dev), scale, fmt,
+                                partition_size=P)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, oracle.dequantize_pool(kp, ks, CODE[fmt]),
+                                   oracle.dequantize_pool(vp, vs, CODE[fmt]), tables, ctx, scale)
+    assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"1-byte partition {P} vs oracle")
