@@ -139,6 +139,44 @@ def cpu_baseline(torch, layers, ctx, threads):
     }
 
 
+def stats(samples):
+    """mean / p50 / std / CI95 of per-step times (ms), in the spirit of the
+    reference bench's schema-v2 statistics (crates/bench/src/lib.rs:236-310):
+    CI95 = mean +- 1.96 std / sqrt(n)."""
+    import numpy as np
+    a = np.asarray(samples, np.float64)
+    n = len(a)
+    sd = float(a.std(ddof=1)) if n > 1 else 0.0
+    h = 1.96 * sd / math.sqrt(n) if n > 1 else 0.0
+    return {"n": n, "mean": round(float(a.mean()), 5), "p50": round(float(np.median(a)), 5),
+            "std": round(sd, 5), "min": round(float(a.min()), 5), "max": round(float(a.max()), 5),
+            "ci95": [round(float(a.mean()) - h, 5), round(float(a.mean()) + h, 5)]}
+
+
+def machine(torch):
+    """Where the numbers were taken: GPU, HIP / torch versions, host CPU."""
+    cpu_model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    cpu_model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    props = torch.cuda.get_device_properties(0)
+    return {"gpu": torch.cuda.get_device_name(0), "gcn_arch": getattr(props, "gcnArchName", None),
+            "compute_units": props.multi_processor_count,
+            "gpu_memory_GiB": round(props.total_memory / 2**30, 1),
+            "hip": torch.version.hip, "torch": torch.__version__, "cpu_model": cpu_model,
+            "host_nproc": os.cpu_count(), "host_cpus_usable": affinity,
+            "timestamp_utc": time.strftime("%Y-%m-%dT%H:%M:%SZ", time.gmtime())}
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the partition kernel from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a 1 GiB copy)."""
@@ -565,12 +603,13 @@ def run_decode_q(torch, dev, args):
 
 def run_config4(torch, dev, args):
     """continuous-batching step mix.  256 running sequences with
-    contexts U[1, 8192] (seed 4) in 32 layer pools of 80,000 blocks (bf16,
-    168 GB), blocks handed out one at a time round-robin by the host block
+    contexts U[1, 8192] (seed 4) in 32 layer pools of 84,000 blocks (bf16,
+    176 GB), blocks handed out one at a time round-robin by the host block
     manager (so finished sequences leave holes).  One step: 10% of the
-    sequences finish (blocks freed), the block manager plans a compaction of
-    up to 25% of the live blocks and copy_blocks moves them (all layers, K and
-    V, one launch), 10% new sequences are admitted with 128-token prefills
+    sequences finish (blocks freed), the block manager plans the relocation of
+    25% of the live blocks (rkv_bm_plan_migration: highest ids first into the
+    lowest free ids) and copy_blocks moves them (all layers, K and V, one
+    launch), 10% new sequences are admitted with 128-token prefills
     appended in bulk (one launch for all layers) and run through causal
     prefill attention (one call per layer), then one decode token for every
     running sequence: append (one launch) + 32 decode-attention calls.
@@ -582,7 +621,7 @@ def run_config4(torch, dev, args):
     from rustral_amd import kv
     from rustral_amd.serving import PagedCache
     rng = np.random.default_rng(4)
-    n_layers, nblk, B, pre = 32, 80000, 256, 128
+    n_layers, nblk, B, pre = 32, 84000, 256, 128
     n_turn = B // 10                                 # finish / admit per step
     blk_bytes = HKV * BS * D * 2
     kp = torch.empty((n_layers, nblk, HKV, BS, D), dtype=torch.bfloat16, device=dev)
@@ -622,7 +661,8 @@ def run_config4(torch, dev, args):
             cache.free(i)
             del ctx[i]
         live = sum(len(cache.table(i)) for i in ctx)
-        pairs = cache.plan_compaction(live // 4)
+        pairs = cache.plan_migration(live // 4)
+        assert len(pairs) == live // 4, "the pool is too small to relocate 25% of the live blocks"
         admitted = []
         for _ in range(n_fin):
             cache.allocate(next_id, pre)
@@ -699,7 +739,9 @@ def run_config4(torch, dev, args):
                  "GB/s", total_ms, types.SimpleNamespace(steps=timed, warmup=warmup), "bf16",
                  {"workload": "configs[4] continuous-batching step mix", "running": B,
                   "layers": n_layers, "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D,
-                  "block_size": BS, "pool_blocks_per_layer": nblk, "prefill": pre},
+                  "block_size": BS, "pool_blocks_per_layer": nblk, "prefill": pre,
+                  "relocated_share_of_live_blocks": round(float(np.mean(
+                      [s["pairs"] / s["live_blocks"] for s in steps])), 4)},
                  components={c: {"ms": round(float(m), 3), "GBps": round(float(gb), 1),
                                  "bytes": int(b)} for c, m, gb, b in zip(comps, ms, gbps, by)},
                  decode_tokens_per_s=round(float(np.mean([s["running"] for s in steps]))
@@ -845,13 +887,17 @@ def main():
     graph.replay()
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     start, stop = ev(), ev()
+    marks_step = [ev() for _ in range(args.steps + 1)]   # per-replay boundaries
     torch.cuda.synchronize()
     start.record()
+    marks_step[0].record()
     for s in range(args.steps):
         graph.replay()
+        marks_step[s + 1].record()
     stop.record()
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(stop) / args.steps
+    step_stats = stats([marks_step[i].elapsed_time(marks_step[i + 1]) for i in range(args.steps)])
     del graph
 
     # (2) roofline: the partition kernel alone, HIP events on its launch
@@ -904,8 +950,14 @@ def main():
     copy_gbps = copy_bandwidth(torch, dev)
     cpu = None
     if not args.no_cpu_baseline:
+        # 16 threads: the host share of one GPU on the box (nproc there counts
+        # the whole host); the host's nproc and CPU model are recorded beside
         threads = args.cpu_threads or min(os.cpu_count() or 1, 16)
         cpu = cpu_baseline(torch, layers, ctx, threads)
+        m = machine(torch)
+        cpu.update({"cpu_model": m["cpu_model"], "host_nproc": m["host_nproc"],
+                    "host_cpus_usable": m["host_cpus_usable"],
+                    "threads_note": "threads = min(nproc, 16): the CPU share of one GPU on the box"})
 
     line = {
         "metric": "paged-KV decode attention GB/s (% of HBM peak); decode tokens/s at batch 64",
@@ -929,6 +981,8 @@ def main():
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
         "decode_tokens_per_s_b64": round(tokens_per_s, 1),
         "us_per_call": round(call_us, 2),
+        "step_ms_stats": step_stats,
+        "value_at_p50_step": round(bytes_call * n_layers / (step_stats["p50"] * 1e-3) / 1e9, 2),
         "step_ms_eager_with_events": round(ms_step_eager, 4),
         "partition_kernel_us": round(avg_burst_part_us, 2),
         "partition_kernel_us_events_per_launch": round(avg_part_us, 2),
@@ -940,6 +994,7 @@ def main():
                      "kernel": "decode_stream_kernel<bf16, D=128, G=4> (640-token partitions, 4 waves each, LDS combine)",
                      "traffic": traffic},
         "cpu_baseline": cpu,
+        "machine": machine(torch),
     }
     print(json.dumps(line), flush=True)
 

@@ -82,6 +82,16 @@ int rkv_bm_fill_tables(const rkv_block_manager* bm, const int64_t* seq_ids, int 
 int64_t rkv_bm_plan_compaction(rkv_block_manager* bm, int64_t max_moves, int32_t* pairs,
                                int64_t cap_pairs);
 
+/* Migration plan: the same moves without the stop at the first free id above
+ * the source, so exactly min(max_moves, live blocks, free blocks) live
+ * blocks move, highest id first, to the lowest free ids -- it drains the top
+ * of the pool (a region to release, or the configs[4] step's relocation of a
+ * fixed share of the live blocks).  Pairs, tables and free list as for
+ * rkv_bm_plan_compaction; sources (live) and destinations (free) are
+ * disjoint. */
+int64_t rkv_bm_plan_migration(rkv_block_manager* bm, int64_t max_moves, int32_t* pairs,
+                              int64_t cap_pairs);
+
 /* ---- device-side block manager ----------------------------------------------
  * The same FIFO manager with its state in device memory: the free list is a
  * ring of block ids, the tables are an int32 [max_seqs][max_blocks_per_seq]

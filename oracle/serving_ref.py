@@ -58,7 +58,10 @@ class PagedCacheRef:
     def table(self, seq_id: int) -> list[int]:
         return list(self.block_tables.get(seq_id, []))
 
-    def plan_compaction(self, max_moves: int):
+    def plan_migration(self, max_moves: int):
+        return self.plan_compaction(max_moves, below_only=False)
+
+    def plan_compaction(self, max_moves: int, below_only: bool = True):
         owner = {}
         for s, t in self.block_tables.items():
             for i, b in enumerate(t):
@@ -67,7 +70,7 @@ class PagedCacheRef:
         free = sorted(self.free_blocks)
         pairs, j = [], 0
         for b in live:
-            if len(pairs) >= max_moves or j >= len(free) or free[j] >= b:
+            if len(pairs) >= max_moves or j >= len(free) or (below_only and free[j] >= b):
                 break
             s, i = owner[b]
             self.block_tables[s][i] = free[j]

@@ -135,7 +135,12 @@ extern "C" {
         max_context: c_int,
         partition_size: c_int,
     ) -> usize;
-    pub fn rkv_decode_partition_size(partition_size: c_int, head_dim: c_int, dtype: c_int) -> c_int;
+    pub fn rkv_decode_partition_size(
+        partition_size: c_int,
+        head_dim: c_int,
+        dtype: c_int,
+        max_context: c_int,
+    ) -> c_int;
     pub fn rkv_decode_attention(
         out: *mut f32,
         q: *const f32,
@@ -470,6 +475,12 @@ extern "C" {
         max_blocks: c_int,
     ) -> c_int;
     pub fn rkv_bm_plan_compaction(
+        bm: *mut RkvBlockManager,
+        max_moves: i64,
+        pairs: *mut i32,
+        cap_pairs: i64,
+    ) -> i64;
+    pub fn rkv_bm_plan_migration(
         bm: *mut RkvBlockManager,
         max_moves: i64,
         pairs: *mut i32,

@@ -25,7 +25,7 @@ SIGNATURES = {
     "rkv_gather": (_i, [_p, _p, _p, _p, _p, _i, _p, _p, _i, _i, _i, _i, _i64, _i, _i, _i, _p]),
     "rkv_copy_blocks": (_i, [_p, _p, _i64, _i, _p, _i, _i64, _i64, _p]),
     "rkv_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
-    "rkv_decode_partition_size": (_i, [_i, _i, _i]),
+    "rkv_decode_partition_size": (_i, [_i, _i, _i, _i]),
     "rkv_decode_attention": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64, _i, _f,
                                   _i, _i, _p, _sz, _p]),
     "rkv_decode_attention_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,
@@ -63,6 +63,7 @@ SIGNATURES = {
     "rkv_bm_free_list": (_i64, [_p, _p, _i64]),
     "rkv_bm_fill_tables": (_i, [_p, _p, _i, _p, _i]),
     "rkv_bm_plan_compaction": (_i64, [_p, _i64, _p, _i64]),
+    "rkv_bm_plan_migration": (_i64, [_p, _i64, _p, _i64]),
     "rkv_sched_create": (_p, [_i64, _i, _i, _i]),
     "rkv_sched_destroy": (None, [_p]),
     "rkv_sched_add_request": (_i64, [_p, _p, _i, _i, _i]),

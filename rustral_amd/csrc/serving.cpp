@@ -101,18 +101,24 @@ class BlockManager {
   }
   const std::deque<int32_t>& free_list() const { return free_; }
 
-  // Highest live ids move into the lowest free ids below them.
-  int64_t plan_compaction(int64_t max_moves, std::vector<int32_t>* pairs) {
+  // Highest live ids move into the lowest free ids: below them only
+  // (compaction), or wherever the lowest free ids are (migration).
+  int64_t plan_compaction(int64_t max_moves, std::vector<int32_t>* pairs,
+                          bool below_only = true) {
     std::vector<int32_t> fr(free_.begin(), free_.end());
     std::sort(fr.begin(), fr.end());
     int64_t moves = 0;
     size_t j = 0;
     std::vector<int32_t> freed;
+    // only blocks live before the plan move (a destination of this plan is
+    // never moved again, so sources and destinations stay disjoint)
+    std::vector<char> dest((size_t)num_blocks(), 0);
     for (int64_t b = num_blocks() - 1; b >= 0 && moves < max_moves && j < fr.size(); --b) {
-      if (owner_[b] < 0) continue;
+      if (owner_[b] < 0 || dest[(size_t)b]) continue;
       const int32_t dst = fr[j];
-      if (dst >= b) break;
+      if (below_only && dst >= b) break;
       ++j;
+      dest[(size_t)dst] = 1;
       const int64_t seq = owner_[b], p = pos_[b];
       tables_[seq][p] = dst;
       owner_[dst] = seq;
@@ -427,6 +433,17 @@ extern "C" int64_t rkv_bm_plan_compaction(rkv_block_manager* bm, int64_t max_mov
     return fail(RKV_ERR_INVALID_ARG, "rkv_bm_plan_compaction: bad argument");
   std::vector<int32_t> p;
   const int64_t n = bm->bm->plan_compaction(std::min(max_moves, cap_pairs), &p);
+  std::memcpy(pairs, p.data(), p.size() * sizeof(int32_t));
+  return n;
+}
+
+extern "C" int64_t rkv_bm_plan_migration(rkv_block_manager* bm, int64_t max_moves,
+                                         int32_t* pairs, int64_t cap_pairs) {
+  rkv::clear_error();
+  if (!bm || max_moves < 0 || cap_pairs < 0 || (max_moves > 0 && !pairs))
+    return fail(RKV_ERR_INVALID_ARG, "rkv_bm_plan_migration: bad argument");
+  std::vector<int32_t> p;
+  const int64_t n = bm->bm->plan_compaction(std::min(max_moves, cap_pairs), &p, false);
   std::memcpy(pairs, p.data(), p.size() * sizeof(int32_t));
   return n;
 }

@@ -108,6 +108,16 @@ class PagedCache:
             raise _err(n)
         return buf[:n].copy()
 
+    def plan_migration(self, max_moves: int) -> np.ndarray:
+        """Like plan_compaction without the stop at the first free id above
+        the source: min(max_moves, live, free) live blocks move, highest
+        first, to the lowest free ids."""
+        buf = np.empty((max(max_moves, 1), 2), np.int32)
+        n = lib().rkv_bm_plan_migration(self._h, max_moves, _ptr(buf), max_moves)
+        if n < 0:
+            raise _err(n)
+        return buf[:n].copy()
+
 
 @dataclass
 class Batch:

@@ -140,12 +140,16 @@ def test_gather_bitexact_padded_and_packed(dev, dtype, out_f32):
     assert np.array_equal(to_np(ko), rk) and np.array_equal(to_np(vo), rv)
 
 
-def test_gather_of_append_roundtrip_config1_shape(dev):
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_gather_of_append_roundtrip_config1_shape(dev, dtype):
     """Config-1 shape (Hkv 8, D 128, BS 16, 65,536-block pool, 64 sequences with
-    contexts U[512, 4096]), two layers: append every token of every sequence,
+    contexts U[512, 4096]), two layers, both storage types (the fp32 pool is
+    4 GiB per layer for K and for V): append every token of every sequence,
     gather, and get the appended rows back bit for bit (bf16 pool: their RNE
     rounding, checked against the oracle's bit routine)."""
-    say("append+gather round trip, config-1 shape")
+    say(f"append+gather round trip, config-1 shape, {dtype}")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    bits = torch.int16 if dtype == "bf16" else torch.int32
     rng = np.random.default_rng(1)
     nl, nb, hkv, bs, d, B = 2, 65536, 8, 16, 128, 64
     ctx = contexts(rng, B, 512, 4096)
@@ -157,7 +161,7 @@ def test_gather_of_append_roundtrip_config1_shape(dev):
     g = torch.Generator(device=dev).manual_seed(1)
     kn = torch.randn((nl, n, hkv, d), generator=g, device=dev)
     vn = torch.randn((nl, n, hkv, d), generator=g, device=dev)
-    gk = torch.zeros((nl, nb, hkv, bs, d), dtype=torch.bfloat16, device=dev)
+    gk = torch.zeros((nl, nb, hkv, bs, d), dtype=tdt, device=dev)
     gv = torch.zeros_like(gk)
     kv.append(gk, gv, kn, vn, to_dev(slots, dev))
     gt, gc = to_dev(tables, dev), to_dev(ctx, dev)
@@ -167,15 +171,16 @@ def test_gather_of_append_roundtrip_config1_shape(dev):
         # compare a strided subset of sequences on the host, all of them on device
         for b in range(0, B, 9):
             L = int(ctx[b])
-            want_k = oracle.bf16_from_f32(
-                kn[l, offs[b]:offs[b] + L].cpu().numpy()).transpose(1, 0, 2)
+            src = kn[l, offs[b]:offs[b] + L].cpu().numpy()
+            want_k = (oracle.bf16_from_f32(src) if dtype == "bf16" else src).transpose(1, 0, 2)
             assert np.array_equal(to_np(ko[b, :, :L]), want_k)
         for b in range(B):
             L = int(ctx[b])
-            sk = kn[l, offs[b]:offs[b] + L].to(torch.bfloat16).transpose(0, 1)
-            sv = vn[l, offs[b]:offs[b] + L].to(torch.bfloat16).transpose(0, 1)
-            assert torch.equal(ko[b, :, :L].view(torch.int16), sk.contiguous().view(torch.int16))
-            assert torch.equal(vo[b, :, :L].view(torch.int16), sv.contiguous().view(torch.int16))
+            sk = kn[l, offs[b]:offs[b] + L].to(tdt).transpose(0, 1)
+            sv = vn[l, offs[b]:offs[b] + L].to(tdt).transpose(0, 1)
+            assert torch.equal(ko[b, :, :L].view(bits), sk.contiguous().view(bits))
+            assert torch.equal(vo[b, :, :L].view(bits), sv.contiguous().view(bits))
+        del ko, vo
     torch.cuda.synchronize()
 
 

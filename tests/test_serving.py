@@ -165,10 +165,16 @@ def test_block_manager_matches_restatement(seed):
             assert c.reserve(sid, n) == r.reserve(sid, n)
         elif op < 0.85:
             assert c.free(sid) == r.free(sid)
-        else:
+        elif op < 0.93:
             m = rng.randrange(0, 20)
             got = c.plan_compaction(m)
             want = r.plan_compaction(m)
+            assert [tuple(p) for p in got.tolist()] == want
+            assert len(set(got[:, 0].tolist()) & set(got[:, 1].tolist())) == 0
+        else:
+            m = rng.randrange(0, 20)
+            got = c.plan_migration(m)
+            want = r.plan_migration(m)
             assert [tuple(p) for p in got.tolist()] == want
             assert len(set(got[:, 0].tolist()) & set(got[:, 1].tolist())) == 0
         _check_tables(c, r)
@@ -274,3 +280,27 @@ def test_greedy_ref_matches_library_on_random_vectors():
     for _ in range(50):
         v = rng.integers(-3, 3, size=int(rng.integers(1, 40))).astype(np.float32)
         assert Sampler.greedy(v) == greedy_ref(v.tolist())
+
+
+def test_migration_moves_the_requested_share_even_without_lower_holes():
+    """Compaction stops at the first free id above the source; migration
+    keeps going, so a fixed share of the live blocks moves (configs[4]'s
+    relocation of 25% of the live blocks), with the data gathered unchanged."""
+    rng = np.random.default_rng(5)
+    nb, bs = 200, 16
+    c = PagedCache(bs, nb)
+    for sid in range(12):
+        c.allocate(sid, int(rng.integers(50, 200)))
+    live = sum(len(c.table(s)) for s in range(12))
+    assert len(c.plan_compaction(1000)) == 0            # dense prefix: nothing to compact
+    pool = rng.standard_normal((nb, 2, bs, 4)).astype(np.float32)
+    before = {s: pool[c.table(s)].copy() for s in range(12)}
+    want = live // 4
+    pairs = c.plan_migration(want)
+    assert len(pairs) == min(want, nb - live)
+    src, dst = pairs[:, 0], pairs[:, 1]
+    assert not set(src.tolist()) & set(dst.tolist())
+    pool[dst] = pool[src]
+    for s in range(12):
+        np.testing.assert_array_equal(pool[c.table(s)], before[s])
+    assert c.num_free() == nb - live
