@@ -175,8 +175,13 @@ __device__ __forceinline__ float lo_col(float x) {
 //   A (16 x 32) = queries: rows 0..G-1 = bf16(q) of the G heads, rows
 //                 G..2G-1 = bf16(q - bf16(q)), other rows zero.  hi + lo keeps
 //                 ~16 significant bits of q: scores as accurate as fp32 dots.
-//   B (32 x 16) = K^T of the tile: lane l loads 16 bytes of token row l % 16
-//                 at dims 32c + 8 (l / 16) straight from the pool.
+//   B (32 x 16) = K^T of the tile: lane l holds 16 bytes of token row l % 16
+//                 at dims 32c + 8 (l / 16).  bf16 tiles are loaded like V
+//                 tiles (four 256-byte rows per wave-load) and reach this
+//                 layout through the wave's LDS staging buffer: loading it
+//                 straight from the pool touches 16 rows x 64 bytes per
+//                 wave-load, half of every 128-byte line, which streams ~9%
+//                 slower.  1-byte tiles are loaded in the operand layout.
 //   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
 // (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
 // D[4(l/16)+r][l%16].)  PV runs on the matrix cores too (below); fp32 pools
@@ -185,6 +190,10 @@ __device__ __forceinline__ float lo_col(float x) {
 // 1-byte kernels at D = 128, G <= 4 at 3 waves per SIMD without spilling.
 #ifndef RKV_DECODE_WAVES_PER_SIMD
 #define RKV_DECODE_WAVES_PER_SIMD 3
+#endif
+// bf16 K tiles through LDS (1) or loaded in the MFMA operand layout (0).
+#ifndef RKV_DECODE_K_LDS
+#define RKV_DECODE_K_LDS 1
 #endif
 template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT>
 __global__ __launch_bounds__(64 * SPLIT)
@@ -330,9 +339,15 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // its loads.  A masked tile re-reads the wave's tile 0 (its streaming
   // re-reads add ~2% to FETCH_SIZE; masking them with an empty buffer
   // resource instead removed that traffic but made the kernel ~4% slower).
-  const uint32_t koff = (MFMA ? kt * D + (QNT ? (D / 4) * kq : 8 * kq) : slot * D + dl * E) * sizeof(T);
+  // MFMA: K tiles staged through LDS are loaded like V tiles.
+  constexpr bool KLDS = MFMA && RKV_DECODE_K_LDS;
+  constexpr int KROW = D * sizeof(T) + 16;  // staged K row (bytes): the 16 rows
+                                            // of one operand read hit distinct banks
+  static_assert(!KLDS || BS * KROW <= VT * BS * VROW, "K staging fits the V staging buffer");
+  constexpr bool kmfma = MFMA && !KLDS;
+  const uint32_t koff = (kmfma ? kt * D + (QNT ? (D / 4) * kq : 8 * kq) : slot * D + dl * E) * sizeof(T);
   const uint32_t voff = (slot * D + dl * E) * sizeof(T);
-  constexpr uint32_t KSTEP = (MFMA ? (QNT ? 16 : 32) : TPL * D) * sizeof(T);
+  constexpr uint32_t KSTEP = (kmfma ? (QNT ? 16 : 32) : TPL * D) * sizeof(T);
   constexpr uint32_t VSTEP = TPL * D * sizeof(T);
   auto tile_load = [&](int t, int n) __attribute__((always_inline)) {
     const bool is_k = t < NTW;
@@ -341,6 +356,9 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
                        (is_k ? koff : voff) + n * (is_k ? KSTEP : VSTEP));
   };
 
+  const int tok0 = lb0 * BS;  // first token of this wave's slice
+  float acc[G][E];
+  float m[G], l[G];
   uint4 ring[R][NL];
 #pragma unroll
   for (int t = 0; t < R; ++t) {
@@ -390,36 +408,71 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     }
   }
 
-  const int tok0 = lb0 * BS;  // first token of this wave's slice
-  float acc[G][E];
-  float m[G], l[G];
   // The 2*NTW steps are instantiated one by one (static_for) so that every
   // ring slot is a fixed set of registers.
   static_for<0, NT>([&](auto tc) __attribute__((always_inline)) {
     constexpr int t = decltype(tc)::value;
     constexpr int i = t % NTW;
     uint4* tile = ring[t % R];
+    // Refill the slot just consumed with tile t + R; the refill's loads issue
+    // at raised wave priority, ahead of the other waves' arithmetic on the
+    // SIMD (about 1% at configs[2]).  A tile staged in LDS frees its slot
+    // once written there, before the step's arithmetic.
+    auto refill = [&]() __attribute__((always_inline)) {
+      if constexpr (t + R < NT) {
+        constexpr int tn = t + R;
+        __builtin_amdgcn_s_setprio(3);
+#pragma unroll
+        for (int n = 0; n < NL; ++n) tile[n] = tile_load(tn, n);
+        __builtin_amdgcn_s_setprio(0);
+      }
+    };
+    constexpr bool staged = t < NTW ? KLDS : MPV;
     if constexpr (t < NTW) {
       // ---- QK^T for the 16 tokens of tile i ----
       if constexpr (MFMA) {
         f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+        // This lane's K operand: NL 16-byte pieces of token kt (bf16: dims
+        // 32c + 8 kq .. + 7 for MFMA c; 1-byte: bytes (D/4) kq + 16 n .. + 15).
+        uint4 kb[NL];
+        if constexpr (KLDS) {
+          // rows to LDS (token n TPL + slot, 16 bytes at element E dl), the
+          // ring slot refilled, then the operand pieces read back
+          uint8_t* kbuf = s_vq[w];
+#pragma unroll
+          for (int n = 0; n < NL; ++n)
+            *reinterpret_cast<uint4*>(kbuf + (n * TPL + slot) * KROW + dl * 16) = tile[n];
+          if constexpr (staged) refill();
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the rows ...
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads
+#pragma unroll
+          for (int n = 0; n < NL; ++n)
+            kb[n] = *reinterpret_cast<const uint4*>(
+                kbuf + kt * KROW + (QNT ? (D / 4) * kq + 16 * n : 64 * n + 16 * kq));
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before
+          __builtin_amdgcn_wave_barrier();                         // the next tile's rows
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else {
+#pragma unroll
+          for (int n = 0; n < NL; ++n) kb[n] = tile[n];
+        }
         if constexpr (QNT) {
 #pragma unroll
           for (int n = 0; n < NL; ++n) {
             sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                 __builtin_bit_cast(bf16x8_t, qa[2 * n]),
-                __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(tile[n].x, tile[n].y)), sacc, 0, 0,
-                0);
+                __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(kb[n].x, kb[n].y)), sacc, 0, 0, 0);
             sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                 __builtin_bit_cast(bf16x8_t, qa[2 * n + 1]),
-                __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(tile[n].z, tile[n].w)), sacc, 0, 0,
-                0);
+                __builtin_bit_cast(bf16x8_t, to_bf16x8_q<FMT>(kb[n].z, kb[n].w)), sacc, 0, 0, 0);
           }
         } else {
+          static_assert(QNT || NL == NC, "one 16-byte K piece per MFMA");
 #pragma unroll
           for (int c = 0; c < NC; ++c)
             sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa[c]),
-                                                          __builtin_bit_cast(bf16x8_t, tile[c]),
+                                                          __builtin_bit_cast(bf16x8_t, kb[c]),
                                                           sacc, 0, 0, 0);
         }
         // dot * scale (the reference's order), then the token's K row scale
@@ -539,6 +592,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
           *reinterpret_cast<uint4*>(vb + ((i % VT) * BS + n * TPL + slot) * VROW + dl * 16) = vv;
         }
       }
+      if constexpr (staged) refill();
       if constexpr (!QNT) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the tile's rows ...
         __builtin_amdgcn_wave_barrier();
@@ -629,15 +683,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
           for (int e = 0; e < E; ++e) acc[g][e] = fmaf(pr[g], vf[e], acc[g][e]);
       }
     }
-    if constexpr (t + R < NT) {  // refill the slot just consumed
-      constexpr int tn = t + R;
-      // the refill's loads issue at raised wave priority, ahead of the other
-      // waves' arithmetic on the SIMD (about 1% at configs[2])
-      __builtin_amdgcn_s_setprio(3);
-#pragma unroll
-      for (int n = 0; n < NL; ++n) tile[n] = tile_load(tn, n);
-      __builtin_amdgcn_s_setprio(0);
-    }
+    if constexpr (!staged) refill();
     // keep the ring a ring: the scheduler may not hoist later refills above
     // this step's arithmetic (that would need all 2*NTW tiles in registers)
     __builtin_amdgcn_sched_barrier(0);
