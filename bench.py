@@ -303,8 +303,12 @@ def run_config1(torch, dev, args):
         kp = torch.empty((n_layers, nb, hkv, bs, d), dtype=tdt, device=dev)
         vp = torch.empty_like(kp)
         g = torch.Generator(device=dev).manual_seed(1)
-        kn = torch.randn((n_layers, B, hkv, d), generator=g, device=dev)
-        vn = torch.randn((n_layers, B, hkv, d), generator=g, device=dev)
+        # N_SRC distinct per-step sources (512 MiB for bf16, beyond the 256 MB
+        # Infinity Cache), so a step's fp32 K/V rows come from HBM
+        n_src = 32
+        kns = torch.randn((n_src, n_layers, B, hkv, d), generator=g, device=dev)
+        vns = torch.randn((n_src, n_layers, B, hkv, d), generator=g, device=dev)
+        kn, vn = kns[0], vns[0]
         steps = max(args.steps, 4)
         slot_sets = []
         for s in range(16):                       # token L + s of every sequence, cycled
@@ -313,27 +317,29 @@ def run_config1(torch, dev, args):
                 tables[np.arange(B), p // bs].astype(np.int64) * bs + p % bs).to(dev))
         it = iter(range(10 ** 9))
         def app():
-            i = next(it) % len(slot_sets)
-            kv.append(kp, vp, kn, vn, slot_sets[i])
+            i = next(it)
+            kv.append(kp, vp, kns[i % n_src], vns[i % n_src], slot_sets[i % len(slot_sets)])
         for _ in range(args.warmup):
             app()
         ms_app = _timed(torch, app, steps)
         app_bytes = n_layers * B * hkv * d * 2 * (4 + s_pool) + B * 8
-        # the same 16 per-step launches captured once in a HIP graph and
-        # replayed, as a serving loop captures its step (no host launch cost)
+        # n_src per-step launches (sources rotating, slots cycling) captured
+        # once in a HIP graph and replayed, as a serving loop captures its
+        # step (no host launch cost)
+        def steps_of_graph():
+            for j in range(n_src):
+                kv.append(kp, vp, kns[j], vns[j], slot_sets[j % len(slot_sets)])
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            for s in slot_sets:
-                kv.append(kp, vp, kn, vn, s)
+            steps_of_graph()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         with torch.cuda.graph(graph):
-            for s in slot_sets:
-                kv.append(kp, vp, kn, vn, s)
+            steps_of_graph()
         graph.replay()
-        ms_graph = _timed(torch, graph.replay, max(steps // 4, 3)) / len(slot_sets)
+        ms_graph = _timed(torch, graph.replay, max(steps // 4, 3)) / n_src
         del graph
         # bulk: the 16 steps' tokens (1024 per layer) in one launch, as a
         # prefill or a batch of queued steps would append them
@@ -374,12 +380,12 @@ def run_config1(torch, dev, args):
                                      "bytes_per_launch": bulk_bytes,
                                      "GBps": round(bulk_bytes / (ms_bulk * 1e-3) / 1e9, 1)},
             "gather_packed": outs}
-        del kp, vp, kn, vn
+        del kp, vp, kn, vn, kns, vns
         torch.cuda.empty_cache()
     a = res["bf16"]["append_graph"]
     gb = res["bf16"]["gather_packed"]["same"]
-    return _line("KV append GB/s per step (64 tokens x 32 layers, one launch per step; 16 steps "
-                 "replayed from a HIP graph), bf16 pool", a["GBps"],
+    return _line("KV append GB/s per step (64 tokens x 32 layers, one launch per step; 32 steps "
+                 "with distinct sources replayed from a HIP graph), bf16 pool", a["GBps"],
                  "GB/s", a["us_per_step"] / 1e3, args, "bf16",
                  {"workload": "configs[1] KV append + gather microbench", "num_kv_heads": hkv,
                   "head_dim": d, "block_size": bs, "pool_blocks": nb, "sequences": B,

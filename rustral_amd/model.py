@@ -93,7 +93,11 @@ class SafetensorsFile:
             lib().rkv_st_close(self._h)
             self._h = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the module is torn down
+            pass
 
     def __enter__(self):
         return self
@@ -172,7 +176,10 @@ class Decoder:
 
     def __del__(self):
         if getattr(self, "_h", None):
-            lib().rkv_decoder_destroy(self._h)
+            try:
+                lib().rkv_decoder_destroy(self._h)
+            except Exception:  # interpreter shutdown: the module is torn down
+                pass
             self._h = None
 
     def generate(self, prompt, n_new: int, *, logits: bool = False):
@@ -206,7 +213,10 @@ class Engine:
     def __del__(self):
         if getattr(self, "_h", None):
             self.scheduler = None
-            lib().rkv_engine_destroy(self._h)
+            try:
+                lib().rkv_engine_destroy(self._h)
+            except Exception:  # interpreter shutdown: the module is torn down
+                pass
             self._h = None
 
     def submit(self, prompt, max_tokens: int, priority: int = 1) -> int:

@@ -42,7 +42,10 @@ class PagedCache:
 
     def __del__(self):
         if getattr(self, "_owned", False) and self._h:
-            lib().rkv_bm_destroy(self._h)
+            try:
+                lib().rkv_bm_destroy(self._h)
+            except Exception:  # interpreter shutdown: the module is torn down
+                pass
             self._h = None
 
     @property

@@ -1,6 +1,8 @@
-"""The device-side block manager (rkv_dbm_*) against the host one (rkv_bm_*,
-the C++ PagedCache): the same calls give the same block ids in the same
-tables and the same free-list order (bit-exact), failures change nothing,
+"""The device-side block manager (rkv_dbm_*) against the oracle's restatement
+of PagedCache (oracle/serving_ref.PagedCacheRef, kv_cache.rs:381-432) and
+the product's host manager (rkv_bm_*): the same calls give the same block
+ids in the same tables and the same free-list order (bit-exact) in all
+three, failures change nothing,
 and a decode step driven entirely from device memory -- reserve, slot
 mapping, append, batch tables, attention -- equals the same step driven by
 host-built tables.  A HIP-graph replay of reserve + slot mapping matches the
@@ -12,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle.serving_ref import PagedCacheRef
 from rustral_amd import kv
 from rustral_amd.serving import PagedCache
 from tests.gpu_util import say
@@ -21,11 +24,42 @@ pytestmark = pytest.mark.gpu
 ERR_OOM, ERR_TABLE_FULL, ERR_ARG = 1, 2, 4
 
 
-def assert_same_state(dbm, host, slots_in_use):
+class Managers:
+    """The oracle's PagedCacheRef and the product host manager, driven by
+    the same calls; reserve reports None on OOM in both."""
+
+    def __init__(self, bs, nb):
+        self.ref, self.host = PagedCacheRef(bs, nb), PagedCache(bs, nb)
+
+    def reserve(self, seq, tokens):
+        a, b = self.ref.reserve(seq, tokens), self.host.reserve(seq, tokens)
+        assert (a is None) == (b is None), (seq, tokens, a, b)
+        return a
+
+    def free(self, seq):
+        assert self.ref.free(seq) == self.host.free(seq)
+
+    def table(self, seq):
+        return self.ref.table(seq)
+
+    def num_free(self):
+        return len(self.ref.free_blocks)
+
+    def fill_tables(self, seqs, width):
+        t = np.full((len(seqs), width), -1, np.int32)
+        for i, s in enumerate(seqs):
+            row = self.ref.table(s)
+            t[i, :len(row)] = row
+        return t
+
+
+def assert_same_state(dbm, mgr, slots_in_use):
     tables, lengths, free = dbm.download()
-    assert free.tolist() == host.free_list(), "free list order"
+    assert free.tolist() == mgr.ref.free_blocks, "free list order vs the oracle"
+    assert mgr.host.free_list() == mgr.ref.free_blocks, "free list order: host vs the oracle"
     for s in range(dbm.max_seqs):
-        want = host.table(s) if s in slots_in_use else []
+        want = mgr.ref.table(s) if s in slots_in_use else []
+        assert mgr.host.table(s) == want, f"slot {s}: host table vs the oracle"
         assert lengths[s] == len(want), f"slot {s} length"
         assert tables[s, :len(want)].tolist() == want, f"slot {s} table"
         assert (tables[s, len(want):] == -1).all(), f"slot {s} tail"
@@ -36,7 +70,7 @@ def test_random_trace_matches_host_manager(dev):
     rng = np.random.default_rng(5)
     nb, bs, max_seqs, max_blocks = 400, 16, 40, 64
     dbm = kv.DeviceBlockManager(nb, bs, max_seqs, max_blocks, device=dev)
-    host = PagedCache(bs, nb)
+    host = Managers(bs, nb)
     lens = {}
     for step in range(60):
         if lens and rng.random() < 0.25:
@@ -73,7 +107,7 @@ def test_reserve_is_all_or_nothing(dev):
     say("device block manager: OOM / table full / bad slot change nothing")
     nb, bs = 20, 16
     dbm = kv.DeviceBlockManager(nb, bs, 8, 16, device=dev)
-    host = PagedCache(bs, nb)
+    host = Managers(bs, nb)
     dbm.reserve([0, 1], [100, 150])              # 7 + 10 blocks
     host.reserve(0, 100), host.reserve(1, 150)
     before = dbm.download()
@@ -105,7 +139,7 @@ def test_repeated_slot_fails_the_call(dev):
     say("device block manager: repeated slots fail the call")
     nb, bs, max_seqs = 3000, 16, 1500
     dbm = kv.DeviceBlockManager(nb, bs, max_seqs, 8, device=dev)
-    host = PagedCache(bs, nb)
+    host = Managers(bs, nb)
     dbm.reserve([0, 1], [20, 40])
     host.reserve(0, 20), host.reserve(1, 40)
     before = dbm.download()
@@ -143,7 +177,7 @@ def test_device_resident_decode_step_equals_host_driven_step(dev):
     scale = 1.0 / math.sqrt(d)
     pools = [torch.zeros((nb, hkv, bs, d), dtype=torch.bfloat16, device=dev) for _ in range(4)]
     dbm = kv.DeviceBlockManager(nb, bs, 16, max_blocks, device=dev)
-    host = PagedCache(bs, nb)
+    host = Managers(bs, nb)
     slots = list(range(3, 3 + B))
     lens = prompt.copy()
     outs = []
@@ -194,7 +228,7 @@ def test_graph_replay_of_reserve_and_slot_mapping(dev):
     say("device block manager under HIP graph replay")
     nb, bs, B, max_blocks = 120, 16, 5, 24
     dbm = kv.DeviceBlockManager(nb, bs, 8, max_blocks, device=dev)
-    host = PagedCache(bs, nb)
+    host = Managers(bs, nb)
     slots = torch.tensor([1, 4, 2, 7, 0], dtype=torch.int32, device=dev)
     lens = np.array([15, 16, 17, 40, 1], np.int32)
     ntok = torch.tensor(lens, dtype=torch.int32, device=dev)
