@@ -997,7 +997,7 @@ def main():
         "measured_copy_GBps": round(copy_gbps, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "kernel": "decode_stream_kernel<bf16, D=128, G=4> (640-token partitions, 4 waves each, LDS combine)",
+                     "kernel": "decode_stream_kernel<bf16, D=128, G=4> (640-token partitions, 4 waves each, K/V tiles staged in LDS, MFMA QK^T and PV)",
                      "traffic": traffic},
         "cpu_baseline": cpu,
         "machine": machine(torch),
