@@ -50,7 +50,7 @@ def parse():
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
                    choices=["config0", "config1", "config2", "config3", "config4", "prefill",
-                            "decode_q", "device_step"],
+                            "decode_q", "device_step", "ceilings"],
                    help="config2 (default): the headline decode line; the others print "
                         "their own line (benchmark configs[0], [1], [3], [4])")
     return p.parse_args()
@@ -841,6 +841,80 @@ def run_device_step(torch, dev, args):
                  free_blocks_after=nf_end)
 
 
+def run_ceilings(torch, dev, args):
+    """What HBM streams at on this part for the access patterns of the
+    paged-KV kernels (rustral_amd/ceiling: kernels that move bytes and do
+    nothing else): flat nontemporal read, flat write and flat copy of 4 GiB;
+    32 KiB block copies inside a 4 GiB pool (a quarter of its blocks: random
+    pairs, sorted by destination, sequential runs); and the decode kernel's
+    own loads at configs[2] (its grid, block tables and ring of tiles over
+    the bench's 32 layer pools) timed beside the decode partition kernel on
+    the same pools."""
+    import numpy as np
+    from rustral_amd import ceiling as C
+    from rustral_amd import kv
+    reps = max(args.steps // 4, 5)
+    res = {}
+
+    def rate(fn, moved):
+        fn()
+        ms = _timed(torch, fn, reps)
+        return {"GBps": round(moved / (ms * 1e-3) / 1e9, 1), "us": round(1e3 * ms, 2),
+                "bytes": int(moved)}
+
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    nbytes = 4 << 30
+    a = torch.full((nbytes // 4,), 1, dtype=torch.int32, device=dev)
+    b = torch.empty_like(a)
+    res["read_flat"] = rate(lambda: C.read(torch, a, sink), nbytes)
+    res["write_flat"] = rate(lambda: C.write(torch, b), nbytes)
+    res["copy_flat"] = rate(lambda: C.copy(torch, a, b), 2 * nbytes)
+    blk = 32768                                   # a bf16 block, Hkv 8, D 128
+    nblk = nbytes // blk
+    npairs = nblk // 4
+    rng = np.random.default_rng(3)
+    perm = rng.permutation(nblk).astype(np.int32)
+    pairs = {"random": np.stack([perm[:npairs], perm[npairs:2 * npairs]], 1)}
+    pairs["sorted_dst"] = pairs["random"][np.argsort(pairs["random"][:, 1], kind="stable")]
+    pairs["sequential"] = np.stack([np.arange(nblk - 1, nblk - 1 - npairs, -1),
+                                    np.arange(npairs)], 1).astype(np.int32)
+    for name, pr in pairs.items():
+        pd = torch.from_numpy(np.ascontiguousarray(pr, dtype=np.int32)).to(dev)
+        res[f"block_copy_{name}"] = rate(lambda: C.block_copy(torch, a, pd, blk), 2 * npairs * blk)
+    del a, b
+    torch.cuda.empty_cache()
+    layers, ctx, ctx_d, nb, mbs = build_workload(torch, dev, args.layers)
+    n_layers, max_ctx = len(layers), mbs * BS
+    parts = (max_ctx + 639) // 640
+    kv_bytes = sum(int(L) * HKV * D * 2 * 2 for L in ctx)
+
+    def stream_all():
+        for q, k, v, t in layers:
+            C.tile_stream(torch, k, v, t, ctx_d, sink, parts)
+    st = rate(stream_all, kv_bytes * n_layers)
+    res["decode_tile_stream"] = {"GBps": st["GBps"], "us_per_layer": round(st["us"] / n_layers, 2),
+                                 "kv_bytes_per_layer": kv_bytes}
+    ws = torch.empty(kv.workspace_bytes(B, HQ, D, max_ctx), dtype=torch.uint8, device=dev)
+    out = torch.empty((B, HQ, D), device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def decode_all():
+        for q, k, v, t in layers:
+            kv.decode_attention(q, k, v, t, ctx_d, scale, max_context=max_ctx, out=out,
+                                workspace=ws, passes="partitions")
+    dp = rate(decode_all, kv_bytes * n_layers)
+    res["decode_partition_kernel"] = {"GBps_kv": dp["GBps"],
+                                      "us_per_layer": round(dp["us"] / n_layers, 2)}
+    ratio = round(dp["GBps"] / st["GBps"], 4)
+    return _line("HBM ceilings of the paged-KV access patterns: the decode kernel's loads "
+                 "streamed with no arithmetic (configs[2])", st["GBps"], "GB/s",
+                 st["us"] / n_layers / 1e3, args, "bf16",
+                 {"workload": "stream kernels of rustral_amd/ceiling; configs[2] pools for the "
+                              "decode pattern", "flat_bytes": nbytes, "block_bytes": blk,
+                  "block_pairs": npairs, "layers": n_layers},
+                 decode_partition_over_stream=ratio, results=res)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -855,7 +929,8 @@ def main():
     if args.workload != "config2":
         line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
                 "prefill": run_prefill, "decode_q": run_decode_q,
-                "config4": run_config4, "device_step": run_device_step}[args.workload](
+                "config4": run_config4, "device_step": run_device_step,
+                "ceilings": run_ceilings}[args.workload](
                     torch, dev, args)
         print(json.dumps(line), flush=True)
         return

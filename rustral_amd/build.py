@@ -73,6 +73,25 @@ def _compile(src: str) -> str:
     return obj
 
 
+CEILING_SRC = os.path.join(HERE, "ceiling", "ceiling.hip")
+CEILING_LIB = os.path.join(LIB_DIR, "librkv_ceiling.so")
+
+
+def build_ceiling(verbose: bool = False) -> str:
+    """The measurement library of bench.py's ceilings workload (stream
+    kernels, not part of librustral_kv.so)."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = CEILING_LIB + ".tmp"
+    r = subprocess.run([hipcc(), *HIPCC_FLAGS, "-shared", "-o", tmp, CEILING_SRC],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed for {CEILING_SRC}:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CEILING_LIB)
+    if verbose:
+        print(f"built {CEILING_LIB}", file=sys.stderr)
+    return CEILING_LIB
+
+
 def build(verbose: bool = False, changed_only: bool = False) -> str:
     """Compiles every source (or, with changed_only, those newer than their
     objects) and links the library."""
@@ -91,6 +110,9 @@ def build(verbose: bool = False, changed_only: bool = False) -> str:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}", file=sys.stderr)
+    if not changed_only or not os.path.exists(CEILING_LIB) or \
+            os.path.getmtime(CEILING_SRC) > os.path.getmtime(CEILING_LIB):
+        build_ceiling(verbose)
     return LIB_PATH
 
 

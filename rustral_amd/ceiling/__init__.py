@@ -1,0 +1,86 @@
+"""ctypes binding of librkv_ceiling.so: stream kernels that measure what HBM
+delivers on this part for the access patterns of the paged-KV kernels (flat
+read / write / copy, block copies, the decode kernel's tile loads with the
+arithmetic removed).  A measurement aid for ``bench.py --workload
+ceilings``, not part of the product ABI; torch supplies the device buffers
+and the stream."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+from rustral_amd.build import LIB_DIR
+
+CEILING_LIB = os.path.join(LIB_DIR, "librkv_ceiling.so")
+
+_SIG = {
+    "rkvc_read": [C.c_void_p, C.c_int64, C.c_void_p, C.c_uint, C.c_int, C.c_void_p],
+    "rkvc_write": [C.c_void_p, C.c_int64, C.c_int, C.c_void_p],
+    "rkvc_copy": [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p],
+    "rkvc_block_copy": [C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p],
+    "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                         C.c_int, C.c_int64, C.c_int, C.c_void_p, C.c_uint, C.c_void_p],
+}
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        # torch first: its HIP runtime (soname libamdhip64.so.7) is then the
+        # one this library binds to, so torch's buffers and streams are valid
+        # here; loaded the other way round the process holds two runtimes
+        import torch  # noqa: F401
+        if not os.path.exists(CEILING_LIB):
+            raise ImportError(f"{CEILING_LIB} is missing: build it with `python -m rustral_amd.build`")
+        L = C.CDLL(CEILING_LIB)
+        for name, args in _SIG.items():
+            fn = getattr(L, name)
+            fn.restype = C.c_int
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _stream(torch, dev):
+    return C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _ok(rc: int, what: str) -> None:
+    if rc < 0:
+        raise ValueError(f"{what}: invalid argument")
+    if rc > 0:
+        raise RuntimeError(f"{what}: launch failed (hipError_t {rc})")
+
+
+def read(torch, buf, sink, grid: int = 4096) -> None:
+    _ok(lib().rkvc_read(buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
+                        0x9E3779B9, grid, _stream(torch, buf.device)), "rkvc_read")
+
+
+def write(torch, buf, grid: int = 8192) -> None:
+    _ok(lib().rkvc_write(buf.data_ptr(), buf.numel() * buf.element_size(), grid,
+                         _stream(torch, buf.device)), "rkvc_write")
+
+
+def copy(torch, src, dst, grid: int = 8192) -> None:
+    n = src.numel() * src.element_size()
+    assert dst.numel() * dst.element_size() >= n
+    _ok(lib().rkvc_copy(src.data_ptr(), dst.data_ptr(), n, grid, _stream(torch, src.device)),
+        "rkvc_copy")
+
+
+def block_copy(torch, pool, pairs, block_bytes: int) -> None:
+    """pairs: int32 [n, 2] (src, dst) on the device; pool: the blocks."""
+    nb = pool.numel() * pool.element_size() // block_bytes
+    _ok(lib().rkvc_block_copy(pool.data_ptr(), pairs.data_ptr(), pairs.shape[0], block_bytes, nb,
+                              _stream(torch, pool.device)), "rkvc_block_copy")
+
+
+def tile_stream(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int) -> None:
+    """bf16 pools [num_blocks, Hkv, 16, 128]; tables int32 [B, max_blocks]."""
+    nb, hkv = k_pool.shape[0], k_pool.shape[1]
+    _ok(lib().rkvc_tile_stream(k_pool.data_ptr(), v_pool.data_ptr(), tables.data_ptr(),
+                               tables.shape[1], ctx_lens.data_ptr(), tables.shape[0], hkv, nb,
+                               partitions, sink.data_ptr(), 0x9E3779B9,
+                               _stream(torch, k_pool.device)), "rkvc_tile_stream")

@@ -1,0 +1,230 @@
+// ceiling.hip -- what HBM streams at on this part, for the access patterns of
+// the paged-KV kernels: a measurement library (librkv_ceiling.so), not part
+// of the product ABI.  The kernels move bytes and do no arithmetic beyond
+// folding what they read into a value that is stored only when it equals a
+// runtime argument (so the loads cannot be dropped).
+//
+//   rkvc_read         flat read, nontemporal 16-byte loads, grid-stride
+//   rkvc_write        flat write, 16-byte stores, grid-stride
+//   rkvc_copy         flat copy, nontemporal loads and stores
+//   rkvc_block_copy   one workgroup per (src, dst) pair of fixed-size blocks
+//                     within one pool (the copy_blocks pattern)
+//   rkvc_tile_stream  the decode kernel's loads alone: grid (Hkv, partitions,
+//                     sequences), 4 waves per 640-token partition, each wave
+//                     streaming 10 K then 10 V (block, head) tiles of bf16
+//                     D = 128 through a ring of 4 tiles, four 256-byte rows
+//                     per wave-load, tiles past the context re-reading the
+//                     wave's first tile
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <type_traits>
+
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ u32x4 ld(const u32x4* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool NT>
+__device__ __forceinline__ void st(u32x4* p, u32x4 v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+__device__ __forceinline__ unsigned fold(u32x4 a) { return a[0] ^ a[1] ^ a[2] ^ a[3]; }
+
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+constexpr int kUnr = 8;
+
+__global__ __launch_bounds__(256) void read_kernel(const u32x4* __restrict__ s, int64_t n,
+                                                   unsigned* sink, unsigned magic) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * kUnr;
+  unsigned acc = 0;
+  for (int64_t u0 = (int64_t)blockIdx.x * 256 * kUnr + threadIdx.x; u0 < n; u0 += stride) {
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) acc ^= fold(ld<true>(s + u));
+    }
+  }
+  if (acc == magic) sink[0] = acc;
+}
+
+__global__ __launch_bounds__(256) void write_kernel(u32x4* __restrict__ d, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * kUnr;
+  const u32x4 v = {threadIdx.x, blockIdx.x, 0x3f800000u, 0u};
+  for (int64_t u0 = (int64_t)blockIdx.x * 256 * kUnr + threadIdx.x; u0 < n; u0 += stride) {
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) st<false>(d + u, v);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ s,
+                                                   u32x4* __restrict__ d, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * kUnr;
+  for (int64_t u0 = (int64_t)blockIdx.x * 256 * kUnr + threadIdx.x; u0 < n; u0 += stride) {
+    u32x4 x[kUnr];
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) x[k] = ld<true>(s + u);
+    }
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) st<true>(d + u, x[k]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void block_copy_kernel(char* __restrict__ pool,
+                                                         const int32_t* __restrict__ pairs,
+                                                         int64_t block_bytes, int64_t num_blocks) {
+  const int32_t src = pairs[2 * blockIdx.x], dst = pairs[2 * blockIdx.x + 1];
+  if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) return;
+  const u32x4* s = reinterpret_cast<const u32x4*>(pool + src * block_bytes);
+  u32x4* d = reinterpret_cast<u32x4*>(pool + dst * block_bytes);
+  const int64_t n = block_bytes >> 4;
+  for (int64_t u0 = threadIdx.x; u0 < n; u0 += kUnr * 256) {
+    u32x4 x[kUnr];
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) x[k] = ld<true>(s + u);
+    }
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) st<true>(d + u, x[k]);
+    }
+  }
+}
+
+// bf16, D = 128, 16-token blocks: a (block, head) tile is 4 KiB.
+constexpr int kD = 128, kBS = 16, kNTW = 10, kNT = 2 * kNTW, kR = 4, kSplit = 4;
+constexpr int kP = kNTW * kSplit * kBS;  // tokens per partition (640)
+
+__global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
+    const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
+    const int32_t* __restrict__ tables, int max_blocks, const int32_t* __restrict__ ctx_lens,
+    int num_kv_heads, int64_t num_blocks, unsigned* sink, unsigned magic) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int kh = blockIdx.x, part = blockIdx.y, b = blockIdx.z;
+  const int L = ctx_lens[b];
+  if (part * kP >= L) return;
+  const int lb0 = part * (kP / kBS) + w * kNTW;
+  const int32_t* tab = tables + (int64_t)b * max_blocks;
+  int32_t pb[kNTW];
+#pragma unroll
+  for (int i = 0; i < kNTW; ++i) {
+    const int lb = lb0 + i;
+    pb[i] = tab[lb < max_blocks ? lb : max_blocks - 1];
+  }
+  const int32_t pb0 = pb[0] >= 0 && pb[0] < num_blocks ? pb[0] : 0;
+  int64_t base[kNTW];
+#pragma unroll
+  for (int i = 0; i < kNTW; ++i) {
+    const bool ok = (lb0 + i) * kBS < L && pb[i] >= 0 && pb[i] < num_blocks;
+    base[i] = ((int64_t)(ok ? pb[i] : pb0) * num_kv_heads + kh) * kBS * kD * 2;  // bytes
+  }
+  const uint32_t off = ((lane >> 4) * kD + (lane & 15) * 8) * 2;  // row lane/16, 16 B chunk
+  auto tile_load = [&](int t, int n) __attribute__((always_inline)) {
+    const char* p = reinterpret_cast<const char*>(t < kNTW ? k_pool : v_pool) + base[t % kNTW];
+    return ld<true>(reinterpret_cast<const u32x4*>(p + off + n * 4 * kD * 2));
+  };
+  u32x4 ring[kR][4];
+#pragma unroll
+  for (int t = 0; t < kR; ++t)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) ring[t][n] = tile_load(t, n);
+  unsigned acc = 0;
+  static_for<0, kNT>([&](auto tc) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc ^= fold(ring[t % kR][n]) + t;
+    if constexpr (t + kR < kNT) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) ring[t % kR][n] = tile_load(t + kR, n);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  if (acc == magic) sink[0] = acc;
+}
+
+// The launch's own status: an error left by an earlier runtime call of the
+// process is cleared before the launch (clear_errors), so it is not
+// reported as this launch's.  Returns 0 or the positive hipError_t code.
+void clear_errors() { (void)hipGetLastError(); }
+int launched() { return (int)hipGetLastError(); }
+
+}  // namespace
+
+extern "C" {
+
+int rkvc_read(const void* src, int64_t bytes, unsigned* sink, unsigned magic, int grid,
+              void* stream) {
+  if (!src || !sink || bytes < 16 || (bytes & 15) || grid <= 0) return -1;
+  clear_errors();
+  read_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4*>(src), bytes >> 4, sink, magic);
+  return launched();
+}
+
+int rkvc_write(void* dst, int64_t bytes, int grid, void* stream) {
+  if (!dst || bytes < 16 || (bytes & 15) || grid <= 0) return -1;
+  clear_errors();
+  write_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<u32x4*>(dst),
+                                                                   bytes >> 4);
+  return launched();
+}
+
+int rkvc_copy(const void* src, void* dst, int64_t bytes, int grid, void* stream) {
+  if (!src || !dst || bytes < 16 || (bytes & 15) || grid <= 0) return -1;
+  clear_errors();
+  copy_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), bytes >> 4);
+  return launched();
+}
+
+int rkvc_block_copy(void* pool, const int32_t* pairs, int n_pairs, int64_t block_bytes,
+                    int64_t num_blocks, void* stream) {
+  if (!pool || !pairs || n_pairs <= 0 || block_bytes <= 0 || (block_bytes & 15) ||
+      num_blocks <= 0)
+    return -1;
+  clear_errors();
+  block_copy_kernel<<<n_pairs, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<char*>(pool), pairs, block_bytes, num_blocks);
+  return launched();
+}
+
+// Pools [num_blocks][num_kv_heads][16][128] bf16; tables int32 [B][max_blocks]
+// (ids outside [0, num_blocks) are absent); partitions = ceil(max_ctx / 640).
+int rkvc_tile_stream(const void* k_pool, const void* v_pool, const int32_t* tables,
+                     int max_blocks, const int32_t* ctx_lens, int num_seqs, int num_kv_heads,
+                     int64_t num_blocks, int partitions, unsigned* sink, unsigned magic,
+                     void* stream) {
+  if (!k_pool || !v_pool || !tables || !ctx_lens || !sink || max_blocks <= 0 ||
+      num_seqs <= 0 || num_kv_heads <= 0 || num_blocks <= 0 || partitions <= 0)
+    return -1;
+  const dim3 grid((unsigned)num_kv_heads, (unsigned)partitions, (unsigned)num_seqs);
+  clear_errors();
+  tile_stream_kernel<<<grid, 64 * kSplit, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(k_pool), static_cast<const uint16_t*>(v_pool), tables,
+      max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
+  return launched();
+}
+
+}  // extern "C"

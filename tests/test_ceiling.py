@@ -1,0 +1,62 @@
+"""The measurement library of ``bench.py --workload ceilings``
+(rustral_amd/ceiling, librkv_ceiling.so): it loads and exports its five
+stream kernels (CPU); on the GPU its copies copy (bit-exact) and its read
+and decode-pattern streams leave the sink untouched (their fold is stored
+only when it equals a runtime value that no fold of these inputs takes)."""
+import numpy as np
+import pytest
+import torch
+
+from rustral_amd import ceiling as C
+
+NAMES = ("rkvc_read", "rkvc_write", "rkvc_copy", "rkvc_block_copy", "rkvc_tile_stream")
+
+
+def test_library_loads_and_exports_the_stream_kernels():
+    L = C.lib()
+    for n in NAMES:
+        assert hasattr(L, n), n
+
+
+def test_arguments_are_checked_before_any_launch():
+    L = C.lib()
+    assert L.rkvc_read(None, 1 << 20, None, 0, 16, None) != 0
+    assert L.rkvc_copy(None, None, 100, 16, None) != 0        # also not a multiple of 16
+    assert L.rkvc_block_copy(None, None, 0, 32768, 1, None) != 0
+    assert L.rkvc_tile_stream(None, None, None, 0, None, 0, 0, 0, 0, None, 0, None) != 0
+
+
+@pytest.mark.gpu
+def test_copies_are_bit_exact_and_streams_leave_the_sink(dev):
+    from tests.gpu_util import say
+    say("ceiling kernels: copy, block copy, read, tile stream")
+    g = torch.Generator(device=dev).manual_seed(3)
+    a = torch.randint(-2 ** 31, 2 ** 31 - 1, (1 << 22,), generator=g, dtype=torch.int32, device=dev)
+    b = torch.zeros_like(a)
+    C.copy(torch, a, b, grid=64)
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    C.read(torch, a, sink, grid=64)
+    C.write(torch, b[: 1 << 20], grid=16)                     # rows 0 .. 2^20 rewritten
+    torch.cuda.synchronize()
+    assert torch.equal(a[1 << 20:], b[1 << 20:])
+    assert int(sink.abs().sum()) == 0
+    # block copy: 8 KiB blocks of a 16 MiB pool, disjoint sources and targets
+    pool = a.clone()
+    nblk, blk = pool.numel() * 4 // 8192, 8192
+    rng = np.random.default_rng(1)
+    perm = rng.permutation(nblk).astype(np.int32)
+    pairs = np.stack([perm[:64], perm[64:128]], 1)
+    C.block_copy(torch, pool, torch.from_numpy(pairs).to(dev), blk)
+    torch.cuda.synchronize()
+    want = a.cpu().numpy().reshape(nblk, -1).copy()
+    want[pairs[:, 1]] = want[pairs[:, 0]]
+    assert np.array_equal(pool.cpu().numpy().reshape(nblk, -1), want)
+    # the decode pattern over a small bf16 pool (ids outside the pool are absent)
+    nb, hkv = 64, 2
+    k = torch.randn((nb, hkv, 16, 128), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn_like(k)
+    tab = torch.tensor([[3, 9, -1, 70], [5, 6, 7, 8]], dtype=torch.int32, device=dev)
+    ctx = torch.tensor([40, 64], dtype=torch.int32, device=dev)
+    C.tile_stream(torch, k, v, tab, ctx, sink, partitions=1)
+    torch.cuda.synchronize()
+    assert int(sink.abs().sum()) == 0
