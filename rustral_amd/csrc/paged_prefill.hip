@@ -264,13 +264,19 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     constexpr bool MASKED = decltype(masked)::value;
     const int kfirst = it * KB * kBS;
 
-    // ---- S^T = K Q^T for the KB * 16 keys, per head ----
+    // ---- S^T - m = K Q^T - m for the KB * 16 keys, per head ----
+    // The accumulators start at -mref (the row's reference maximum, 0 before
+    // the row has seen a key), so the scores come out of the matrix cores
+    // already relative to it: no subtraction before the exponentials.
+    float mref[HW];
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) mref[hh] = m[hh] == -INFINITY ? 0.0f : m[hh];
     float s[HW][KB][4];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
       f32x4_t st[HW];
 #pragma unroll
-      for (int hh = 0; hh < HW; ++hh) st[hh] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int hh = 0; hh < HW; ++hh) st[hh] = f32x4_t{-mref[hh], -mref[hh], -mref[hh], -mref[hh]};
       const uint16_t* kr0 = &s_k[buf][0][(kb * kBS + r16) * KP + 8 * grp];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -315,8 +321,11 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     // more than kSlack (log2 units, a factor 2^8): exponentials stay <= 2^8,
     // exact in fp32 and split hi + lo as before, and the rare rescale of the
     // accumulators is one wave-uniform branch for all heads of the wave.
+    // Whether some row needs it is decided from each lane's own keys (a
+    // row's maximum exceeds m + kSlack iff one of its lanes' does), so the
+    // cross-lane maximum is only taken inside the branch.
     constexpr float kSlack = 8.0f;
-    float mn[HW];
+    float lm[HW];
     bool up = false;
 #pragma unroll
     for (int hh = 0; hh < HW; ++hh) {
@@ -324,32 +333,40 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
         mb = max2(mb, max2(max2(s[hh][kb][0], s[hh][kb][1]), max2(s[hh][kb][2], s[hh][kb][3])));
-      mn[hh] = max2(m[hh], xor48_max(mb));
-      up = up || mn[hh] > m[hh] + kSlack;  // -inf + 8 = -inf: the first key always moves m
+      lm[hh] = mb;  // relative to mref
+      // before the row's first key (m = -inf) any key moves m
+      up = up || mb > (m[hh] == -INFINITY ? -INFINITY : kSlack);
     }
     if (__builtin_amdgcn_ballot_w64(up) != 0) {
 #pragma unroll
       for (int hh = 0; hh < HW; ++hh) {
+        const float mx = xor48_max(lm[hh]);  // the row's maximum, relative to mref
+        const float mn = max2(m[hh], mx == -INFINITY ? -INFINITY : mx + mref[hh]);
+        const float mref_new = mn == -INFINITY ? 0.0f : mn;
         // rows without any key so far (m = -inf) get alpha = 0 on o = l = 0
-        const float alpha = __builtin_amdgcn_exp2f(m[hh] - (mn[hh] == -INFINITY ? 0.0f : mn[hh]));
+        const float alpha = __builtin_amdgcn_exp2f(m[hh] - mref_new);
         l[hh] *= alpha;
 #pragma unroll
         for (int c = 0; c < NO; ++c)
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[hh][c][r] *= alpha;
-        m[hh] = mn[hh];
+        m[hh] = mn;
+        const float d = mref_new - mref[hh];  // the scores move to the new reference
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[hh][kb][r] -= d;
       }
     }
 #pragma unroll
     for (int hh = 0; hh < HW; ++hh) {
-      const float mref = m[hh] == -INFINITY ? 0.0f : m[hh];
       float ls = 0.0f;
       // v_exp_f32 directly: exp2(-inf) = 0, results below 2^-126 do not matter
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          s[hh][kb][r] = __builtin_amdgcn_exp2f(s[hh][kb][r] - mref);
+          s[hh][kb][r] = __builtin_amdgcn_exp2f(s[hh][kb][r]);
           ls += s[hh][kb][r];
         }
       l[hh] += ls;  // this lane's keys of the row; the row's lanes are summed at the end
