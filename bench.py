@@ -906,13 +906,45 @@ def run_ceilings(torch, dev, args):
     res["decode_partition_kernel"] = {"GBps_kv": dp["GBps"],
                                       "us_per_layer": round(dp["us"] / n_layers, 2)}
     ratio = round(dp["GBps"] / st["GBps"], 4)
+    # the same shape, tables and q over 1-byte pools (int8 bytes, fp32 row scales)
+    g8 = torch.Generator(device=dev).manual_seed(SEED + 1)
+    layers8 = []
+    for i in range(n_layers):
+        q, k, v, t = layers[i]
+        shp = tuple(k.shape)
+        layers[i] = None                          # the bf16 pools are not needed any more
+        kp = torch.randint(0, 256, shp, generator=g8, dtype=torch.uint8, device=dev)
+        vp = torch.randint(0, 256, shp, generator=g8, dtype=torch.uint8, device=dev)
+        ks = torch.rand(shp[:3], generator=g8, device=dev) * 0.02
+        vs = torch.rand(shp[:3], generator=g8, device=dev) * 0.02
+        layers8.append((q, kp, vp, ks, vs, t))
+    del layers
+    torch.cuda.empty_cache()
+    kv8_bytes = sum(int(L) * HKV * (D + 4) * 2 for L in ctx)
+
+    def stream8_all():
+        for q, kp, vp, ks, vs, t in layers8:
+            C.tile_stream(torch, kp, vp, t, ctx_d, sink, parts, k_scale=ks, v_scale=vs)
+    st8 = rate(stream8_all, kv8_bytes * n_layers)
+    res["decode_tile_stream_1byte"] = {"GBps": st8["GBps"],
+                                       "us_per_layer": round(st8["us"] / n_layers, 2),
+                                       "kv_bytes_per_layer": kv8_bytes}
+
+    def decode8_all():
+        for q, kp, vp, ks, vs, t in layers8:
+            kv.decode_attention_q(q, kp, vp, ks, vs, t, ctx_d, scale, "int8",
+                                  max_context=max_ctx, out=out, workspace=ws)
+    d8 = rate(decode8_all, kv8_bytes * n_layers)
+    res["decode_int8_both_passes"] = {"GBps_kv": d8["GBps"],
+                                      "us_per_layer": round(d8["us"] / n_layers, 2)}
     return _line("HBM ceilings of the paged-KV access patterns: the decode kernel's loads "
                  "streamed with no arithmetic (configs[2])", st["GBps"], "GB/s",
                  st["us"] / n_layers / 1e3, args, "bf16",
                  {"workload": "stream kernels of rustral_amd/ceiling; configs[2] pools for the "
                               "decode pattern", "flat_bytes": nbytes, "block_bytes": blk,
                   "block_pairs": npairs, "layers": n_layers},
-                 decode_partition_over_stream=ratio, results=res)
+                 decode_partition_over_stream=ratio,
+                 decode_int8_over_stream_1byte=round(d8["GBps"] / st8["GBps"], 4), results=res)
 
 
 def main():

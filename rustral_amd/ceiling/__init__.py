@@ -18,8 +18,9 @@ _SIG = {
     "rkvc_write": [C.c_void_p, C.c_int64, C.c_int, C.c_void_p],
     "rkvc_copy": [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p],
     "rkvc_block_copy": [C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p],
-    "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
-                         C.c_int, C.c_int64, C.c_int, C.c_void_p, C.c_uint, C.c_void_p],
+    "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                         C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_void_p,
+                         C.c_uint, C.c_void_p],
 }
 _lib = None
 
@@ -77,10 +78,15 @@ def block_copy(torch, pool, pairs, block_bytes: int) -> None:
                               _stream(torch, pool.device)), "rkvc_block_copy")
 
 
-def tile_stream(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int) -> None:
-    """bf16 pools [num_blocks, Hkv, 16, 128]; tables int32 [B, max_blocks]."""
+def tile_stream(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int,
+                k_scale=None, v_scale=None) -> None:
+    """Pools [num_blocks, Hkv, 16, 128] of bf16, or of 1-byte elements with
+    fp32 scales [num_blocks, Hkv, 16]; tables int32 [B, max_blocks]."""
     nb, hkv = k_pool.shape[0], k_pool.shape[1]
-    _ok(lib().rkvc_tile_stream(k_pool.data_ptr(), v_pool.data_ptr(), tables.data_ptr(),
-                               tables.shape[1], ctx_lens.data_ptr(), tables.shape[0], hkv, nb,
-                               partitions, sink.data_ptr(), 0x9E3779B9,
+    eb = k_pool.element_size()
+    ks = k_scale.data_ptr() if k_scale is not None else None
+    vs = v_scale.data_ptr() if v_scale is not None else None
+    _ok(lib().rkvc_tile_stream(k_pool.data_ptr(), v_pool.data_ptr(), ks, vs, eb,
+                               tables.data_ptr(), tables.shape[1], ctx_lens.data_ptr(),
+                               tables.shape[0], hkv, nb, partitions, sink.data_ptr(), 0x9E3779B9,
                                _stream(torch, k_pool.device)), "rkvc_tile_stream")

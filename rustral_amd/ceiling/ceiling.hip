@@ -11,10 +11,11 @@
 //                     within one pool (the copy_blocks pattern)
 //   rkvc_tile_stream  the decode kernel's loads alone: grid (Hkv, partitions,
 //                     sequences), 4 waves per 640-token partition, each wave
-//                     streaming 10 K then 10 V (block, head) tiles of bf16
-//                     D = 128 through a ring of 4 tiles, four 256-byte rows
-//                     per wave-load, tiles past the context re-reading the
-//                     wave's first tile
+//                     streaming 10 K then 10 V (block, head) tiles of
+//                     D = 128 (bf16, or 1-byte with row scales) through a
+//                     ring of 4 tiles, 1 KiB of whole rows per wave-load,
+//                     tiles past the context re-reading the wave's first
+//                     tile
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -113,14 +114,23 @@ __global__ __launch_bounds__(256) void block_copy_kernel(char* __restrict__ pool
   }
 }
 
-// bf16, D = 128, 16-token blocks: a (block, head) tile is 4 KiB.
+// D = 128, 16-token blocks.  EB = 2 (bf16): a (block, head) tile is 4 KiB,
+// four 256-byte rows per wave-load.  EB = 1 (1-byte pools): a tile is 2 KiB,
+// eight 128-byte rows per wave-load, plus the fp32 row scales the decode
+// kernel reads (one K scale per lane and K tile, the V scales of the wave's
+// slice up front).
 constexpr int kD = 128, kBS = 16, kNTW = 10, kNT = 2 * kNTW, kR = 4, kSplit = 4;
 constexpr int kP = kNTW * kSplit * kBS;  // tokens per partition (640)
 
+template <int EB>
 __global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
-    const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
+    const uint8_t* __restrict__ k_pool, const uint8_t* __restrict__ v_pool,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale,
     const int32_t* __restrict__ tables, int max_blocks, const int32_t* __restrict__ ctx_lens,
     int num_kv_heads, int64_t num_blocks, unsigned* sink, unsigned magic) {
+  constexpr int ROW = kD * EB;          // bytes per token row
+  constexpr int RPL = 1024 / ROW;       // rows per 1 KiB wave-load
+  constexpr int NL = kBS / RPL;         // wave-loads per tile
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kh = blockIdx.x, part = blockIdx.y, b = blockIdx.z;
   const int L = ctx_lens[b];
@@ -134,33 +144,44 @@ __global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
     pb[i] = tab[lb < max_blocks ? lb : max_blocks - 1];
   }
   const int32_t pb0 = pb[0] >= 0 && pb[0] < num_blocks ? pb[0] : 0;
-  int64_t base[kNTW];
+  int64_t row0[kNTW];  // first token row of each (block, head) tile
 #pragma unroll
   for (int i = 0; i < kNTW; ++i) {
     const bool ok = (lb0 + i) * kBS < L && pb[i] >= 0 && pb[i] < num_blocks;
-    base[i] = ((int64_t)(ok ? pb[i] : pb0) * num_kv_heads + kh) * kBS * kD * 2;  // bytes
+    row0[i] = ((int64_t)(ok ? pb[i] : pb0) * num_kv_heads + kh) * kBS;
   }
-  const uint32_t off = ((lane >> 4) * kD + (lane & 15) * 8) * 2;  // row lane/16, 16 B chunk
+  const uint32_t off = (lane / (64 / RPL)) * ROW + (lane % (64 / RPL)) * 16;
   auto tile_load = [&](int t, int n) __attribute__((always_inline)) {
-    const char* p = reinterpret_cast<const char*>(t < kNTW ? k_pool : v_pool) + base[t % kNTW];
-    return ld<true>(reinterpret_cast<const u32x4*>(p + off + n * 4 * kD * 2));
+    const uint8_t* p = (t < kNTW ? k_pool : v_pool) + row0[t % kNTW] * ROW;
+    return ld<true>(reinterpret_cast<const u32x4*>(p + off + n * 1024));
   };
-  u32x4 ring[kR][4];
+  unsigned acc = 0;
+  u32x4 ring[kR][NL];
 #pragma unroll
   for (int t = 0; t < kR; ++t)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) ring[t][n] = tile_load(t, n);
-  unsigned acc = 0;
+    for (int n = 0; n < NL; ++n) ring[t][n] = tile_load(t, n);
+  float sc = 0.0f;
+  if constexpr (EB == 1) {
+#pragma unroll
+    for (int i = 0; i < kNTW; ++i) sc += k_scale[row0[i] + (lane & 15)];
+#pragma unroll
+    for (int j = 0; j < (kNTW * kBS + 63) / 64; ++j) {
+      const int x = lane + 64 * j;
+      if (x < kNTW * kBS) sc += v_scale[row0[x / kBS] + x % kBS];
+    }
+  }
   static_for<0, kNT>([&](auto tc) __attribute__((always_inline)) {
     constexpr int t = decltype(tc)::value;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc ^= fold(ring[t % kR][n]) + t;
+    for (int n = 0; n < NL; ++n) acc ^= fold(ring[t % kR][n]) + t;
     if constexpr (t + kR < kNT) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) ring[t % kR][n] = tile_load(t + kR, n);
+      for (int n = 0; n < NL; ++n) ring[t % kR][n] = tile_load(t + kR, n);
     }
     __builtin_amdgcn_sched_barrier(0);
   });
+  acc += __float_as_uint(sc);
   if (acc == magic) sink[0] = acc;
 }
 
@@ -210,20 +231,24 @@ int rkvc_block_copy(void* pool, const int32_t* pairs, int n_pairs, int64_t block
   return launched();
 }
 
-// Pools [num_blocks][num_kv_heads][16][128] bf16; tables int32 [B][max_blocks]
-// (ids outside [0, num_blocks) are absent); partitions = ceil(max_ctx / 640).
-int rkvc_tile_stream(const void* k_pool, const void* v_pool, const int32_t* tables,
-                     int max_blocks, const int32_t* ctx_lens, int num_seqs, int num_kv_heads,
-                     int64_t num_blocks, int partitions, unsigned* sink, unsigned magic,
-                     void* stream) {
+// Pools [num_blocks][num_kv_heads][16][128] of elem_bytes-byte elements
+// (2: bf16; 1: int8 / fp8, with fp32 scales [num_blocks][num_kv_heads][16]);
+// tables int32 [B][max_blocks] (ids outside [0, num_blocks) are absent);
+// partitions = ceil(max_ctx / 640).
+int rkvc_tile_stream(const void* k_pool, const void* v_pool, const float* k_scale,
+                     const float* v_scale, int elem_bytes, const int32_t* tables, int max_blocks,
+                     const int32_t* ctx_lens, int num_seqs, int num_kv_heads, int64_t num_blocks,
+                     int partitions, unsigned* sink, unsigned magic, void* stream) {
   if (!k_pool || !v_pool || !tables || !ctx_lens || !sink || max_blocks <= 0 ||
-      num_seqs <= 0 || num_kv_heads <= 0 || num_blocks <= 0 || partitions <= 0)
+      num_seqs <= 0 || num_kv_heads <= 0 || num_blocks <= 0 || partitions <= 0 ||
+      (elem_bytes != 1 && elem_bytes != 2) || (elem_bytes == 1 && (!k_scale || !v_scale)))
     return -1;
   const dim3 grid((unsigned)num_kv_heads, (unsigned)partitions, (unsigned)num_seqs);
   clear_errors();
-  tile_stream_kernel<<<grid, 64 * kSplit, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(k_pool), static_cast<const uint16_t*>(v_pool), tables,
-      max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
+  auto kern = elem_bytes == 2 ? tile_stream_kernel<2> : tile_stream_kernel<1>;
+  kern<<<grid, 64 * kSplit, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool), k_scale, v_scale,
+      tables, max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
   return launched();
 }
 

@@ -23,7 +23,8 @@ def test_arguments_are_checked_before_any_launch():
     assert L.rkvc_read(None, 1 << 20, None, 0, 16, None) != 0
     assert L.rkvc_copy(None, None, 100, 16, None) != 0        # also not a multiple of 16
     assert L.rkvc_block_copy(None, None, 0, 32768, 1, None) != 0
-    assert L.rkvc_tile_stream(None, None, None, 0, None, 0, 0, 0, 0, None, 0, None) != 0
+    assert L.rkvc_tile_stream(None, None, None, None, 2, None, 0, None, 0, 0, 0, 0, None, 0,
+                              None) != 0
 
 
 @pytest.mark.gpu
@@ -58,5 +59,9 @@ def test_copies_are_bit_exact_and_streams_leave_the_sink(dev):
     tab = torch.tensor([[3, 9, -1, 70], [5, 6, 7, 8]], dtype=torch.int32, device=dev)
     ctx = torch.tensor([40, 64], dtype=torch.int32, device=dev)
     C.tile_stream(torch, k, v, tab, ctx, sink, partitions=1)
+    k8 = torch.randint(0, 255, (nb, hkv, 16, 128), generator=g, dtype=torch.uint8, device=dev)
+    v8 = torch.randint(0, 255, (nb, hkv, 16, 128), generator=g, dtype=torch.uint8, device=dev)
+    ks = torch.rand((nb, hkv, 16), generator=g, device=dev)
+    C.tile_stream(torch, k8, v8, tab, ctx, sink, partitions=1, k_scale=ks, v_scale=ks.clone())
     torch.cuda.synchronize()
     assert int(sink.abs().sum()) == 0

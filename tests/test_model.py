@@ -347,6 +347,26 @@ def test_gpu_argmax_matches_reference_rule(torch_dev):
 
 
 @pytest.mark.gpu
+def test_gpu_decoder_pool_size_does_not_change_tokens(dev):
+    """The same weights in decoders of max_seq 1024 and 128 (64 and 8 KV
+    blocks per layer, other attention grids): tokens equal the CPU
+    decoder's in both, logits within 1e-4 / 1e-3 of it and of each other."""
+    from tests.gpu_util import say
+    say("decoder: max_seq 1024 and 128")
+    params = model.init_params(model.config(), seed=5, std=0.02)
+    prompt = np.random.default_rng(6).integers(0, 1000, 20).astype(np.int32)
+    want, wlg = oracle.decoder_generate(oracle.decoder_config(), params, prompt, 40, logits=True)
+    outs = []
+    for max_seq in (1024, 128):
+        dec = model.Decoder(model.config(max_seq=max_seq), params)
+        toks, lg = dec.generate(prompt, 40, logits=True)
+        assert toks.tolist() == want.tolist(), max_seq
+        np.testing.assert_allclose(lg, wlg, atol=1e-4, rtol=1e-3)
+        outs.append(lg)
+    np.testing.assert_allclose(outs[0], outs[1], atol=1e-4, rtol=1e-3)
+
+
+@pytest.mark.gpu
 def test_gpu_decoder_config0_tokens_equal_oracle(dev):
     """weights N(0, 0.02) from seed 0, prompt of 32 ids from seed
     0, 64 greedy tokens through paged KV (16-token blocks): token-identical
