@@ -23,6 +23,11 @@
 //     mapping as the loads (each lane accumulates p[g][token] * v for its E
 //     dims, then lanes of different rows are summed by shuffles).  The waves
 //     of a partition combine their states through LDS.
+//   * int8 pools (G <= 4) keep both products on the integer matrix cores:
+//     q and the PV weights are split into three int8 limbs (fixed point
+//     against the head's maximum, ~24 bits), the stored bytes enter
+//     v_mfma_i32_16x16x64_i8 / _16x16x32_i8 unconverted and the int32 sums
+//     are exact; fp8 pools convert their bytes to bf16 (exact).
 // Pass 2 (decode_merge_kernel): per (query head, sequence) merge of the
 // partition partials m (max), l (sum), acc (unnormalised PV):
 //   M = max m_p;  out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.
@@ -71,9 +76,10 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Matrix-core operand types (v_mfma_f32_16x16x32_bf16).
+// Matrix-core operand types (bf16 and int8 MFMAs).
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 typedef __attribute__((ext_vector_type(4))) short bf16x4_t;
 
 // Converts one 16-byte load into E floats.
@@ -176,12 +182,12 @@ __device__ __forceinline__ float lo_col(float x) {
 //                 G..2G-1 = bf16(q - bf16(q)), other rows zero.  hi + lo keeps
 //                 ~16 significant bits of q: scores as accurate as fp32 dots.
 //   B (32 x 16) = K^T of the tile: lane l holds 16 bytes of token row l % 16
-//                 at dims 32c + 8 (l / 16).  bf16 tiles are loaded like V
-//                 tiles (four 256-byte rows per wave-load) and reach this
-//                 layout through the wave's LDS staging buffer: loading it
-//                 straight from the pool touches 16 rows x 64 bytes per
-//                 wave-load, half of every 128-byte line, which streams ~9%
-//                 slower.  1-byte tiles are loaded in the operand layout.
+//                 at dims 32c + 8 (l / 16) (bf16).  K tiles are loaded like
+//                 V tiles (contiguous token rows, 1 KiB per wave-load) and
+//                 reach this layout through the wave's LDS staging buffer:
+//                 loading it straight from the pool touches 16 rows x 64
+//                 bytes per wave-load, half of every 128-byte line, which
+//                 streams ~9% slower (RKV_DECODE_K_LDS=0 builds that form).
 //   D (16 x 16) = row 4 (l / 16) + r in lane l register r, column l % 16.
 // (Lane layout checked on gfx950: A[l%16][8(l/16)+e], B[8(l/16)+e][l%16],
 // D[4(l/16)+r][l%16].)  PV runs on the matrix cores too (below); fp32 pools
@@ -194,6 +200,16 @@ __device__ __forceinline__ float lo_col(float x) {
 // bf16 K tiles through LDS (1) or loaded in the MFMA operand layout (0).
 #ifndef RKV_DECODE_K_LDS
 #define RKV_DECODE_K_LDS 1
+#endif
+// int8 pools: QK^T on v_mfma_i32_16x16x64_i8 with q in three int8 limbs (1)
+// or on the bf16 MFMA with the K bytes converted (0); PV on
+// v_mfma_i32_16x16x32_i8 with the weights in three int8 limbs (1) or on the
+// bf16 MFMA with the V bytes converted (0).
+#ifndef RKV_DECODE_I8_QK
+#define RKV_DECODE_I8_QK 1
+#endif
+#ifndef RKV_DECODE_I8_PV
+#define RKV_DECODE_I8_PV 1
 #endif
 template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT>
 __global__ __launch_bounds__(64 * SPLIT)
@@ -264,6 +280,21 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // v_mfma_f32_16x16x16_bf16, ds_read_b64_tr_b16 (4 keys of one dim per lane),
   // which keeps the staging buffer at one tile.
   constexpr bool MPV = MFMA;
+  // int8 pools (G <= 4): QK^T on the integer matrix cores, exact in int32.
+  // q of head h is written as (M_h / 127) (a0 + a1 / 254 + a2 / 254^2) with
+  // M_h = max |q| over the head's dims and int8 limbs a0, a1, a2 (round to
+  // nearest at each step: |q - that sum| <= M_h 2^-23.9), the limbs are rows
+  // 4 h + j of A, and B is the stored K bytes as they are.  Row 4 h + j of
+  // the result lands in lane 16 h + token, register j: each lane combines
+  // the three limb dots of one (head, token) pair in its own registers.  No
+  // K byte is converted, and a 64-dim K block is one MFMA instead of two.
+  constexpr bool I8QK = MFMA && FMT == RKV_I8 && G <= 4 && RKV_DECODE_I8_QK;
+  // PV likewise: the weights w = p * (V row scale) of head h over the
+  // wave's slice are written as (W_h / 127) (b0 + b1 / 254 + b2 / 254^2)
+  // with W_h = their maximum, the limbs are the A rows 4 h + j (bytes in
+  // LDS, written once per slice by the softmax pass), B is the staged V
+  // bytes read transposed, and the int32 sums over the slice are exact.
+  constexpr bool I8PV = MPV && FMT == RKV_I8 && G <= 4 && RKV_DECODE_I8_PV;
   constexpr int VROW = QNT ? D + 16 : 2 * (D + 16);  // staged V row (bytes): the rows of
                                                       // one transposing read hit distinct banks
   constexpr int NK = NTW * BS;   // keys of this wave's slice
@@ -271,21 +302,25 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   static_assert(!MPV || NTW % VT == 0, "MFMA PV takes 1-byte V tiles in pairs");
   __shared__ __align__(16) uint8_t s_vq[MPV ? SPLIT : 1][MPV ? VT * BS * VROW : 16];
   __shared__ __align__(16) float s_pq[MPV ? SPLIT : 1][MPV ? G * NK : 4];  // p, head-major
-  f32x4_t ov[MPV ? D / 16 : 1];
+  f32x4_t ov[MPV && !I8PV ? D / 16 : 1];
 #pragma unroll
-  for (int c = 0; c < (MPV ? D / 16 : 1); ++c) ov[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < (MPV && !I8PV ? D / 16 : 1); ++c) ov[c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  i32x4_t iov[I8PV ? D / 16 : 1];  // I8PV: lane (kq, kt) rows 4 kq + r, dim 16 c + kt
+#pragma unroll
+  for (int c = 0; c < (I8PV ? D / 16 : 1); ++c) iov[c] = i32x4_t{0, 0, 0, 0};
+  float pmul = 0.0f;  // I8PV: W_h / 127 of head kq (NaN when a weight is NaN or inf)
   constexpr int NC = D / 32;                     // MFMAs per tile
   const int kt = lane & 15, kq = lane >> 4;      // MFMA lanes: token row, k-quarter
   // VALU path: this lane's E dims of each head.  MFMA path: the A operand
   // row kt (hi rows 0..G-1, lo rows G..2G-1), chunk c at dims 32c + 8 kq .. + 8
-  // for bf16; for 1-byte pools a lane loads the contiguous quarter
+  // for bf16; for 1-byte pools a lane reads the contiguous quarter
   // [D/4 kq, D/4 (kq+1)) of its key row, so chunk c holds dims D/4 kq + 8c ..
   // + 8 (any assignment of dims to k-slots gives the same dot product, as long
   // as q and K use the same one).
   constexpr int QN = MFMA ? NC * 8 : G * E;
   float qv[QN];
   if constexpr (MFMA) {
-    const int qrow = kt < G ? kt : (kt < 2 * G ? kt - G : 0);
+    const int qrow = I8QK ? (kt / 4 < G ? kt / 4 : 0) : (kt < G ? kt : (kt < 2 * G ? kt - G : 0));
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d0 = QNT ? (D / 4) * kq + 8 * c : 32 * c + 8 * kq;
@@ -392,7 +427,44 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // MFMA A operands: q split into bf16 hi + lo rows, two values per
   // v_cvt_pk_bf16_f32 (round to nearest even, no branch)
   uint4 qa[MFMA ? NC : 1];
-  if constexpr (MFMA) {
+  float qmul = 0.0f;  // I8QK: M_h / 127 of head kq (NaN when q_h holds NaN or inf)
+  if constexpr (I8QK) {
+    // M_h over the four lanes kt, kt + 16, kt + 32, kt + 48 (one head, a
+    // quarter of its dims each); z = 0, or NaN for a NaN / infinite q value
+    float amax = 0.0f, z = 0.0f;
+#pragma unroll
+    for (int e = 0; e < QN; ++e) {
+      amax = fmaxf(amax, fabsf(qv[e]));
+      z += qv[e] * 0.0f;
+    }
+    amax = pair32_max(pair16_max(amax));
+    z = pair32_sum(pair16_sum(z));
+    const float inv = amax >= 0x1p-120f ? 127.0f / amax : 0.0f;  // finite
+    const int limb = kt & 3;
+    const bool live = kt / 4 < G && limb < 3;
+#pragma unroll
+    for (int n = 0; n < NL; ++n) {
+      uint32_t h[4];
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = qv[16 * n + 4 * e4 + e] * inv;  // |a| <= 127
+          const float a0 = rintf(a);
+          const float r1 = (a - a0) * 254.0f;  // |r1| <= 127
+          const float a1 = rintf(r1);
+          const float a2 = rintf((r1 - a1) * 254.0f);
+          const float v = limb == 0 ? a0 : (limb == 1 ? a1 : a2);
+          word |= ((uint32_t)(int32_t)v & 0xffu) << (8 * e);
+        }
+        h[e4] = live ? word : 0u;
+      }
+      qa[n] = make_uint4(h[0], h[1], h[2], h[3]);
+    }
+    // this lane's result rows belong to head kq: its M_h sits in lane 4 kq
+    qmul = __shfl(amax * (1.0f / 127.0f) + z, 4 * kq);
+  } else if constexpr (MFMA) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       uint32_t h[4];
@@ -457,7 +529,16 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 #pragma unroll
           for (int n = 0; n < NL; ++n) kb[n] = tile[n];
         }
-        if constexpr (QNT) {
+        if constexpr (I8QK) {
+          i32x4_t iacc = {0, 0, 0, 0};
+#pragma unroll
+          for (int n = 0; n < NL; ++n)
+            iacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, qa[n]),
+                                                         __builtin_bit_cast(i32x4_t, kb[n]),
+                                                         iacc, 0, 0, 0);
+          sacc[0] = ((float)iacc[0] + (float)iacc[1] * (1.0f / 254.0f) +
+                     (float)iacc[2] * (1.0f / 64516.0f)) * qmul;
+        } else if constexpr (QNT) {
 #pragma unroll
           for (int n = 0; n < NL; ++n) {
             sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -480,7 +561,9 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
         if constexpr (QNT) qs *= ksc[i];
         const int tp = i * BS + kt;  // token of this lane's column
         const bool valid = ok[i] && (tok0 + tp < L);
-        if constexpr (G == 1) {
+        if constexpr (I8QK) {
+          if (kq < G) s_p[tp * G + kq] = valid ? sacc[0] * qs : -INFINITY;
+        } else if constexpr (G == 1) {
           if (kq == 0) s_p[tp] = valid ? (sacc[0] + sacc[1]) * qs : -INFINITY;
         } else if constexpr (G == 2) {
           if (kq == 0) {
@@ -536,6 +619,50 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
           m[g] = wave_max(m[g]);
           l[g] = 0.0f;
         }
+        if constexpr (I8PV) {
+          // weights in registers, their maximum per head, then the limbs
+          constexpr int NJ = (NK + 63) / 64;
+          float wv[NJ][G];
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const int x = lane + 64 * j;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              const float sv = x < NK ? s_p[x * G + g] : -INFINITY;
+              const float pv = (sv == -INFINITY) ? 0.0f : exp2f(sv - m[g]);
+              l[g] += pv;
+              wv[j][g] = pv > 0.0f ? pv * vsc[j] : 0.0f;  // masked: the scale never enters
+            }
+          }
+          uint8_t* s_w8 = reinterpret_cast<uint8_t*>(s_pq[w]);  // rows 4 g + limb, NK bytes
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float wm = 0.0f, z = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              wm = fmaxf(wm, wv[j][g]);
+              z += wv[j][g] * 0.0f;
+            }
+            wm = wave_max(wm);
+            z = wave_sum(z);
+            const float inv = wm >= 0x1p-120f ? 127.0f / wm : 0.0f;
+            pmul = kq == g ? wm * (1.0f / 127.0f) + z : pmul;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+              const int x = lane + 64 * j;
+              if (x < NK) {
+                const float a = wv[j][g] * inv;  // 0 <= a <= 127
+                const float b0 = rintf(a);
+                const float r1 = (a - b0) * 254.0f;
+                const float b1 = rintf(r1);
+                const float b2 = rintf((r1 - b1) * 254.0f);
+                s_w8[(4 * g + 0) * NK + x] = (uint8_t)(int32_t)b0;
+                s_w8[(4 * g + 1) * NK + x] = (uint8_t)(int32_t)b1;
+                s_w8[(4 * g + 2) * NK + x] = (uint8_t)(int32_t)b2;
+              }
+            }
+          }
+        } else {
 #pragma unroll
         for (int j = 0; j < (NTW * BS + 63) / 64; ++j) {
           const int x = lane + 64 * j;
@@ -557,6 +684,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
                 s_p[x * G + g] = pv;
             }
           }
+        }
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -619,6 +747,30 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before the
         __builtin_amdgcn_wave_barrier();                         // next tile overwrites
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      } else if constexpr ((i & 1) && I8PV) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the pair's rows ...
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads below
+        // A = weight limbs: lane (kq, kt) holds row kt (head kt / 4, limb
+        // kt % 4; limb 3 and heads >= G are zero rows), keys 8 kq .. + 7 of
+        // the pair
+        const uint8_t* s_w8 = reinterpret_cast<const uint8_t*>(s_pq[w]);
+        const bool arow = kt < 4 * G && (kt & 3) < 3;
+        const uint2 wa = *reinterpret_cast<const uint2*>(
+            s_w8 + (arow ? kt : 0) * NK + (i - 1) * BS + 8 * kq);
+        const long pa = arow ? __builtin_bit_cast(long, wa) : 0l;
+        // B = V: lane (kq, kt) holds keys 8 kq .. + 7 of dim 16 c + kt (the
+        // transposing read of the bf16 path's A operand)
+        const uint8_t* va = vb + (8 * kq + (kt >> 1)) * VROW + 8 * (kt & 1);
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const uint2 raw = lds_read_tr8(va + 16 * c);
+          iov[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(pa, __builtin_bit_cast(long, raw),
+                                                         iov[c], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // reads done before the
+        __builtin_amdgcn_wave_barrier();                         // next pair overwrites
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       } else if constexpr (i & 1) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the pair's rows ...
@@ -691,8 +843,15 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 
   // MFMA PV: lane (kq, kt) holds O^T[dim 16 c + 4 kq + r][column kt]; head
   // g's sum is column g (hi) plus column G + g (lo): lanes kt < G take it.
-  f32x4_t hv[MPV ? D / 16 : 1];
-  if constexpr (MPV) {
+  // I8PV: lane (kq, kt) holds head kq's sums for dims 16 c + kt.
+  f32x4_t hv[MPV && !I8PV ? D / 16 : 1];
+  float iv[I8PV ? D / 16 : 1];
+  if constexpr (I8PV) {
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      iv[c] = ((float)iov[c][0] + (float)iov[c][1] * (1.0f / 254.0f) +
+               (float)iov[c][2] * (1.0f / 64516.0f)) * pmul;
+  } else if constexpr (MPV) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
@@ -706,7 +865,31 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[g][e] += __shfl_xor(acc[g][e], o);
   }
-  if constexpr (SPLIT == 1 && MPV) {
+  if constexpr (SPLIT == 1 && I8PV) {
+    if (kq < G) {
+      float mg = m[0], lg = l[0];  // head kq's state
+#pragma unroll
+      for (int x = 1; x < G; ++x) {
+        mg = kq == x ? m[x] : mg;
+        lg = kq == x ? l[x] : lg;
+      }
+      float* dst;
+      float scl = 1.0f;
+      if (nparts == 1) {
+        dst = out + (head0 + kq) * D;
+        scl = lg > 0.0f ? 1.0f / lg : 0.0f;
+      } else {
+        const int64_t row = (head0 + kq) * max_parts + part;
+        dst = part_acc + row * D;
+        if (kt == 0) {
+          part_ml[row * 2 + 0] = mg;
+          part_ml[row * 2 + 1] = lg;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) dst[16 * c + kt] = iv[c] * scl;
+    }
+  } else if constexpr (SPLIT == 1 && MPV) {
     if (kt < G) {
       float mg = m[0], lg = l[0];  // head kt's state (selects: kt is not constant)
 #pragma unroll
@@ -762,7 +945,19 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     // m = -inf and weight 0).
     __shared__ float s_cm[SPLIT][G], s_cl[SPLIT][G];
     float(*s_cacc)[SPW] = s_pw;
-    if constexpr (MPV) {
+    if constexpr (I8PV) {
+      if (kq < G) {
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) s_cacc[sub][kq * D + 16 * c + kt] = iv[c];
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          s_cm[sub][g] = m[g];
+          s_cl[sub][g] = l[g];
+        }
+      }
+    } else if constexpr (MPV) {
       if (kt < G) {
 #pragma unroll
         for (int c = 0; c < D / 16; ++c)

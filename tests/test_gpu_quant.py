@@ -142,6 +142,43 @@ def test_decode_q_config2_shape_and_partial_blocks(dev, fmt):
     assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle")
 
 
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 4), (4, 4)])
+def test_decode_q_int8_wide_dynamic_range(dev, hq, hkv):
+    """int8 pools with K rows scaled by 10^U(-1.5, 1.5) and V rows by
+    10^U(-2, 2) per (token, head), q heads by 10^U(-1.5, 1), one q head all
+    zeros and one a single spike over 1e-3 values.  For G <= 4 the kernel
+    runs QK^T and PV on the integer matrix cores with q and the PV weights in
+    three int8 limbs, fixed point against each head's maximum: these inputs
+    put the small terms many decades under that maximum, where a dropped or
+    mis-scaled limb would show.  (G = 8 runs the bf16 path, q as bf16 hi +
+    lo; the other cases cover it.)"""
+    say(f"decode_q int8 wide range hq={hq} hkv={hkv}")
+    rng = np.random.default_rng(5 + hq)
+    ctx = np.array([1, 17, 300, 640, 641, 1500, 2600], np.int32)
+    bs, d = 16, 128
+    nb = int(sum((c + bs - 1) // bs for c in ctx)) + 4
+    n = nb * bs
+    kn = rng.standard_normal((n, hkv, d)) * 10 ** rng.uniform(-1.5, 1.5, (n, hkv, 1))
+    vn = rng.standard_normal((n, hkv, d)) * 10 ** rng.uniform(-2, 2, (n, hkv, 1))
+    kp = np.zeros((nb, hkv, bs, d), np.uint8)
+    vp = np.zeros_like(kp)
+    ks = np.zeros((nb, hkv, bs), np.float32)
+    vs = np.zeros_like(ks)
+    oracle.append_q(kp, vp, ks, vs, kn.astype(np.float32), vn.astype(np.float32),
+                    np.arange(n, dtype=np.int64), oracle.I8)
+    tables = make_tables(rng, ctx, bs, nb)
+    q = rng.standard_normal((len(ctx), hq, d)) * 10 ** rng.uniform(-1.5, 1, (len(ctx), hq, 1))
+    q = q.astype(np.float32)
+    q[0, 0] = 0.0
+    q[1, 1] = 1e-3
+    q[1, 1, 5] = 50.0
+    scale = float(np.float32(1 / math.sqrt(d)))
+    got = run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, "int8")
+    want = oracle.decode_attention(q, oracle.dequantize_pool(kp, ks, oracle.I8),
+                                   oracle.dequantize_pool(vp, vs, oracle.I8), tables, ctx, scale)
+    assert_allclose_ref(got, want, RTOL, ATOL, "int8 wide range vs oracle")
+
+
 def test_decode_q_quantization_error_is_small(dev):
     """Against fp32 attention on the unquantized values: the int8 / fp8
     storage error stays within a few 1e-2 (max-abs) on N(0,1) data."""
