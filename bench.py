@@ -104,6 +104,23 @@ def copy_bandwidth(torch, dev, nbytes=2 << 30, reps=10):
     return 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
 
 
+def read_bandwidth(torch, dev, nbytes=2 << 30, reps=10):
+    """Flat nontemporal read GB/s of rustral_amd/ceiling's stream kernel: the
+    achievable rate for a read-only kernel such as the decode (None if that
+    measurement library is not built)."""
+    try:
+        from rustral_amd import ceiling as C
+        C.lib()
+    except (ImportError, OSError):
+        return None
+    a = torch.full((nbytes // 4,), 1, dtype=torch.int32, device=dev)
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    C.read(torch, a, sink)
+    ms = _timed(torch, lambda: C.read(torch, a, sink), reps)
+    del a
+    return nbytes / (ms * 1e-3) / 1e9
+
+
 def cpu_baseline(torch, layers, ctx, threads):
     """The C oracle (a restatement of the reference's CPU semantics) on a
     bounded sample: layer 0 of the workload, all 64 sequences, timed with
@@ -1061,6 +1078,7 @@ def main():
 
     traffic = traffic_from_profiles()
     copy_gbps = copy_bandwidth(torch, dev)
+    read_gbps = read_bandwidth(torch, dev)
     cpu = None
     if not args.no_cpu_baseline:
         # 16 threads: the host share of one GPU on the box (nproc there counts
@@ -1102,6 +1120,8 @@ def main():
         "merge_kernel_us": round(avg_merge_us, 2),
         "algorithmic_bytes_per_call": bytes_call,
         "measured_copy_GBps": round(copy_gbps, 1),
+        "measured_read_GBps": None if read_gbps is None else round(read_gbps, 1),
+        "value_over_measured_read": None if read_gbps is None else round(value / read_gbps, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "kernel": "decode_stream_kernel<bf16, D=128, G=4> (640-token partitions, 4 waves each, K/V tiles staged in LDS, MFMA QK^T and PV)",
