@@ -135,11 +135,12 @@ def cpu_baseline(torch, layers, ctx, threads):
     th = tables.cpu().numpy()
     scale = 1.0 / math.sqrt(D)
     oracle.decode_attention(qh[:1], kh, vh, th[:1], ctx[:1], scale)  # load + warm
-    reps, t_mt = 0, 0.0
+    reps, t_mt, calls = 0, 0.0, []
     while t_mt < 10.0 and reps < 500:  # about 10 s of CPU work
         t0 = time.perf_counter()
         oracle.decode_attention(qh, kh, vh, th, ctx, scale, n_threads=threads)
-        t_mt += time.perf_counter() - t0
+        calls.append(time.perf_counter() - t0)
+        t_mt += calls[-1]
         reps += 1
     t0 = time.perf_counter()
     oracle.decode_attention(qh[:4], kh, vh, th[:4], ctx[:4], scale)
@@ -153,6 +154,7 @@ def cpu_baseline(torch, layers, ctx, threads):
                    f"single thread on 4 seqs: {st_gbps:.3f} GB/s"),
         "single_thread_GBps": round(st_gbps, 4),
         "tokens_per_s_32_layers": round(B * reps / (t_mt * 32), 3),
+        "call_ms_stats": stats([1e3 * t for t in calls]),
     }
 
 
