@@ -25,7 +25,7 @@
 //     of a partition combine their states through LDS.
 //   * int8 pools (G <= 4) keep both products on the integer matrix cores:
 //     q and the PV weights are split into three int8 limbs (fixed point
-//     against the head's maximum, ~24 bits), the stored bytes enter
+//     against the head's maximum, ~22 bits), the stored bytes enter
 //     v_mfma_i32_16x16x64_i8 / _16x16x32_i8 unconverted and the int32 sums
 //     are exact; fp8 pools convert their bytes to bf16 (exact).
 // Pass 2 (decode_merge_kernel): per (query head, sequence) merge of the
@@ -283,7 +283,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // int8 pools (G <= 4): QK^T on the integer matrix cores, exact in int32.
   // q of head h is written as (M_h / 127) (a0 + a1 / 254 + a2 / 254^2) with
   // M_h = max |q| over the head's dims and int8 limbs a0, a1, a2 (round to
-  // nearest at each step: |q - that sum| <= M_h 2^-23.9), the limbs are rows
+  // nearest at each step; with the fp32 roundings of q * 127 / M_h and of
+  // the residuals, |q - that sum| < M_h 2^-22), the limbs are rows
   // 4 h + j of A, and B is the stored K bytes as they are.  Row 4 h + j of
   // the result lands in lane 16 h + token, register j: each lane combines
   // the three limb dots of one (head, token) pair in its own registers.  No
