@@ -309,7 +309,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   i32x4_t iov[I8PV ? D / 16 : 1];  // I8PV: lane (kq, kt) rows 4 kq + r, dim 16 c + kt
 #pragma unroll
   for (int c = 0; c < (I8PV ? D / 16 : 1); ++c) iov[c] = i32x4_t{0, 0, 0, 0};
-  float pmul = 0.0f;  // I8PV: W_h / 127 of head kq (NaN when a weight is NaN or inf)
+  float pmul = 0.0f;  // I8PV: W_h / 127 of head kq (inf when a weight is NaN or inf)
   constexpr int NC = D / 32;                     // MFMAs per tile
   const int kt = lane & 15, kq = lane >> 4;      // MFMA lanes: token row, k-quarter
   // VALU path: this lane's E dims of each head.  MFMA path: the A operand
@@ -318,10 +318,20 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // [D/4 kq, D/4 (kq+1)) of its key row, so chunk c holds dims D/4 kq + 8c ..
   // + 8 (any assignment of dims to k-slots gives the same dot product, as long
   // as q and K use the same one).
-  constexpr int QN = MFMA ? NC * 8 : G * E;
+  // I8QK: lane l loads dims (D/16) (l % 16) .. + D/16 of head l / 16 (the
+  // limbs are built once per (head, dim) and exchanged through LDS).
+  constexpr int QN = I8QK ? D / 16 : (MFMA ? NC * 8 : G * E);
   float qv[QN];
-  if constexpr (MFMA) {
-    const int qrow = I8QK ? (kt / 4 < G ? kt / 4 : 0) : (kt < G ? kt : (kt < 2 * G ? kt - G : 0));
+  if constexpr (I8QK) {
+    const int hq = (lane >> 4) < G ? (lane >> 4) : 0;
+#pragma unroll
+    for (int e = 0; e < QN; e += 4) {
+      const float4 x =
+          *reinterpret_cast<const float4*>(q + (head0 + hq) * D + (lane & 15) * QN + e);
+      qv[e + 0] = x.x; qv[e + 1] = x.y; qv[e + 2] = x.z; qv[e + 3] = x.w;
+    }
+  } else if constexpr (MFMA) {
+    const int qrow = kt < G ? kt : (kt < 2 * G ? kt - G : 0);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d0 = QNT ? (D / 4) * kq + 8 * c : 32 * c + 8 * kq;
@@ -380,6 +390,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   constexpr int KROW = D * sizeof(T) + 16;  // staged K row (bytes): the 16 rows
                                             // of one operand read hit distinct banks
   static_assert(!KLDS || BS * KROW <= VT * BS * VROW, "K staging fits the V staging buffer");
+  static_assert(!I8QK || BS * KROW + 16 * D <= VT * BS * VROW,
+                "K staging and the q limb rows fit the V staging buffer");
   constexpr bool kmfma = MFMA && !KLDS;
   const uint32_t koff = (kmfma ? kt * D + (QNT ? (D / 4) * kq : 8 * kq) : slot * D + dl * E) * sizeof(T);
   const uint32_t voff = (slot * D + dl * E) * sizeof(T);
@@ -428,43 +440,54 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // MFMA A operands: q split into bf16 hi + lo rows, two values per
   // v_cvt_pk_bf16_f32 (round to nearest even, no branch)
   uint4 qa[MFMA ? NC : 1];
-  float qmul = 0.0f;  // I8QK: M_h / 127 of head kq (NaN when q_h holds NaN or inf)
+  float qmul = 0.0f;  // I8QK: M_h / 127 of head kq (inf when q_h holds NaN or inf)
   if constexpr (I8QK) {
-    // M_h over the four lanes kt, kt + 16, kt + 32, kt + 48 (one head, a
-    // quarter of its dims each); z = 0, or NaN for a NaN / infinite q value
-    float amax = 0.0f, z = 0.0f;
+    // M_h over the 16 lanes of head l / 16 (a NaN counts as inf: the limbs
+    // are then zero and the head's dots 0 * inf = NaN, as in the float path)
+    float amax = 0.0f;
 #pragma unroll
-    for (int e = 0; e < QN; ++e) {
-      amax = fmaxf(amax, fabsf(qv[e]));
-      z += qv[e] * 0.0f;
-    }
-    amax = pair32_max(pair16_max(amax));
-    z = pair32_sum(pair16_sum(z));
+    for (int e = 0; e < QN; ++e) amax = fmaxf(amax, qv[e] != qv[e] ? INFINITY : fabsf(qv[e]));
+    amax = group_max<16>(amax);
     const float inv = amax >= 0x1p-120f ? 127.0f / amax : 0.0f;  // finite
-    const int limb = kt & 3;
-    const bool live = kt / 4 < G && limb < 3;
+    // limb rows 4 h + j of D bytes each, after the K staging rows
+    uint8_t* qbuf = s_vq[w] + BS * KROW;
+    uint32_t lw[3][QN / 4];
+#pragma unroll
+    for (int e4 = 0; e4 < QN / 4; ++e4) {
+      lw[0][e4] = lw[1][e4] = lw[2][e4] = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = qv[4 * e4 + e] * inv;  // |a| <= 127
+        const float a0 = rintf(a);
+        const float r1 = (a - a0) * 254.0f;  // |r1| <= 127
+        const float a1 = rintf(r1);
+        const float a2 = rintf((r1 - a1) * 254.0f);
+        lw[0][e4] |= ((uint32_t)(int32_t)a0 & 0xffu) << (8 * e);
+        lw[1][e4] |= ((uint32_t)(int32_t)a1 & 0xffu) << (8 * e);
+        lw[2][e4] |= ((uint32_t)(int32_t)a2 & 0xffu) << (8 * e);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      uint8_t* dst = qbuf + (4 * (lane >> 4) + j) * D + (lane & 15) * QN;
+      if constexpr (QN == 8)
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lw[j][0], lw[j][1]);
+      else
+        *reinterpret_cast<uint32_t*>(dst) = lw[j][0];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the limb rows ...
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads
+    // A row kt: head kt / 4, limb kt % 4 (limb 3 and heads >= G are zero)
+    const bool live = kt / 4 < G && (kt & 3) < 3;
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
-      uint32_t h[4];
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = qv[16 * n + 4 * e4 + e] * inv;  // |a| <= 127
-          const float a0 = rintf(a);
-          const float r1 = (a - a0) * 254.0f;  // |r1| <= 127
-          const float a1 = rintf(r1);
-          const float a2 = rintf((r1 - a1) * 254.0f);
-          const float v = limb == 0 ? a0 : (limb == 1 ? a1 : a2);
-          word |= ((uint32_t)(int32_t)v & 0xffu) << (8 * e);
-        }
-        h[e4] = live ? word : 0u;
-      }
-      qa[n] = make_uint4(h[0], h[1], h[2], h[3]);
+      const uint4 v = *reinterpret_cast<const uint4*>(
+          qbuf + (live ? kt : 0) * D + (D / 4) * kq + 16 * n);
+      qa[n] = live ? v : make_uint4(0u, 0u, 0u, 0u);
     }
-    // this lane's result rows belong to head kq: its M_h sits in lane 4 kq
-    qmul = __shfl(amax * (1.0f / 127.0f) + z, 4 * kq);
+    // this lane's result rows belong to head kq, whose M_h this lane holds
+    qmul = amax * (1.0f / 127.0f);
   } else if constexpr (MFMA) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -638,16 +661,14 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
           uint8_t* s_w8 = reinterpret_cast<uint8_t*>(s_pq[w]);  // rows 4 g + limb, NK bytes
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            float wm = 0.0f, z = 0.0f;
+            // a NaN weight counts as inf: the limbs are then zero and the
+            // head's sums 0 * inf = NaN, as in the float path
+            float wm = 0.0f;
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-              wm = fmaxf(wm, wv[j][g]);
-              z += wv[j][g] * 0.0f;
-            }
+            for (int j = 0; j < NJ; ++j) wm = fmaxf(wm, wv[j][g] != wv[j][g] ? INFINITY : wv[j][g]);
             wm = wave_max(wm);
-            z = wave_sum(z);
             const float inv = wm >= 0x1p-120f ? 127.0f / wm : 0.0f;
-            pmul = kq == g ? wm * (1.0f / 127.0f) + z : pmul;
+            pmul = kq == g ? wm * (1.0f / 127.0f) : pmul;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
               const int x = lane + 64 * j;
