@@ -179,6 +179,38 @@ def test_decode_q_int8_wide_dynamic_range(dev, hq, hkv):
     assert_allclose_ref(got, want, RTOL, ATOL, "int8 wide range vs oracle")
 
 
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_decode_q_invalid_blocks_empty_sequences_and_clamp(dev, fmt):
+    """1-byte pools over 70 sequences (more than one 64-length scan of the
+    work plan): block ids of -1 and past the pool leave their tokens out,
+    empty sequences give zero rows, a context past its table is clamped to
+    the table, and a second call gives the same bits."""
+    say(f"decode_q invalid ids / empty / clamp fmt={fmt}")
+    rng = np.random.default_rng(11)
+    hkv, bs, d, hq, mb = 8, 16, 128, 32, 96
+    ctx = rng.integers(0, 1500, size=70).astype(np.int32)
+    ctx[::9] = 0
+    ctx[4] = 1
+    ctx[1] = 5000                                   # > mb * bs: clamped to 1536
+    eff = np.minimum(ctx, mb * bs)
+    nb = int(sum((c + bs - 1) // bs for c in eff)) + 8
+    kp, vp, ks, vs = quant_case(12, nb, hkv, bs, d, fmt)
+    tables = make_tables(rng, eff, bs, nb, max_blocks=mb)
+    seq = int(np.argmax(eff >= 6 * bs))
+    tables[seq, 3] = -1
+    tables[seq, 5] = 10 ** 6
+    q = rng.standard_normal((len(ctx), hq, d)).astype(np.float32)
+    scale = float(np.float32(1 / math.sqrt(d)))
+    got = run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, fmt)
+    want = oracle.decode_attention(q, oracle.dequantize_pool(kp, ks, CODE[fmt]),
+                                   oracle.dequantize_pool(vp, vs, CODE[fmt]), tables, ctx, scale,
+                                   n_threads=8)
+    assert_allclose_ref(got, want, RTOL, ATOL, "1-byte invalid ids / clamp vs oracle")
+    assert not got[ctx == 0].any()
+    again = run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, fmt)
+    assert np.array_equal(got, again)
+
+
 def test_decode_q_quantization_error_is_small(dev):
     """Against fp32 attention on the unquantized values: the int8 / fp8
     storage error stays within a few 1e-2 (max-abs) on N(0,1) data."""
