@@ -81,7 +81,7 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ q_start,
     const int32_t* __restrict__ ctx_lens, int num_kv_heads, int64_t num_blocks, int max_q_len,
-    float q_scale) {
+    float q_scale, int heavy_first) {
   constexpr bool F32 = sizeof(T) == 4;
   static_assert(G % HW == 0, "heads per wave must divide the group");
   constexpr int NT = 64 * (G / HW) * QS;
@@ -101,7 +101,14 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
 
   const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
   const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
-  const int qt = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+  // Grid order.  heavy_first: x = KV head + num_kv_heads * sequence, y = the
+  // query tiles from the last (the most keys) down, so the longest tiles are
+  // dispatched first and the tiles of one (KV head, sequence) share an XCD's
+  // L2 when num_kv_heads * num_seqs is a multiple of 8 (workgroups go to the
+  // XCDs round robin).  Otherwise x = query tile, y = KV head, z = sequence.
+  const int qt = heavy_first ? (int)(gridDim.y - 1 - blockIdx.y) : (int)blockIdx.x;
+  const int kh = heavy_first ? (int)(blockIdx.x % num_kv_heads) : (int)blockIdx.y;
+  const int b = heavy_first ? (int)(blockIdx.x / num_kv_heads) : (int)blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = w % (G / HW), rt = w / (G / HW);  // head set within the group, row sub-tile
@@ -511,7 +518,7 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
 }
 
 using PrefillFn = void (*)(float*, const float*, const void*, const void*, const int32_t*, int,
-                           const int32_t*, const int32_t*, int, int64_t, int, float);
+                           const int32_t*, const int32_t*, int, int64_t, int, float, int);
 
 // Waves per workgroup, query heads per wave (for groups of at least 4 heads)
 // and key blocks per staged iteration.  With 8 waves a workgroup may hold up
@@ -524,6 +531,11 @@ using PrefillFn = void (*)(float*, const float*, const void*, const void*, const
 #endif
 #ifndef RKV_PREFILL_KB
 #define RKV_PREFILL_KB 2
+#endif
+// Heaviest query tiles first (1) or the query tile as the fastest grid
+// dimension (0).
+#ifndef RKV_PREFILL_HEAVY_FIRST
+#define RKV_PREFILL_HEAVY_FIRST 1
 #endif
 constexpr int kWaves = RKV_PREFILL_WAVES;
 constexpr int kHW = RKV_PREFILL_HW;
@@ -604,10 +616,13 @@ extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_p
   if (!aligned16(out) || !aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG,
                 "rkv_prefill_attention: out, q and pools must be 16-byte aligned");
-  const dim3 grid((unsigned)((max_q_len + cfg.tile - 1) / cfg.tile), (unsigned)num_kv_heads,
-                  (unsigned)num_seqs);
+  const int64_t n_tiles = (max_q_len + cfg.tile - 1) / cfg.tile;
+  const int64_t n_heads = (int64_t)num_seqs * num_kv_heads;
+  const int heavy = RKV_PREFILL_HEAVY_FIRST && n_tiles <= 65535 && n_heads <= 0x7fffffff;
+  const dim3 grid = heavy ? dim3((unsigned)n_heads, (unsigned)n_tiles, 1)
+                          : dim3((unsigned)n_tiles, (unsigned)num_kv_heads, (unsigned)num_seqs);
   hipLaunchKernelGGL(cfg.fn, grid, dim3(64 * cfg.waves), 0, static_cast<hipStream_t>(stream), out, q, k_pool,
                      v_pool, block_tables, max_blocks_per_seq, q_start, ctx_lens, num_kv_heads,
-                     num_blocks, max_q_len, scale * kLog2e);
+                     num_blocks, max_q_len, scale * kLog2e, heavy);
   return check_launch("rkv_prefill_attention");
 }
