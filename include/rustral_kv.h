@@ -116,9 +116,9 @@ size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, i
 /* Partition size (tokens) rkv_decode_attention uses for pools of dtype and
  * this max_context, for a request of partition_size: the request itself when
  * it is a multiple of 64 tokens (16 tokens x 4 waves) up to 640; for
- * partition_size <= 0 the default -- 640, and 512 for fp32 / bf16 pools when
- * max_context exceeds 8192 (long contexts run ~3% faster with 512-token
- * partitions).  RKV_ERR_UNSUPPORTED for other requests. */
+ * partition_size <= 0 the default, 640 at every max_context (measured
+ * faster than 512 for contexts from U[1, 8192] to U[16384, 65536]).
+ * RKV_ERR_UNSUPPORTED for other requests. */
 int rkv_decode_partition_size(int partition_size, int head_dim, int dtype, int max_context);
 
 /* Single-token paged decode attention with GQA (two passes: partitions of

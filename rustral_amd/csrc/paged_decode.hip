@@ -1282,21 +1282,17 @@ constexpr int split_of() { return sizeof(T) == 1 ? RKV_DECODE_SPLIT_Q : RKV_DECO
 // 16 * SPLIT up to the build's largest (640); its waves stream
 // tw = P / (16 * SPLIT) tiles each.  The kernels are built for two slice
 // lengths: the largest, and for 16-bit and fp32 pools also 512 tokens, so
-// that long-context calls run 512-token partitions without masked slots (at
-// configs[3] 512-token partitions measured ~3% faster than 640); other sizes
-// run on the smallest build that holds them, the extra slots masked.
-// Default: 640, and 512 for 16-bit / fp32 pools once max_context exceeds
-// kLongContext.
+// that a caller asking for 512-token partitions runs them without masked
+// slots; other sizes run on the smallest build that holds them, the extra
+// slots masked.  Default: the largest (640 tokens) at every context length
+// -- bf16 pools measured 640 faster than 512 by 0.4-2% from contexts
+// U[1, 8192] at 256 sequences to U[16384, 65536] at 8.
 constexpr int kSmallP = 512;
-constexpr int kLongContext = 8192;
 static_assert(kSmallP <= kP && kSmallP % (16 * RKV_DECODE_SPLIT) == 0, "small partition build");
 
 inline bool one_byte(int dtype) { return dtype == RKV_I8 || dtype == RKV_FP8; }
 
-int default_part(int dtype, int max_context) {
-  if (one_byte(dtype)) return kPQ;
-  return max_context > kLongContext ? kSmallP : kP;
-}
+int default_part(int dtype, int /*max_context*/) { return one_byte(dtype) ? kPQ : kP; }
 
 // The partition size a call uses: the request when it is > 0 (a multiple of
 // 16 * SPLIT, at most the largest build), else the default; a negative

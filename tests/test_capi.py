@@ -82,10 +82,10 @@ def test_workspace_size():
             Pd = L.rkv_decode_partition_size(0, 128, dt, maxc)
             assert Pd > 0 and Pd % 64 == 0
             assert ws >= L.rkv_decode_workspace_bytes(8, 32, 128, maxc, Pd)
-    # long contexts default to 512-token partitions for 16-bit / fp32 pools
-    assert L.rkv_decode_partition_size(0, 128, RKV_BF16, 65536) == 512
-    assert L.rkv_decode_partition_size(0, 128, RKV_F32, 65536) == 512
-    assert L.rkv_decode_partition_size(0, 128, RKV_I8, 65536) == 640
+    # the default is 640-token partitions at every context length
+    for dt in (RKV_F32, RKV_BF16, RKV_I8, RKV_FP8):
+        for maxc in (16, 4096, 65536):
+            assert L.rkv_decode_partition_size(0, 128, dt, maxc) == 640
     # a request is honoured when it is a multiple of 64 up to 640
     for req in (64, 128, 320, 512, 576, 640):
         assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == req
