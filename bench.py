@@ -557,7 +557,10 @@ def run_decode_q(torch, dev, args):
     scale per (token, KV head) row, filled by the quantizing append from
     N(0, 1) rows.  A step (32 calls) is replayed from a HIP graph as in the
     headline line.  Bytes per call: the bytes and scales of K and V once, q
-    in, out, block ids, lengths."""
+    in, out, block ids, lengths.  Beside it, per format: the dequantizing
+    gather of a layer into the packed fp32 KVCache layout (bytes and scales
+    read, fp32 written) and the quantizing append of 1,024 tokens into 32
+    layers in one launch (fp32 rows read, bytes and scales written)."""
     import numpy as np
     from rustral_amd import kv
     rng = np.random.default_rng(SEED)
@@ -614,7 +617,47 @@ def run_decode_q(torch, dev, args):
         res[fmt] = {"us_per_call": round(us, 2), "bytes_per_call": nbytes,
                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                     "decode_tokens_per_s_b64": round(B / (ms * 1e-3), 1)}
-        del layers, ws
+        # dequantizing gather into the packed KVCache layout, one layer per
+        # call, rotating over the 32 layer pools
+        n_tok = int(ctx.astype(np.int64).sum())
+        offs = torch.from_numpy(np.concatenate(
+            [[0], np.cumsum(ctx.astype(np.int64) * HKV * D)[:-1]])).to(dev)
+        total = n_tok * HKV * D
+        ko = torch.empty(total, dtype=torch.float32, device=dev)
+        vo = torch.empty_like(ko)
+        li = iter(range(10 ** 9))
+
+        def gat():
+            _, kp, vp, ks, vs, t, _ = layers[next(li) % len(layers)]
+            kv.gather_q(kp, vp, ks, vs, t, ctx_d, fmt, out_offsets=offs, out_total=total,
+                        k_out=ko, v_out=vo)
+        gat()
+        ms_g = _timed(torch, gat, len(layers))
+        g_bytes = n_tok * HKV * 2 * ((D + 4) + 4 * D) + int(need.sum()) * 4 + B * 4
+        res[fmt]["gather_packed"] = {"us_per_call": round(1e3 * ms_g, 2), "bytes_per_call": g_bytes,
+                                     "GBps": round(g_bytes / (ms_g * 1e-3) / 1e9, 1)}
+        del layers, ws, ko, vo
+        torch.cuda.empty_cache()
+        # quantizing append: 16 decode steps' tokens (1,024) into all 32
+        # layers of a 4,096-block pool set in one launch, distinct random slots
+        nl, nba, n_app = 32, 4096, 16 * B
+        akp = torch.empty((nl, nba, HKV, BS, D), dtype=torch.uint8, device=dev)
+        avp = torch.empty_like(akp)
+        aks = torch.empty((nl, nba, HKV, BS), dtype=torch.float32, device=dev)
+        avs = torch.empty_like(aks)
+        akn = torch.randn((nl, n_app, HKV, D), generator=g, device=dev)
+        avn = torch.randn_like(akn)
+        aslots = torch.randperm(nba * BS, generator=g, device=dev)[:n_app].contiguous()
+
+        def app():
+            kv.append_q(akp, avp, aks, avs, akn, avn, aslots, fmt)
+        app()
+        ms_a = _timed(torch, app, max(args.steps, 5))
+        a_bytes = nl * n_app * HKV * 2 * (4 * D + D + 4) + n_app * 8
+        res[fmt]["append_bulk_16_steps"] = {"us_per_launch": round(1e3 * ms_a, 2),
+                                            "bytes_per_launch": a_bytes,
+                                            "GBps": round(a_bytes / (ms_a * 1e-3) / 1e9, 1)}
+        del akp, avp, aks, avs, akn, avn
         torch.cuda.empty_cache()
     r = res["int8"]
     return _line("paged-KV decode over int8 pools GB/s (configs[2] shape); tokens/s at batch 64",

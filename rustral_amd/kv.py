@@ -217,17 +217,39 @@ def append_q(k_pool: torch.Tensor, v_pool: torch.Tensor, k_scale: torch.Tensor,
 
 def gather_q(k_pool: torch.Tensor, v_pool: torch.Tensor, k_scale: torch.Tensor,
              v_scale: torch.Tensor, block_tables: torch.Tensor, ctx_lens: torch.Tensor,
-             fmt: str = "int8", *, max_ctx: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """Dequantized K/V per sequence, padded fp32 [B, Hkv, max_ctx, D]."""
+             fmt: str = "int8", *, max_ctx: int | None = None,
+             out_offsets: torch.Tensor | None = None, out_total: int | None = None,
+             k_out=None, v_out=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dequantized K/V per sequence in fp32: padded [B, Hkv, max_ctx, D], or
+    packed (out_offsets int64 [B] given) as flat tensors of out_total
+    elements.  Untouched rows keep the contents of k_out/v_out (zeros when
+    allocated here)."""
+    _dev(k_pool, "k_pool", torch.uint8), _dev(v_pool, "v_pool", torch.uint8)
+    _dev(k_scale, "k_scale", torch.float32), _dev(v_scale, "v_scale", torch.float32)
+    _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
     nb, hkv, bs, d = k_pool.shape
     B, mbs = block_tables.shape
-    if max_ctx is None:
-        max_ctx = mbs * bs
-    k_out = torch.zeros((B, hkv, max_ctx, d), dtype=torch.float32, device=k_pool.device)
-    v_out = torch.zeros_like(k_out)
+    if out_offsets is None:
+        if max_ctx is None:
+            max_ctx = mbs * bs
+        shape = (B, hkv, max_ctx, d)
+        off_ptr = None
+    else:
+        _dev(out_offsets, "out_offsets", torch.int64)
+        if out_total is None:
+            raise ValueError("packed gather needs out_total")
+        shape = (out_total,)
+        off_ptr = out_offsets.data_ptr()
+        max_ctx = 0
+    if k_out is None:
+        k_out = torch.zeros(shape, dtype=torch.float32, device=k_pool.device)
+        v_out = torch.zeros(shape, dtype=torch.float32, device=k_pool.device)
+    _dev(k_out, "k_out", torch.float32), _dev(v_out, "v_out", torch.float32)
+    if k_out.numel() < math.prod(shape) or v_out.numel() < math.prod(shape):
+        raise ValueError("gather_q output smaller than the layout needs")
     check(lib().rkv_gather_q(k_out.data_ptr(), v_out.data_ptr(), k_pool.data_ptr(),
                              v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
-                             block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), None, B, hkv, d,
+                             block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), off_ptr, B, hkv, d,
                              bs, nb, max_ctx, _qcode(fmt), _stream(k_pool)))
     return k_out, v_out
 

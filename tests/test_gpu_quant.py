@@ -90,6 +90,39 @@ def test_gather_q_dequantizes_bitexact(dev, fmt):
     assert np.array_equal(to_np(k_out), wk) and np.array_equal(to_np(v_out), wv)
 
 
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_gather_q_packed_layout_bitexact(dev, fmt):
+    """The packed KVCache layout (sequence b's [Hkv, L_b, D] at its offset):
+    dequantized values equal the oracle's gather of the dequantized pool, and
+    the guard rows between sequences and after the last stay untouched."""
+    say(f"gather_q packed fmt={fmt}")
+    rng = np.random.default_rng(23)
+    nb, hkv, bs, d = 96, 4, 16, 64
+    ctx = np.array([5, 0, 16, 33, 250, 1], np.int32)
+    kp, vp, ks, vs = quant_case(23, nb, hkv, bs, d, fmt)
+    tables = make_tables(rng, ctx, bs, nb)
+    gap = hkv * d  # one row of guard elements after every sequence
+    sizes = ctx.astype(np.int64) * hkv * d + gap
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    total = int(sizes.sum())
+    guard = np.float32(-7.25)
+    k_out = torch.full((total,), float(guard), dtype=torch.float32, device=dev)
+    v_out = torch.full((total,), float(guard), dtype=torch.float32, device=dev)
+    kv.gather_q(to_dev(kp, dev), to_dev(vp, dev), to_dev(ks, dev), to_dev(vs, dev),
+                to_dev(tables, dev), to_dev(ctx, dev), fmt, out_offsets=to_dev(offs, dev),
+                out_total=total, k_out=k_out, v_out=v_out)
+    torch.cuda.synchronize()
+    kf = oracle.dequantize_pool(kp, ks, CODE[fmt])
+    vf = oracle.dequantize_pool(vp, vs, CODE[fmt])
+    wk = np.full(total, guard, np.float32)
+    wv = np.full(total, guard, np.float32)
+    oracle.gather(kf, vf, tables, ctx, out_offsets=offs, out_f32=True, k_out=wk, v_out=wv)
+    assert np.array_equal(to_np(k_out), wk) and np.array_equal(to_np(v_out), wv)
+    for b in range(len(ctx)):   # the guard rows themselves
+        g0 = int(offs[b] + ctx[b] * hkv * d)
+        assert (wk[g0:g0 + gap] == guard).all()
+
+
 def run_q(dev, q, kp, vp, ks, vs, tables, ctx, scale, fmt, max_context=None):
     out = kv.decode_attention_q(to_dev(q, dev), to_dev(kp, dev), to_dev(vp, dev),
                                 to_dev(ks, dev), to_dev(vs, dev), to_dev(tables, dev),
