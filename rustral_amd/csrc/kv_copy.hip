@@ -301,15 +301,31 @@ __global__ __launch_bounds__(256) void append_q_kernel(
 }
 
 // gather_q: grid = (max_blocks_per_seq, num_seqs, 2 [K,V]); like gather_kernel,
-// one workgroup per logical block; each thread turns 16 stored bytes of a row
-// into 16 fp32 values (byte value * row scale).
-template <int FMT>
+// one workgroup per logical block of a sequence, K or V.  The block's
+// (block, head) tiles are consecutive in the pool, so its rows (every head)
+// are one run of num_kv_heads * block_size rows of D bytes, with their scales
+// one run of floats.  A thread turns one 4-byte word of a row into one
+// float4 (byte value * row scale): consecutive lanes take consecutive words,
+// so a wave-load reads 256 contiguous bytes and a wave-store writes 1 KiB of
+// one head's contiguous output rows (writing 16 floats per lane, the stores
+// of a wave were 64 bytes apart and the kernel streamed at half the rate).
+// Every load of a thread's share is issued before its first store; rows
+// past the context (the sequence's last block) are skipped.
+// Ordinary loads and nontemporal stores: 302-310 us at configs[2] (int8 /
+// fp8) against 314-324 us for the other three combinations.
+#ifndef RKV_GATHER_Q_NTL
+#define RKV_GATHER_Q_NTL 0
+#endif
+#ifndef RKV_GATHER_Q_NTS
+#define RKV_GATHER_Q_NTS 1
+#endif
+template <int D, int FMT>
 __global__ __launch_bounds__(256) void gather_q_kernel(
     float* __restrict__ k_out, float* __restrict__ v_out, const uint8_t* __restrict__ k_pool,
     const uint8_t* __restrict__ v_pool, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
-    const int64_t* __restrict__ out_offsets, int num_kv_heads, int head_dim, int block_size,
+    const int64_t* __restrict__ out_offsets, int num_kv_heads, int block_size, int bs_log2,
     int64_t num_blocks, int max_ctx) {
   const int j = blockIdx.x, b = blockIdx.y;
   const bool is_v = blockIdx.z != 0;
@@ -325,34 +341,58 @@ __global__ __launch_bounds__(256) void gather_q_kernel(
     row_stride = L;
   } else {
     L = L > max_ctx ? max_ctx : L;
-    seq_base = (int64_t)b * num_kv_heads * max_ctx * head_dim;
+    seq_base = (int64_t)b * num_kv_heads * max_ctx * D;
     row_stride = max_ctx;
   }
   const int p0 = j * block_size;
   if (p0 >= L) return;
   if (blk < 0 || blk >= num_blocks) return;
   const int nt = (L - p0) < block_size ? (L - p0) : block_size;
-  const uint8_t* src_pool = is_v ? v_pool : k_pool;
-  const float* scales = is_v ? v_scale : k_scale;
-  float* dst_all = is_v ? v_out : k_out;
-  const int per_row = head_dim >> 4;  // 16-byte units per row
-  const int units = num_kv_heads * nt * per_row;
-  for (int u = threadIdx.x; u < units; u += blockDim.x) {
-    const int hr = u / per_row, c = u - hr * per_row;  // hr = head * nt + token row
-    const int h = hr / nt, rr = hr - h * nt;
-    const int64_t r = ((int64_t)blk * num_kv_heads + h) * block_size + rr;
-    const uint4 w = *reinterpret_cast<const uint4*>(src_pool + r * head_dim + c * 16);
-    const float s = scales[r];
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-    float f[16];
+  constexpr int U = D / 4;  // words per row
+  const int rows = num_kv_heads * block_size;
+  const int units = rows * U;
+  const uint32_t* __restrict__ src =
+      reinterpret_cast<const uint32_t*>((is_v ? v_pool : k_pool) + (int64_t)blk * rows * D);
+  const float* __restrict__ sc = (is_v ? v_scale : k_scale) + (int64_t)blk * rows;
+  float* __restrict__ dst = (is_v ? v_out : k_out) + seq_base + (int64_t)p0 * D;
+  // row -> (head, row within the block)
+  auto split = [&](int row, int& h, int& rr) __attribute__((always_inline)) {
+    h = bs_log2 >= 0 ? row >> bs_log2 : row / block_size;
+    rr = row - h * block_size;
+  };
+  constexpr int UNR = 16;  // words in flight per thread
+  for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {
+    uint32_t w[UNR];
+    float s[UNR];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const uint8_t byte = (uint8_t)(ws[e >> 2] >> (8 * (e & 3)));
-      f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3(byte)) * s;
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * 256;
+      const int row = u / U;
+      int h, rr;
+      split(row, h, rr);
+      if (u < units && rr < nt) {
+        if constexpr (RKV_GATHER_Q_NTL) w[k] = __builtin_nontemporal_load(src + u);
+        else w[k] = src[u];
+        s[k] = sc[row];
+      }
     }
-    float* d = dst_all + seq_base + ((int64_t)h * row_stride + p0 + rr) * head_dim + c * 16;
 #pragma unroll
-    for (int e = 0; e < 16; e += 4) store16(d + e, make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]));
+    for (int k = 0; k < UNR; ++k) {
+      const int u = u0 + k * 256;
+      const int row = u / U, c = u - row * U;
+      int h, rr;
+      split(row, h, rr);
+      if (u < units && rr < nt) {
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t byte = (w[k] >> (8 * e)) & 0xffu;
+          f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3((uint8_t)byte)) * s[k];
+        }
+        store16<RKV_GATHER_Q_NTS>(dst + ((int64_t)h * row_stride + rr) * D + 4 * c,
+                make_float4(f[0], f[1], f[2], f[3]));
+      }
+    }
   }
 }
 
@@ -524,16 +564,22 @@ extern "C" int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, cons
     return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
   const dim3 grid((unsigned)max_blocks_per_seq, (unsigned)num_seqs, 2);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == RKV_I8)
-    gather_q_kernel<RKV_I8><<<grid, 256, 0, s>>>(
-        k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),
-        k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,
-        head_dim, block_size, num_blocks, max_ctx);
-  else
-    gather_q_kernel<RKV_FP8><<<grid, 256, 0, s>>>(
-        k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),
-        k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,
-        head_dim, block_size, num_blocks, max_ctx);
+  const int bs_log2 = (block_size & (block_size - 1)) ? -1 : __builtin_ctz((unsigned)block_size);
+#define RKV_GATHER_Q(D, F)                                                                      \
+  gather_q_kernel<D, F><<<grid, 256, 0, s>>>(                                                   \
+      k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),   \
+      k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,  \
+      block_size, bs_log2, num_blocks, max_ctx)
+  if (dtype == RKV_I8) {
+    if (head_dim == 32) RKV_GATHER_Q(32, RKV_I8);
+    else if (head_dim == 64) RKV_GATHER_Q(64, RKV_I8);
+    else RKV_GATHER_Q(128, RKV_I8);
+  } else {
+    if (head_dim == 32) RKV_GATHER_Q(32, RKV_FP8);
+    else if (head_dim == 64) RKV_GATHER_Q(64, RKV_FP8);
+    else RKV_GATHER_Q(128, RKV_FP8);
+  }
+#undef RKV_GATHER_Q
   return check_launch("rkv_gather_q");
 }
 

@@ -91,6 +91,34 @@ def test_gather_q_dequantizes_bitexact(dev, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
+@pytest.mark.parametrize("bs,d", [(12, 32), (16, 64), (8, 128)])
+def test_gather_q_every_byte_code_and_block_sizes(dev, fmt, bs, d):
+    """Every one of the 256 byte codes (fp8: NaN codes 0x7f / 0xff, both
+    zeros, subnormals, +-448) at several scales, block sizes that are not a
+    power of two, partial last blocks: the dequantized values equal the
+    oracle's bit for bit (NaNs compared as bit patterns)."""
+    say(f"gather_q all codes fmt={fmt} bs={bs} d={d}")
+    rng = np.random.default_rng(29)
+    hkv, nb = 3, 40
+    kp = (np.arange(nb * hkv * bs * d) % 256).astype(np.uint8).reshape(nb, hkv, bs, d)
+    vp = np.roll(kp, 7, axis=-1).copy()
+    ks = rng.choice(np.array([1.0, 0.5, 3.0e-3, 17.25, 2.0 ** -20], np.float32),
+                    (nb, hkv, bs)).astype(np.float32)
+    vs = rng.random((nb, hkv, bs)).astype(np.float32)
+    ctx = np.array([bs * 5 + 3, 1, bs, 0, bs * 9], np.int32)
+    tables = make_tables(rng, ctx, bs, nb)
+    k_out, v_out = kv.gather_q(to_dev(kp, dev), to_dev(vp, dev), to_dev(ks, dev),
+                               to_dev(vs, dev), to_dev(tables, dev), to_dev(ctx, dev), fmt,
+                               max_ctx=int(ctx.max()))
+    torch.cuda.synchronize()
+    kf = oracle.dequantize_pool(kp, ks, CODE[fmt])
+    vf = oracle.dequantize_pool(vp, vs, CODE[fmt])
+    wk, wv = oracle.gather(kf, vf, tables, ctx, max_ctx=int(ctx.max()), out_f32=True)
+    assert np.array_equal(to_np(k_out).view(np.uint32), wk.view(np.uint32))
+    assert np.array_equal(to_np(v_out).view(np.uint32), wv.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
 def test_gather_q_packed_layout_bitexact(dev, fmt):
     """The packed KVCache layout (sequence b's [Hkv, L_b, D] at its offset):
     dequantized values equal the oracle's gather of the dequantized pool, and
