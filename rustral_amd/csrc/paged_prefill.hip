@@ -512,8 +512,11 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     float* op = out + ((int64_t)(s0 + qi) * num_q_heads + h0 + hh) * D + 4 * grp;
 #pragma unroll
     for (int c = 0; c < NO; ++c)
-      *reinterpret_cast<float4*>(op + 16 * c) = make_float4(
-          o[hh][c][0] * inv, o[hh][c][1] * inv, o[hh][c][2] * inv, o[hh][c][3] * inv);
+      // nontemporal: the rows are not read again by this kernel (the
+      // admissions, whose fp32 output is ~45% of their bytes, ran 4% faster)
+      __builtin_nontemporal_store(
+          f32x4_t{o[hh][c][0] * inv, o[hh][c][1] * inv, o[hh][c][2] * inv, o[hh][c][3] * inv},
+          reinterpret_cast<f32x4_t*>(op + 16 * c));
   }
 }
 
