@@ -15,17 +15,22 @@ namespace {
 // Load / store policy: 1 = nontemporal (streaming) hint.  Measured on
 // configs[1]-sized calls (65,536-block pools, GB/s of algorithmic bytes):
 //   gather bf16 -> bf16: plain 5155, nt loads 5387, nt stores 5705, both 6066
-//   gather bf16 -> fp32: plain 4972, nt loads 5197, nt stores 3536 (the two
-//                        16-byte stores of a lane's 8 floats are not a
-//                        contiguous wave store; as streaming stores they lose
-//                        the L2 write combining)
-//   gather fp32 -> fp32: plain 5344, nt loads 5114, both 5277
+//   gather bf16 -> fp32, when a lane stored 8 floats as two 16-byte stores
+//                        (no contiguous wave store): plain 4972, nt loads
+//                        5197, nt stores 3536; with one lane-contiguous
+//                        16-byte store per lane: nt loads 5290-5355, both
+//                        6003-6074
+//   gather fp32 -> fp32: plain 5344, nt loads 5114, both 5277 (two 16-byte
+//                        accesses per lane); lane-contiguous, nt stores
+//                        5317-5325, plain 5208-5250
 //   copy_blocks: 5082 - 5177 for every policy
-// so the gather streams its loads for 16-bit pools and its stores for
-// 16-bit outputs (RKV_GATHER_NT = 0 turns both off), and copy_blocks streams
-// both.
+// so the gather streams its loads for 16-bit pools and its stores always
+// (RKV_GATHER_NT = 0 turns both off), and copy_blocks streams both.
 #ifndef RKV_GATHER_NT
 #define RKV_GATHER_NT 1
+#endif
+#ifndef RKV_GATHER_NTS_F32  // nontemporal stores for fp32 outputs as well
+#define RKV_GATHER_NTS_F32 1
 #endif
 #ifndef RKV_COPY_NTL
 #define RKV_COPY_NTL 1
@@ -54,6 +59,8 @@ __device__ __forceinline__ void store16(void* p, const V& v) {
   if constexpr (NT) __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), static_cast<u32x4_t*>(p));
   else *static_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
 }
+
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
 struct alignas(16) F8 {  // 8 floats = 32 bytes
   float4 a, b;
@@ -133,16 +140,24 @@ __global__ __launch_bounds__(256) void append_kernel(
 
 // ---- gather -----------------------------------------------------------------
 // grid = (max_blocks_per_seq, num_seqs, 2 [K,V]).  One workgroup copies the
-// valid rows of logical block j of sequence b for every head.  Inside a
-// (block, head) tile the first nt rows are contiguous in the pool and in the
-// output, so the copy is a flat run of nt*head_dim elements per head.
-template <typename TIn, typename TOut>
+// valid rows of logical block j of sequence b for every head.  The block's
+// (block, head) tiles are consecutive in the pool, so its rows (every head)
+// are one run of num_kv_heads * block_size rows; rows past the context (the
+// sequence's last block) are skipped.  A unit is 16 bytes of output (8
+// elements of a 16-bit output, 4 of an fp32 one) and its source elements:
+// consecutive lanes take consecutive units, so both the loads and the stores
+// of a wave are contiguous runs (an fp32 output from a bf16 pool: 512-byte
+// wave-loads, 1 KiB wave-stores).  DT is head_dim for the 32 / 64 / 128
+// builds (shifts), 0 for any other multiple of 8.
+template <typename TIn, typename TOut, int DT>
 __global__ __launch_bounds__(256) void gather_kernel(
     TOut* __restrict__ k_out, TOut* __restrict__ v_out, const TIn* __restrict__ k_pool,
     const TIn* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
     const int64_t* __restrict__ out_offsets, int num_kv_heads, int head_dim, int block_size,
-    int64_t num_blocks, int max_ctx) {
+    int bs_log2, int64_t num_blocks, int max_ctx) {
+  constexpr int EPU = 16 / sizeof(TOut);  // elements per unit
+  const int D = DT ? DT : head_dim;
   const int j = blockIdx.x, b = blockIdx.y;
   const bool is_v = blockIdx.z != 0;
   // the three per-sequence reads are independent: issued together
@@ -154,55 +169,87 @@ __global__ __launch_bounds__(256) void gather_kernel(
   L = L > cap ? cap : L;
   int row_stride;  // output rows per head
   if (out_offsets) {
-    if (seq_base < 0 || (seq_base & 7)) return;  // 16-byte vector stores need 8-element alignment
+    if (seq_base < 0 || (seq_base % EPU)) return;  // 16-byte vector stores
     row_stride = L;
   } else {
     L = L > max_ctx ? max_ctx : L;
-    seq_base = (int64_t)b * num_kv_heads * max_ctx * head_dim;
+    seq_base = (int64_t)b * num_kv_heads * max_ctx * D;
     row_stride = max_ctx;
   }
   const int p0 = j * block_size;
   if (p0 >= L) return;
   if (blk < 0 || blk >= num_blocks) return;
   const int nt = (L - p0) < block_size ? (L - p0) : block_size;
-  const TIn* src_pool = is_v ? v_pool : k_pool;
-  TOut* dst_all = is_v ? v_out : k_out;
-  const int per_head = (nt * head_dim) >> 3;  // 8-element units per head
-  const int units = num_kv_heads * per_head;
+  const int upr = D / EPU;  // units per row
+  const int rows = num_kv_heads * block_size;
+  const int units = rows * upr;
+  const TIn* __restrict__ src = (is_v ? v_pool : k_pool) + (int64_t)blk * rows * D;
+  TOut* __restrict__ dst = (is_v ? v_out : k_out) + seq_base + (int64_t)p0 * D;
   // Up to UNR units per thread per round: every load of the round is issued
   // before the first store, so a thread keeps UNR loads in flight.
-  constexpr int UNR = 8;
-  using In = typename std::conditional<sizeof(TIn) == 2, uint4, F8>::type;
+  constexpr int UNR = sizeof(TIn) < sizeof(TOut) ? 16 : 8;
+  constexpr int LB = EPU * sizeof(TIn);  // bytes loaded per unit: 16, or 8 (bf16 -> fp32)
+  using In = typename std::conditional<LB == 16, uint4, uint2>::type;
   constexpr bool NTL = RKV_GATHER_NT && sizeof(TIn) == 2;
-  constexpr bool NTS = RKV_GATHER_NT && sizeof(TIn) == 2 && sizeof(TOut) == 2;
-  for (int u0 = threadIdx.x; u0 < units; u0 += UNR * blockDim.x) {
-    In x[UNR];
+  constexpr bool NTS = RKV_GATHER_NT && (sizeof(TOut) == 2 || RKV_GATHER_NTS_F32);
+  // P2: the block size is a power of two (unit -> head and row by shifts;
+  // the choice is made once, outside the unrolled loops)
+  auto run = [&](auto p2, auto masked) __attribute__((always_inline)) {
+    constexpr bool P2 = decltype(p2)::value;
+    constexpr bool MASKED = decltype(masked)::value;
+    // unit -> (head, row within the block, unit within the row)
+    auto split = [&](int u, int& h, int& rr, int& c) __attribute__((always_inline)) {
+      const int row = u / upr;
+      c = u - row * upr;
+      h = P2 ? row >> bs_log2 : row / block_size;
+      rr = row - h * block_size;
+    };
+    for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {  // 256 threads
+      // Loads without branches: a unit past the block (u >= units) reads the
+      // block's last unit instead, and rows past the context are rows of the
+      // same block, so every load is in bounds; only the stores are
+      // conditional.  (Loads under branches left the compiler unable to
+      // count them, and it waited for all memory operations before every
+      // store.)
+      uint4 y[UNR];  // the 16 output bytes of each unit
 #pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * blockDim.x;
-      if (u < units) {
-        const int h = u / per_head, r = u - h * per_head;
-        const TIn* s = src_pool + ((int64_t)blk * num_kv_heads + h) * block_size * head_dim + r * 8;
-        if constexpr (sizeof(TIn) == 2)
-          x[k] = ld16<NTL>(s);
+      for (int k = 0; k < UNR; ++k) {
+        const int u = u0 + k * 256;
+        const int uc = u < units ? u : units - 1;
+        const In* p = reinterpret_cast<const In*>(src + (int64_t)uc * EPU);
+        In x;
+        if constexpr (LB == 16)
+          x = ld16<NTL>(p);
+        else if constexpr (NTL)
+          x = __builtin_bit_cast(In,
+                                 __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p)));
         else
-          x[k] = load_f8<false>(reinterpret_cast<const float*>(s));
+          x = *p;
+        if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4)
+          y[k] = make_uint4(x.x << 16, x.x & 0xffff0000u, x.y << 16, x.y & 0xffff0000u);
+        else
+          y[k] = x;
+      }
+#pragma unroll
+      for (int k = 0; k < UNR; ++k) {
+        const int u = u0 + k * 256;
+        int h, rr, c;
+        split(u, h, rr, c);
+        if (!MASKED || (u < units && rr < nt))
+          store16<NTS>(dst + ((int64_t)h * row_stride + rr) * D + c * EPU, y[k]);
       }
     }
-#pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * blockDim.x;
-      if (u < units) {
-        const int h = u / per_head, r = u - h * per_head;
-        TOut* d = dst_all + seq_base + ((int64_t)h * row_stride + p0) * head_dim + r * 8;
-        if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 2)
-          store16<NTS>(d, x[k]);
-        else if constexpr (sizeof(TIn) == 2)
-          store_f8<false>(reinterpret_cast<float*>(d), bf16x8_to_f8(x[k]));
-        else
-          store_f8<false>(reinterpret_cast<float*>(d), x[k]);
-      }
-    }
+  };
+  // A full block whose units fill whole rounds stores without conditions,
+  // so the compiler's wait counts follow the loads and stores in order (a
+  // store under a branch made it wait for every earlier store at the end
+  // of a round).
+  if (nt == block_size && units % (UNR * 256) == 0) {
+    if (bs_log2 >= 0) run(std::true_type{}, std::false_type{});
+    else run(std::false_type{}, std::false_type{});
+  } else {
+    if (bs_log2 >= 0) run(std::true_type{}, std::true_type{});
+    else run(std::false_type{}, std::true_type{});
   }
 }
 
@@ -470,11 +517,19 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
     return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
   dim3 grid((unsigned)max_blocks_per_seq, (unsigned)num_seqs, 2);
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define RKV_GATHER(TI, TO)                                                                     \
-  gather_kernel<TI, TO><<<grid, 256, 0, s>>>(                                                  \
+  const int bs_log2 = (block_size & (block_size - 1)) ? -1 : __builtin_ctz((unsigned)block_size);
+#define RKV_GATHER_D(TI, TO, DT)                                                               \
+  gather_kernel<TI, TO, DT><<<grid, 256, 0, s>>>(                                              \
       static_cast<TO*>(k_out), static_cast<TO*>(v_out), static_cast<const TI*>(k_pool),        \
       static_cast<const TI*>(v_pool), block_tables, max_blocks_per_seq, ctx_lens, out_offsets, \
-      num_kv_heads, head_dim, block_size, num_blocks, max_ctx)
+      num_kv_heads, head_dim, block_size, bs_log2, num_blocks, max_ctx)
+#define RKV_GATHER(TI, TO)                       \
+  do {                                           \
+    if (head_dim == 128) RKV_GATHER_D(TI, TO, 128); \
+    else if (head_dim == 64) RKV_GATHER_D(TI, TO, 64); \
+    else if (head_dim == 32) RKV_GATHER_D(TI, TO, 32); \
+    else RKV_GATHER_D(TI, TO, 0);                \
+  } while (0)
   if (dtype == RKV_F32)
     RKV_GATHER(float, float);
   else if (out_dtype == RKV_F32)
@@ -482,6 +537,7 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
   else
     RKV_GATHER(uint16_t, uint16_t);
 #undef RKV_GATHER
+#undef RKV_GATHER_D
   return check_launch("rkv_gather");
 }
 

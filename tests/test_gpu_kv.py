@@ -140,6 +140,44 @@ def test_gather_bitexact_padded_and_packed(dev, dtype, out_f32):
     assert np.array_equal(to_np(ko), rk) and np.array_equal(to_np(vo), rv)
 
 
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("hkv,bs,d", [(1, 16, 32), (2, 12, 64), (3, 8, 40), (8, 32, 96),
+                                      (4, 16, 128), (8, 24, 128)])
+def test_gather_block_sizes_head_dims_and_guards(dev, dtype, out_f32, hkv, bs, d):
+    """Block sizes that are and are not powers of two, head dims with and
+    without a specialised build, blocks that fill whole rounds of the
+    kernel and blocks that do not, partial last blocks: the packed output
+    equals the oracle's, and guard rows after every sequence stay
+    untouched."""
+    say(f"gather hkv={hkv} bs={bs} d={d} dtype={dtype} out_f32={out_f32}")
+    rng = np.random.default_rng(hkv * 100 + bs + d)
+    nb = 64
+    ctx = np.array([bs * 3, 1, bs - 1, 0, bs * 7 + 5, bs + 1], np.int32)
+    kp, vp, _, _ = make_pool(rng, nb, hkv, bs, d, dtype)
+    tables = make_tables(rng, ctx, bs, nb)
+    gap = hkv * d
+    sizes = ctx.astype(np.int64) * hkv * d + gap
+    off = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    total = int(sizes.sum())
+    odt = torch.float32 if (out_f32 or dtype == "f32") else torch.bfloat16
+    guard = -3.5
+    ko = torch.full((total,), guard, dtype=odt, device=dev)
+    vo = torch.full((total,), guard, dtype=odt, device=dev)
+    kv.gather(to_dev(kp, dev), to_dev(vp, dev), to_dev(tables, dev), to_dev(ctx, dev),
+              out_offsets=to_dev(off, dev), out_total=total, out_dtype=odt, k_out=ko, v_out=vo)
+    torch.cuda.synchronize()
+    np_dt = np.float32 if odt == torch.float32 else np.uint16
+    g = np.float32(guard) if np_dt == np.float32 else oracle.bf16_from_f32(np.float32([guard]))[0]
+    rk = np.full(total, g, np_dt)
+    rv = np.full(total, g, np_dt)
+    oracle.gather(kp, vp, tables, ctx, out_offsets=off, out_f32=out_f32, k_out=rk, v_out=rv)
+    assert np.array_equal(to_np(ko), rk) and np.array_equal(to_np(vo), rv)
+    for b in range(len(ctx)):
+        g0 = int(off[b] + ctx[b] * hkv * d)
+        assert (rk[g0:g0 + gap] == g).all()
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_gather_of_append_roundtrip_config1_shape(dev, dtype):
     """Config-1 shape (Hkv 8, D 128, BS 16, 65,536-block pool, 64 sequences with
