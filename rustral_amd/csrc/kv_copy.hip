@@ -402,45 +402,62 @@ __global__ __launch_bounds__(256) void gather_q_kernel(
       reinterpret_cast<const uint32_t*>((is_v ? v_pool : k_pool) + (int64_t)blk * rows * D);
   const float* __restrict__ sc = (is_v ? v_scale : k_scale) + (int64_t)blk * rows;
   float* __restrict__ dst = (is_v ? v_out : k_out) + seq_base + (int64_t)p0 * D;
-  // row -> (head, row within the block)
-  auto split = [&](int row, int& h, int& rr) __attribute__((always_inline)) {
-    h = bs_log2 >= 0 ? row >> bs_log2 : row / block_size;
-    rr = row - h * block_size;
-  };
   constexpr int UNR = 16;  // words in flight per thread
-  for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {
-    uint32_t w[UNR];
-    float s[UNR];
+  // Loads without branches (a unit past the block reads the block's last
+  // word; rows past the context are rows of the same block), and the
+  // power-of-two test made once.  For int8 pools a full block that fills
+  // whole rounds also stores without conditions: branches around the loads
+  // or stores left the compiler waiting for every earlier memory operation
+  // before each store (the fp8 decode, ~8 VALU per byte, measured faster
+  // with each conversion kept beside its conditional store).
+  auto run = [&](auto p2, auto masked) __attribute__((always_inline)) {
+    constexpr bool P2 = decltype(p2)::value;
+    constexpr bool MASKED = decltype(masked)::value;
+    // row -> (head, row within the block)
+    auto split = [&](int row, int& h, int& rr) __attribute__((always_inline)) {
+      h = P2 ? row >> bs_log2 : row / block_size;
+      rr = row - h * block_size;
+    };
+    for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {  // 256 threads
+      uint32_t w[UNR];
+      float sk[UNR];
 #pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * 256;
-      const int row = u / U;
-      int h, rr;
-      split(row, h, rr);
-      if (u < units && rr < nt) {
-        if constexpr (RKV_GATHER_Q_NTL) w[k] = __builtin_nontemporal_load(src + u);
-        else w[k] = src[u];
-        s[k] = sc[row];
+      for (int k = 0; k < UNR; ++k) {
+        const int u = u0 + k * 256;
+        const int uc = u < units ? u : units - 1;
+        if constexpr (RKV_GATHER_Q_NTL) w[k] = __builtin_nontemporal_load(src + uc);
+        else w[k] = src[uc];
+        sk[k] = sc[uc / U];
+      }
+#pragma unroll
+      for (int k = 0; k < UNR; ++k) {
+        const int u = u0 + k * 256;
+        const int row = u / U, c = u - row * U;
+        int h, rr;
+        split(row, h, rr);
+        if (!MASKED || (u < units && rr < nt)) {
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t byte = (w[k] >> (8 * e)) & 0xffu;
+            f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3((uint8_t)byte)) * sk[k];
+          }
+          store16<RKV_GATHER_Q_NTS>(dst + ((int64_t)h * row_stride + rr) * D + 4 * c,
+                                    make_float4(f[0], f[1], f[2], f[3]));
+        }
       }
     }
-#pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int u = u0 + k * 256;
-      const int row = u / U, c = u - row * U;
-      int h, rr;
-      split(row, h, rr);
-      if (u < units && rr < nt) {
-        float f[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t byte = (w[k] >> (8 * e)) & 0xffu;
-          f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3((uint8_t)byte)) * s[k];
-        }
-        store16<RKV_GATHER_Q_NTS>(dst + ((int64_t)h * row_stride + rr) * D + 4 * c,
-                make_float4(f[0], f[1], f[2], f[3]));
-      }
+  };
+  const bool whole = nt == block_size && units % (UNR * 256) == 0;
+  if constexpr (FMT == RKV_I8) {
+    if (whole) {
+      if (bs_log2 >= 0) run(std::true_type{}, std::false_type{});
+      else run(std::false_type{}, std::false_type{});
+      return;
     }
   }
+  if (bs_log2 >= 0) run(std::true_type{}, std::true_type{});
+  else run(std::false_type{}, std::true_type{});
 }
 
 int check_common(int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, int dtype) {
