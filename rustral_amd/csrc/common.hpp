@@ -58,6 +58,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // decode-shaped stream of 4 KiB tiles reads ~12% faster this way
 // (5.6 -> 6.35 TB/s measured for the configs[2] access pattern).
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 load_stream(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
   return make_uint4(v[0], v[1], v[2], v[3]);

@@ -60,8 +60,6 @@ __device__ __forceinline__ void store16(void* p, const V& v) {
   else *static_cast<u32x4_t*>(p) = __builtin_bit_cast(u32x4_t, v);
 }
 
-typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-
 struct alignas(16) F8 {  // 8 floats = 32 bytes
   float4 a, b;
 };
