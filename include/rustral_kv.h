@@ -108,22 +108,36 @@ int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int 
 /* Workspace (bytes) rkv_decode_attention needs for split-K partials.
  * max_context: host-side upper bound on every ctx_lens[b] (for example
  * max_blocks_per_seq*block_size).  partition_size: the size the call will
- * use (rkv_decode_partition_size), or <= 0 for the library's default at this
- * max_context (enough for every pool dtype). */
+ * use (rkv_decode_partition_size_for), or <= 0 for the smallest size any
+ * call picks by itself (640), which is enough for every pool dtype and
+ * shape. */
 size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_context,
                                   int partition_size);
 
-/* Partition size (tokens) rkv_decode_attention uses for pools of dtype and
- * this max_context, for a request of partition_size: the request itself when
- * it is a multiple of 64 tokens (16 tokens x 4 waves) up to 640; for
- * partition_size <= 0 the default, 640 at every max_context (measured
- * faster than 512 for contexts from U[1, 8192] to U[16384, 65536]).
- * RKV_ERR_UNSUPPORTED for other requests. */
+/* Partition size (tokens) for pools of dtype and this max_context, for a
+ * request of partition_size: the request itself when it is a multiple of 64
+ * tokens (16 tokens x 4 waves) up to 640, or for RKV_BF16 pools a multiple
+ * of 128 (16 tokens x 8 waves) up to 1280; for partition_size <= 0 the size
+ * the split entry points (rkv_decode_attention_partitions / _merge) use,
+ * 640.  RKV_ERR_UNSUPPORTED for other requests.  What rkv_decode_attention
+ * picks for a whole call: rkv_decode_partition_size_for. */
 int rkv_decode_partition_size(int partition_size, int head_dim, int dtype, int max_context);
+
+/* Partition size rkv_decode_attention (and _noalloc) uses for a call of this
+ * shape: the request when partition_size > 0 (rules of
+ * rkv_decode_partition_size), else its own pick: for RKV_BF16 pools with
+ * head_dim 128 and at most 4 query heads per KV head, 1280 when
+ * num_kv_heads * num_seqs * max_context / 2 >= 1200 * 1280 tokens, else 768
+ * when that is >= 1000 * 768, else 640; 640 for every other shape and
+ * dtype.  The split entry points take this value as their partition_size to
+ * match the one-call entry point. */
+int rkv_decode_partition_size_for(int partition_size, int num_seqs, int num_q_heads,
+                                  int num_kv_heads, int head_dim, int dtype, int max_context);
 
 /* Single-token paged decode attention with GQA (two passes: partitions of
  * partition_size tokens -- see rkv_decode_partition_size; <= 0 for the
- * default -- then a merge; one partition skips the merge).
+ * library's pick for this shape, rkv_decode_partition_size_for -- then a
+ * merge; one partition skips the merge).
  * Replaces the per-head recipe of TapeMultiHeadAttention
  * (crates/nn/src/tape_transformer.rs:87-139), for one query token per
  * sequence attending to its whole cache, and AttentionOps
@@ -166,7 +180,10 @@ size_t rkv_decode_noalloc_max_bytes(void);
 /* The two passes of rkv_decode_attention as separate launches, for callers
  * that schedule them apart (and for per-kernel timing).  Same arguments;
  * pass 1 writes finished rows for single-partition sequences and partials
- * for the rest, pass 2 merges the partials. */
+ * for the rest, pass 2 merges the partials.  Both passes must be given the
+ * same partition_size; <= 0 means 640 here (the merge has no KV-head count
+ * to pick by shape), so to match rkv_decode_attention pass the value of
+ * rkv_decode_partition_size_for. */
 int rkv_decode_attention_partitions(float* out, const float* q, const void* k_pool,
                                     const void* v_pool, const int32_t* block_tables,
                                     int max_blocks_per_seq, const int32_t* ctx_lens,

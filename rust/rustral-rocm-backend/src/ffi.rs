@@ -141,6 +141,15 @@ extern "C" {
         dtype: c_int,
         max_context: c_int,
     ) -> c_int;
+    pub fn rkv_decode_partition_size_for(
+        partition_size: c_int,
+        num_seqs: c_int,
+        num_q_heads: c_int,
+        num_kv_heads: c_int,
+        head_dim: c_int,
+        dtype: c_int,
+        max_context: c_int,
+    ) -> c_int;
     pub fn rkv_decode_attention(
         out: *mut f32,
         q: *const f32,

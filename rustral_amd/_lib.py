@@ -26,6 +26,7 @@ SIGNATURES = {
     "rkv_copy_blocks": (_i, [_p, _p, _i64, _i, _p, _i, _i64, _i64, _p]),
     "rkv_decode_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "rkv_decode_partition_size": (_i, [_i, _i, _i, _i]),
+    "rkv_decode_partition_size_for": (_i, [_i, _i, _i, _i, _i, _i, _i]),
     "rkv_decode_attention": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64, _i, _f,
                                   _i, _i, _p, _sz, _p]),
     "rkv_decode_attention_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,

@@ -1284,25 +1284,67 @@ constexpr int split_of() { return sizeof(T) == 1 ? RKV_DECODE_SPLIT_Q : RKV_DECO
 // lengths: the largest, and for 16-bit and fp32 pools also 512 tokens, so
 // that a caller asking for 512-token partitions runs them without masked
 // slots; other sizes run on the smallest build that holds them, the extra
-// slots masked.  Default: the largest (640 tokens) at every context length
-// -- bf16 pools measured 640 faster than 512 by 0.4-2% from contexts
-// U[1, 8192] at 256 sequences to U[16384, 65536] at 8.
+// slots masked.
+// bf16 pools also have two builds of 8-wave workgroups (the same 160-token
+// slice per wave, twice the slices per workgroup): 768 tokens (6 tiles per
+// wave) and 1280 tokens (10 tiles per wave); requests that are multiples of
+// 128 above 640 run on them.  Measured in one process against the 4-wave
+// 640-token build (us per call): configs[2] (64 sequences, contexts
+// U[512, 4096]) 109.0 -> 106.7 at 768 (122.8 at 1280: too few workgroups);
+// 256 x U[1, 8192] 769.3 -> 736.9 at 1280; 64 x U[8192, 16384] 547.0 ->
+// 526.5; 32 x U[12288, 24576] 403.4 -> 387.1; configs[3] (8 x U[16384,
+// 65536]) 221.2 -> 214.2.  Fewer partitions per sequence mean fewer split-K
+// partials and a cheaper merge; the number of waves is the same.
+// They pay off only with enough work: at 8 x U[512, 4096] 768 was 5% slower
+// than 640, at 4 x U[16384, 32768] 1280 was 10% slower, and for 8 query
+// heads per KV head (more registers, two waves per SIMD) both were slower
+// (64 x U[512, 4096]: 125 -> 158 us), as for head_dim 64.
+// Defaults: the split entry points (rkv_decode_attention_partitions /
+// _merge, which take no KV-head count) and fp32 / 1-byte pools use 640;
+// rkv_decode_attention picks by the call's shape (shape_part).
 constexpr int kSmallP = 512;
 static_assert(kSmallP <= kP && kSmallP % (16 * RKV_DECODE_SPLIT) == 0, "small partition build");
+constexpr int kWideSplit = 8;
+constexpr int kWideP1 = 768, kWideP2 = 1280;
+static_assert(kWideP1 % (16 * kWideSplit) == 0 && kWideP2 % (16 * kWideSplit) == 0 &&
+                  kWideP1 > kP,
+              "wide partition builds");
 
 inline bool one_byte(int dtype) { return dtype == RKV_I8 || dtype == RKV_FP8; }
 
 int default_part(int dtype, int /*max_context*/) { return one_byte(dtype) ? kPQ : kP; }
 
+// The partition size rkv_decode_attention uses when the caller leaves it to
+// the library: for bf16 pools with head_dim 128 and at most 4 query heads
+// per KV head, 1280 when the call holds work for at least 1,200 such
+// partitions over all KV heads (contexts taken as uniform up to cap), else
+// 768 when it holds work for 1,000 of those, else 640 (the measurements
+// above: configs[2] 768, configs[3] and 256 x U[1, 8192] 1280, small
+// batches 640).
+int shape_part(int dtype, int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+               int cap) {
+  if (dtype != RKV_BF16 || head_dim != 128 || num_kv_heads <= 0 || num_seqs <= 0 ||
+      num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > 4 || cap <= 0)
+    return default_part(dtype, cap);
+  const double work = (double)num_kv_heads * num_seqs * (0.5 * cap);  // KV-head tokens
+  if (work >= 1200.0 * kWideP2) return kWideP2;
+  if (work >= 1000.0 * kWideP1) return kWideP1;
+  return kP;
+}
+
 // The partition size a call uses: the request when it is > 0 (a multiple of
-// 16 * SPLIT, at most the largest build), else the default; a negative
-// status for an unsupported request.
+// 16 * SPLIT up to the largest 4-wave build, or for bf16 pools a multiple of
+// 128 up to 1280), else the default; a negative status for an unsupported
+// request.
 int resolve_part(int requested, int dtype, int max_context) {
   if (requested <= 0) return default_part(dtype, max_context);
   const int split = one_byte(dtype) ? RKV_DECODE_SPLIT_Q : RKV_DECODE_SPLIT;
   const int maxp = one_byte(dtype) ? kPQ : kP;
-  if (requested % (16 * split) != 0 || requested > maxp) return RKV_ERR_UNSUPPORTED;
-  return requested;
+  if (requested % (16 * split) == 0 && requested <= maxp) return requested;
+  if (dtype == RKV_BF16 && requested > maxp && requested <= kWideP2 &&
+      requested % (16 * kWideSplit) == 0)
+    return requested;
+  return RKV_ERR_UNSUPPORTED;
 }
 
 struct Launch {
@@ -1314,27 +1356,34 @@ struct Launch {
 
 // Ring depth: RKV_DECODE_RING_LOADS 16-byte loads per lane in flight, at most
 // every tile of the wave's slice.
-template <typename T, int D, int NTILE>
+template <typename T, int D, int NTILE, int SPLIT>
 constexpr int ring_for() {
   constexpr int nl = kBS / (64 / (D / Traits<T>::E));
   constexpr int r = (sizeof(T) == 1 ? RKV_DECODE_RING_LOADS_Q : RKV_DECODE_RING_LOADS) / nl;
-  constexpr int nt = 2 * NTILE / split_of<T>();
+  constexpr int nt = 2 * NTILE / SPLIT;
   return r < 1 ? 1 : (r > nt ? nt : r);
 }
 
-template <typename T, int D, int G, int FMT, int NTILE>
+template <typename T, int D, int G, int FMT, int NTILE, int SPLIT = split_of<T>()>
 Launch make_launch() {
   Launch l;
-  l.nw = split_of<T>();
-  l.kernel = &decode_stream_kernel<T, D, G, kBS, NTILE, ring_for<T, D, NTILE>(), split_of<T>(),
+  l.nw = SPLIT;
+  l.kernel = &decode_stream_kernel<T, D, G, kBS, NTILE, ring_for<T, D, NTILE, SPLIT>(), SPLIT,
                                    FMT>;
   return l;
 }
 
-// The build for partitions of P tokens: the 512-token build when it holds
-// them (16-bit and fp32 pools), else the largest.
+// The build for partitions of P tokens: above the largest 4-wave build (bf16
+// pools), the smallest 8-wave build that holds them; else the 512-token
+// build when it holds them (16-bit and fp32 pools), else the largest.
 template <typename T, int D, int G, int FMT>
 Launch pick_p(int P) {
+  if constexpr (FMT == RKV_BF16) {
+    if (P > kP) {
+      if (P <= kWideP1) return make_launch<T, D, G, FMT, kWideP1 / kBS, kWideSplit>();
+      return make_launch<T, D, G, FMT, kWideP2 / kBS, kWideSplit>();
+    }
+  }
   if constexpr (sizeof(T) != 1 && kSmallP < kP) {
     if (P <= kSmallP) return make_launch<T, D, G, FMT, kSmallP / kBS>();
   }
@@ -1427,7 +1476,8 @@ int validate(const DecodeArgs& a, int& max_parts, int& P) {
   P = resolve_part(a.partition_size, a.dtype, a.max_context);
   if (P < 0)
     return fail(RKV_ERR_UNSUPPORTED,
-                "partition_size must be a multiple of 64 tokens up to 640 (or <= 0 for the default)");
+                "partition_size must be a multiple of 64 tokens up to 640, for bf16 pools also a "
+                "multiple of 128 up to 1280 (or <= 0 for the default)");
   if (a.num_seqs > 65535 || a.num_kv_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_kv_heads must be <= 65535");
   if (a.max_context < 0) return fail(RKV_ERR_INVALID_ARG, "max_context must be >= 0");
@@ -1545,7 +1595,24 @@ extern "C" int rkv_decode_partition_size(int partition_size, int head_dim, int d
     return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_F32, RKV_BF16, RKV_I8 or RKV_FP8");
   const int P = resolve_part(partition_size, dtype, max_context);
   if (P < 0)
-    return fail(P, "partition_size must be a multiple of 64 tokens up to 640 (or <= 0)");
+    return fail(P, "partition_size must be a multiple of 64 tokens up to 640, for bf16 pools also "
+                   "a multiple of 128 up to 1280 (or <= 0)");
+  return P;
+}
+
+extern "C" int rkv_decode_partition_size_for(int partition_size, int num_seqs, int num_q_heads,
+                                             int num_kv_heads, int head_dim, int dtype,
+                                             int max_context) {
+  clear_error();
+  if (dtype != RKV_F32 && dtype != RKV_BF16 && !one_byte(dtype))
+    return fail(RKV_ERR_INVALID_ARG, "dtype must be RKV_F32, RKV_BF16, RKV_I8 or RKV_FP8");
+  if (partition_size <= 0)
+    return shape_part(dtype, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                      max_context < 0 ? 0 : max_context);
+  const int P = resolve_part(partition_size, dtype, max_context);
+  if (P < 0)
+    return fail(P, "partition_size must be a multiple of 64 tokens up to 640, for bf16 pools also "
+                   "a multiple of 128 up to 1280 (or <= 0)");
   return P;
 }
 
@@ -1580,7 +1647,8 @@ extern "C" int rkv_decode_attention_merge(float* out, const int32_t* ctx_lens,
   const int P = resolve_part(partition_size, dtype, max_context);
   if (P < 0)
     return fail(RKV_ERR_UNSUPPORTED,
-                "partition_size must be a multiple of 64 tokens up to 640 (or <= 0 for the default)");
+                "partition_size must be a multiple of 64 tokens up to 640, for bf16 pools also a "
+                "multiple of 128 up to 1280 (or <= 0 for the default)");
   if (num_seqs > 65535 || num_q_heads > 65535)
     return fail(RKV_ERR_INVALID_ARG, "num_seqs and num_q_heads must be <= 65535");
   const int cap = ctx_cap_of(max_context, max_blocks_per_seq, block_size);
@@ -1603,15 +1671,23 @@ extern "C" int rkv_decode_attention(float* out, const float* q, const void* k_po
                                     int block_size, int64_t num_blocks, int max_context,
                                     float scale, int dtype, int partition_size, void* workspace,
                                     size_t workspace_bytes, void* stream) {
+  // both passes take the same explicit partition size: the request, or the
+  // size shape_part picks for this call
+  const int P =
+      partition_size > 0
+          ? partition_size
+          : shape_part(dtype, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                       ctx_cap_of(max_context < 0 ? 0 : max_context,
+                                  max_blocks_per_seq < 0 ? 0 : max_blocks_per_seq, block_size));
   int rc = rkv_decode_attention_partitions(out, q, k_pool, v_pool, block_tables,
                                            max_blocks_per_seq, ctx_lens, num_seqs, num_q_heads,
                                            num_kv_heads, head_dim, block_size, num_blocks,
-                                           max_context, scale, dtype, partition_size, workspace,
+                                           max_context, scale, dtype, P, workspace,
                                            workspace_bytes, stream);
   if (rc) return rc;
   return rkv_decode_attention_merge(out, ctx_lens, max_blocks_per_seq, num_seqs, num_q_heads,
-                                    head_dim, block_size, max_context, dtype, partition_size,
-                                    workspace, workspace_bytes, stream);
+                                    head_dim, block_size, max_context, dtype, P, workspace,
+                                    workspace_bytes, stream);
 }
 
 // ---- the entry point that allocates nothing -----------------------------------
@@ -1671,12 +1747,16 @@ extern "C" int rkv_decode_attention_noalloc(float* out, const float* q, const vo
                                             int max_context, float scale, int dtype,
                                             int partition_size, void* stream) {
   clear_error();
-  const int P = resolve_part(partition_size, dtype, max_context);
-  if (P < 0)
-    return fail(RKV_ERR_UNSUPPORTED,
-                "partition_size must be a multiple of 64 tokens up to 640 (or <= 0 for the default)");
   const int cap = ctx_cap_of(max_context < 0 ? 0 : max_context, max_blocks_per_seq < 0 ? 0 : max_blocks_per_seq,
                              block_size);
+  // the size rkv_decode_attention will use (the request, or its shape's pick)
+  const int P = partition_size > 0
+                    ? resolve_part(partition_size, dtype, max_context)
+                    : shape_part(dtype, num_seqs, num_q_heads, num_kv_heads, head_dim, cap);
+  if (P < 0)
+    return fail(RKV_ERR_UNSUPPORTED,
+                "partition_size must be a multiple of 64 tokens up to 640, for bf16 pools also a "
+                "multiple of 128 up to 1280 (or <= 0 for the default)");
   const int max_parts = cap <= 0 ? 1 : (cap + P - 1) / P;
   const size_t need = (num_seqs > 0 && num_q_heads > 0 && head_dim > 0)
                           ? ws_bytes(num_seqs, num_q_heads, head_dim, max_parts)
@@ -1690,7 +1770,7 @@ extern "C" int rkv_decode_attention_noalloc(float* out, const float* q, const vo
     if (int rc = scratch_for(static_cast<hipStream_t>(stream), &ws)) return rc;
   return rkv_decode_attention(out, q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens,
                               num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
-                              num_blocks, max_context, scale, dtype, partition_size, ws,
+                              num_blocks, max_context, scale, dtype, P, ws,
                               need > 0 ? kScratchBytes : 0, stream);
 }
 

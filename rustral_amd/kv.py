@@ -128,8 +128,18 @@ def workspace_bytes(num_seqs: int, num_q_heads: int, head_dim: int, max_context:
 
 
 def partition_size(dtype_code: int, max_context: int, requested: int = 0, head_dim: int = 128) -> int:
-    """The partition size a decode call uses (a request <= 0: the default)."""
+    """The partition size of the split entry points (a request <= 0: 640)."""
     p = lib().rkv_decode_partition_size(requested, head_dim, dtype_code, max_context)
+    check(min(p, 0))
+    return int(p)
+
+
+def partition_size_for(num_seqs: int, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                       dtype_code: int, max_context: int, requested: int = 0) -> int:
+    """The partition size decode_attention uses for a call of this shape (a
+    request <= 0: the library's pick)."""
+    p = lib().rkv_decode_partition_size_for(requested, num_seqs, num_q_heads, num_kv_heads,
+                                            head_dim, dtype_code, max_context)
     check(min(p, 0))
     return int(p)
 
@@ -166,6 +176,10 @@ def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
     dt = _dtype_code(k_pool)
     s = _stream(q)
+    if passes != "both" and partition_size <= 0:
+        # the split entry points take 640 for 0: ask for this shape's pick so
+        # the two passes partition like the one-call entry point
+        partition_size = partition_size_for(B, hq, hkv, d, dt, min(max_context, mbs * bs))
     if passes in ("both", "partitions"):
         fn = lib().rkv_decode_attention if passes == "both" else lib().rkv_decode_attention_partitions
         check(fn(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(),
@@ -405,4 +419,4 @@ class DeviceBlockManager:
 
 __all__ = ["append", "gather", "copy_blocks", "decode_attention", "prefill_attention",
            "append_q", "gather_q", "decode_attention_q", "workspace_bytes",
-           "DeviceBlockManager", "_lib"]
+           "DeviceBlockManager", "_lib", "partition_size_for"]

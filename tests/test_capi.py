@@ -82,15 +82,50 @@ def test_workspace_size():
             Pd = L.rkv_decode_partition_size(0, 128, dt, maxc)
             assert Pd > 0 and Pd % 64 == 0
             assert ws >= L.rkv_decode_workspace_bytes(8, 32, 128, maxc, Pd)
-    # the default is 640-token partitions at every context length
+    # the split entry points' default is 640 for every dtype and context
     for dt in (RKV_F32, RKV_BF16, RKV_I8, RKV_FP8):
         for maxc in (16, 4096, 65536):
             assert L.rkv_decode_partition_size(0, 128, dt, maxc) == 640
+    # the one-call pick by shape: bf16, head_dim 128, <= 4 query heads per KV
+    # head; 1280 with work for >= 1200 such partitions, 768 with work for >=
+    # 1000 of those, else 640 (configs[2]: 768; configs[3] and 256 x 8192:
+    # 1280; small batches, 8 heads per KV head, head_dim 64, fp32 and 1-byte
+    # pools: 640)
+    F = L.rkv_decode_partition_size_for
+    assert F(0, 64, 32, 8, 128, RKV_BF16, 4096) == 768
+    assert F(0, 8, 32, 8, 128, RKV_BF16, 65536) == 1280
+    assert F(0, 256, 32, 8, 128, RKV_BF16, 8192) == 1280
+    assert F(0, 8, 32, 8, 128, RKV_BF16, 4096) == 640
+    assert F(0, 4, 32, 8, 128, RKV_BF16, 32768) == 640
+    assert F(0, 64, 64, 8, 128, RKV_BF16, 4096) == 640    # G = 8
+    assert F(0, 64, 32, 8, 64, RKV_BF16, 4096) == 640     # head_dim 64
+    assert F(0, 64, 8, 8, 128, RKV_BF16, 4096) == 768     # G = 1
+    for dt in (RKV_F32, RKV_I8, RKV_FP8):
+        assert F(0, 256, 32, 8, 128, dt, 65536) == 640
+    # a request is the request, with the rules of rkv_decode_partition_size
+    assert F(512, 64, 32, 8, 128, RKV_BF16, 4096) == 512
+    assert F(1024, 64, 32, 8, 128, RKV_BF16, 4096) == 1024
+    assert F(1024, 64, 32, 8, 128, RKV_F32, 4096) == RKV_ERR_UNSUPPORTED
+    # the thresholds: 1200 x 1280 and 1000 x 768 KV-head tokens (contexts
+    # taken as uniform up to max_context)
+    assert F(0, 1, 32, 8, 128, RKV_BF16, 384000) == 1280  # 8 * 192000 = 1.536M
+    assert F(0, 1, 32, 8, 128, RKV_BF16, 383999) == 768
+    assert F(0, 1, 32, 8, 128, RKV_BF16, 192000) == 768   # 8 * 96000 = 768k
+    assert F(0, 1, 32, 8, 128, RKV_BF16, 191999) == 640
+    # bf16 pools also take multiples of 128 up to 1280; the others do not
+    for req in (768, 896, 1024, 1280):
+        assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == req
+        for dt in (RKV_F32, RKV_I8, RKV_FP8):
+            assert L.rkv_decode_partition_size(req, 128, dt, 4096) == RKV_ERR_UNSUPPORTED
+    for req in (704, 832, 1408):
+        assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == RKV_ERR_UNSUPPORTED
     # a request is honoured when it is a multiple of 64 up to 640
     for req in (64, 128, 320, 512, 576, 640):
         assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == req
-    for req in (100, 704, 1024):
+    for req in (100, 704, 1400):
         assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == RKV_ERR_UNSUPPORTED
+    for req in (100, 704, 1024):
+        assert L.rkv_decode_partition_size(req, 128, RKV_F32, 4096) == RKV_ERR_UNSUPPORTED
 
 
 def test_copy_kernels_reject_bad_arguments():

@@ -280,3 +280,24 @@ def test_decode_caller_partition_sizes(dev, dtype, P):
     torch.cuda.synchronize()
     want = oracle.decode_attention(q, kp, vp, tables, ctx, scale)
     assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"partition {P} vs oracle")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 2, 128), (8, 8, 64), (8, 4, 32),
+                                      (64, 8, 128)])
+@pytest.mark.parametrize("P", [768, 896, 1024, 1280, 0])
+def test_decode_wide_partitions_bf16(dev, P, hq, hkv, d):
+    """bf16 pools: the 8-wave builds (768 and 1280 tokens; sizes between run
+    on the 1280-token build with the slots past the size masked) and the
+    default for the call's max_context give the oracle's result for every
+    group size and head dim, with contexts straddling partition and block
+    boundaries and a sequence long enough for many partitions."""
+    ctx = np.array([1, 127, 128, 129, 767, 768, 769, 1279, 1280, 1281, 2047, 4100, 9000, 0],
+                   np.int32)
+    say(f"decode wide partition_size={P} hq={hq} hkv={hkv} d={d}")
+    q, kp, vp, kf, vf, tables = case(P + hq + d, len(ctx), hq, hkv, d, ctx, "bf16")
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    out = kv.decode_attention(to_dev(q, dev), to_dev(kp, dev), to_dev(vp, dev), to_dev(tables, dev),
+                              to_dev(ctx, dev), scale, partition_size=P)
+    torch.cuda.synchronize()
+    want = oracle.decode_attention(q, kp, vp, tables, ctx, scale)
+    assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"wide partition {P} vs oracle")
