@@ -1285,16 +1285,16 @@ constexpr int split_of() { return sizeof(T) == 1 ? RKV_DECODE_SPLIT_Q : RKV_DECO
 // that a caller asking for 512-token partitions runs them without masked
 // slots; other sizes run on the smallest build that holds them, the extra
 // slots masked.
-// bf16 pools also have two builds of 8-wave workgroups (the same 160-token
-// slice per wave, twice the slices per workgroup): 768 tokens (6 tiles per
-// wave) and 1280 tokens (10 tiles per wave); requests that are multiples of
-// 128 above 640 run on them.  Measured in one process against the 4-wave
+// bf16 pools also have two builds of 8-wave workgroups: 768 tokens (a
+// 96-token slice, 6 tiles, per wave) and 1280 tokens (10 tiles per wave, the
+// 640-token build's slice); requests that are multiples of 128 above 640 run
+// on them.  Measured in one process against the 4-wave
 // 640-token build (us per call): configs[2] (64 sequences, contexts
 // U[512, 4096]) 109.0 -> 106.7 at 768 (122.8 at 1280: too few workgroups);
 // 256 x U[1, 8192] 769.3 -> 736.9 at 1280; 64 x U[8192, 16384] 547.0 ->
 // 526.5; 32 x U[12288, 24576] 403.4 -> 387.1; configs[3] (8 x U[16384,
 // 65536]) 221.2 -> 214.2.  Fewer partitions per sequence mean fewer split-K
-// partials and a cheaper merge; the number of waves is the same.
+// partials and a cheaper merge.
 // They pay off only with enough work: at 8 x U[512, 4096] 768 was 5% slower
 // than 640, at 4 x U[16384, 32768] 1280 was 10% slower, and for 8 query
 // heads per KV head (more registers, two waves per SIMD) both were slower
