@@ -833,7 +833,7 @@ def run_device_step(torch, dev, args):
     steps, warm = args.steps, args.warmup
     rng = np.random.default_rng(SEED)
     ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B).astype(np.int32)
-    grow = warm + steps + 1
+    grow = 3 * (warm + steps + 1)          # three step variants run one after the other
     mbs = (CTX_HI + grow + BS - 1) // BS
     nb = int(((ctx + grow + BS - 1) // BS).sum()) + 64
     g = torch.Generator(device=dev).manual_seed(SEED)
@@ -871,25 +871,68 @@ def run_device_step(torch, dev, args):
                                 out=outs[l], workspace=ws)
         lens.copy_(nlen)
 
+    def step_per_layer():
+        # a model's order: layer l's K/V exist only after layer l's
+        # projections, so each layer appends its own row, then attends
+        torch.add(lens, 1, out=nlen)
+        dbm.reserve(slots, nlen)
+        sm = dbm.slot_mapping(slots, lens)
+        tab = dbm.batch_tables(slots, mbs)
+        for l in range(n_layers):
+            kv.append(kpool[l], vpool[l], k_new[l], v_new[l], sm)
+            kv.decode_attention(q[l], kpool[l], vpool[l], tab, nlen, scale, max_context=max_ctx,
+                                out=outs[l], workspace=ws)
+        lens.copy_(nlen)
+
+    def step_fused():
+        # the same order with the append fused into each layer's decode
+        torch.add(lens, 1, out=nlen)
+        dbm.reserve(slots, nlen)
+        tab = dbm.batch_tables(slots, mbs)
+        for l in range(n_layers):
+            kv.decode_attention_append(q[l], kpool[l], vpool[l], k_new[l], v_new[l], tab, nlen,
+                                       scale, max_context=max_ctx, out=outs[l], workspace=ws)
+        lens.copy_(nlen)
+
     stream = torch.cuda.Stream(device=dev)
-    stream.wait_stream(torch.cuda.current_stream(dev))
-    torch.cuda.synchronize(dev)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(graph, stream=stream):
-            step()
-    torch.cuda.synchronize(dev)
-    lens.copy_(torch.as_tensor(ctx, dtype=torch.int32))  # the capture does not run the step
-    torch.cuda.synchronize(dev)
-    for _ in range(warm):
-        graph.replay()
-    ctx_mid = ctx + warm + 1 + steps // 2   # mean context over the timed steps
-    ms = _timed(torch, graph.replay, steps)
+    base = 0
+
+    def run_graph(fn):
+        nonlocal base
+        stream.wait_stream(torch.cuda.current_stream(dev))
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                fn()
+        torch.cuda.synchronize(dev)
+        lens.copy_(torch.as_tensor(ctx + base, dtype=torch.int32))  # the capture runs nothing
+        torch.cuda.synchronize(dev)
+        for _ in range(warm):
+            graph.replay()
+        mid = ctx + base + warm + 1 + steps // 2   # mean context over the timed steps
+        t = _timed(torch, graph.replay, steps)
+        base += warm + steps
+        del graph
+        return t, mid
+
+    ms, ctx_mid = run_graph(step)
+    ms_pl, ctx_pl = run_graph(step_per_layer)
+    ms_fu, ctx_fu = run_graph(step_fused)
     nf_end, err = dbm.status()
     assert err == 0, "device block manager reported an error during the bench"
     attn_bytes = algorithmic_bytes(ctx_mid) * n_layers
     app_bytes = n_layers * B * HKV * D * 2 * (4 + 2) + B * 8
     tok_s = B / (ms / 1e3)
+    variants = {
+        "per_layer_append_then_decode": {
+            "ms_per_step": round(ms_pl, 4), "tokens_per_s": round(B / (ms_pl / 1e3), 1),
+            "step_GBps": round((algorithmic_bytes(ctx_pl) * n_layers + app_bytes)
+                               / (ms_pl / 1e3) / 1e9, 1)},
+        "per_layer_fused_append_decode": {
+            "ms_per_step": round(ms_fu, 4), "tokens_per_s": round(B / (ms_fu / 1e3), 1),
+            "step_GBps": round((algorithmic_bytes(ctx_fu) * n_layers + app_bytes)
+                               / (ms_fu / 1e3) / 1e9, 1)}}
     dbm.close()
     return _line("decode step tokens/s at batch 64 with the KV cache managed on the device "
                  "(configs[2] shape, 32 layers)", tok_s, "tokens/s", ms, args, "bf16",
@@ -900,7 +943,7 @@ def run_device_step(torch, dev, args):
                           "32 decode calls, one HIP graph replay"},
                  step_GBps=round((attn_bytes + app_bytes) / (ms / 1e3) / 1e9, 1),
                  attention_bytes_per_step=attn_bytes, append_bytes_per_step=app_bytes,
-                 free_blocks_after=nf_end)
+                 free_blocks_after=nf_end, step_variants=variants)
 
 
 def run_ceilings(torch, dev, args):

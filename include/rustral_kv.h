@@ -156,6 +156,30 @@ int rkv_decode_attention(float* out, const float* q, const void* k_pool, const v
                          int max_context, float scale, int dtype, int partition_size,
                          void* workspace, size_t workspace_bytes, void* stream);
 
+/* One decode step's K/V append fused into rkv_decode_attention (RKV_BF16
+ * pools only, else RKV_ERR_UNSUPPORTED).  Replaces the pair a decode step
+ * makes per layer, KVCache::append (crates/nn/src/kv_cache.rs:172-216) of the
+ * step's one token, then the attention over the cache
+ * (crates/nn/src/tape_transformer.rs:87-139).  ctx_lens[b] already counts
+ * the new token: its K/V rows k_new/v_new [num_seqs][num_kv_heads][head_dim]
+ * fp32 (16-byte aligned) go to position ctx_lens[b] - 1, i.e. slot
+ * block_tables[b][(L-1)/16]*16 + (L-1)%16, rounded to bf16 as rkv_append
+ * rounds them; a block id outside [0, num_blocks) is not written, nor is the
+ * row of a sequence whose ctx_lens[b] exceeds the context cap (max_context,
+ * max_blocks_per_seq*block_size).  Pools and out afterwards equal rkv_append
+ * of those rows followed by rkv_decode_attention, bit for bit.  The new
+ * token's block must not be shared with another sequence of the call (a
+ * block being appended to is never shared in a copy-on-write cache).  Other
+ * arguments as rkv_decode_attention. */
+int rkv_decode_attention_append(float* out, const float* q, void* k_pool, void* v_pool,
+                                const float* k_new, const float* v_new,
+                                const int32_t* block_tables, int max_blocks_per_seq,
+                                const int32_t* ctx_lens, int num_seqs, int num_q_heads,
+                                int num_kv_heads, int head_dim, int block_size,
+                                int64_t num_blocks, int max_context, float scale, int dtype,
+                                int partition_size, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
 /* rkv_decode_attention without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference: its

@@ -29,6 +29,8 @@ SIGNATURES = {
     "rkv_decode_partition_size_for": (_i, [_i, _i, _i, _i, _i, _i, _i]),
     "rkv_decode_attention": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64, _i, _f,
                                   _i, _i, _p, _sz, _p]),
+    "rkv_decode_attention_append": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i,
+                                         _i64, _i, _f, _i, _i, _p, _sz, _p]),
     "rkv_decode_attention_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,
                                           _i, _f, _i, _i, _p]),
     "rkv_decode_noalloc_max_bytes": (_sz, []),

@@ -211,7 +211,14 @@ __device__ __forceinline__ float lo_col(float x) {
 #ifndef RKV_DECODE_I8_PV
 #define RKV_DECODE_I8_PV 1
 #endif
-template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT>
+// APPEND (bf16 pools): the step's new K/V rows (k_new / v_new, fp32
+// [num_seqs][Hkv][D]) belong at position ctx_lens[b] - 1.  The wave whose
+// slice holds that position stores them (bf16, rounded to nearest even as
+// rkv_append does) into the pools before it streams its tiles, and reads
+// them back with the rest of the tile.  Nothing else in the launch reads
+// the row.
+template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT,
+          bool APPEND = false>
 __global__ __launch_bounds__(64 * SPLIT)
 __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stream_kernel(
     float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
@@ -219,7 +226,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     const void* __restrict__ v_pool_, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens, int ctx_cap, int num_kv_heads,
-    int64_t num_blocks, float q_scale, int max_parts, int tiles_per_wave) {
+    int64_t num_blocks, float q_scale, int max_parts, int tiles_per_wave,
+    const float* __restrict__ k_new, const float* __restrict__ v_new) {
   const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
   const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
   constexpr int E = Traits<T>::E;
@@ -256,6 +264,7 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 
   // Requests that do not depend on the context length go out first.
   int L = ctx_lens[b];
+  const int L_raw = L;
   const int lb0 = (part * SPLIT + sub) * tw;  // first tile (block index) of this wave
   const int32_t* tab = block_tables + (int64_t)b * max_blocks_per_seq;
   int32_t pb[NTW];
@@ -403,6 +412,37 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     return load_stream(reinterpret_cast<const char*>((is_k ? k_pool : v_pool) + base[i]) +
                        (is_k ? koff : voff) + n * (is_k ? KSTEP : VSTEP));
   };
+
+  // APPEND: the wave whose slice holds position L - 1 stores the new K and V
+  // rows (bf16) into the pools before its ring loads and waits for the
+  // stores; the lanes that store a row piece are the lanes whose ring load
+  // reads it back (row n TPL + slot, piece dl), so the loop sees the new row
+  // with no other change.  The stores wait only in this one wave of the
+  // sequence's last partition.  A block id outside the pool (rkv_append
+  // skips those slots) or a length clamped to ctx_cap stores nothing.
+  static_assert(!APPEND || sizeof(T) == 2, "the fused append is for bf16 pools");
+  if constexpr (APPEND) {
+    const int tn = L - 1, ti = tn / BS;
+    if (L_raw == L && ti >= lb0 && ti < lb0 + tw) {  // wave-uniform
+      const int r = tn - ti * BS;
+      const int32_t blk = tab[ti];
+      if ((uint32_t)blk < nb32 && slot == r % TPL) {
+        const int64_t src = ((int64_t)b * num_kv_heads + kh) * D + dl * E;
+        const int64_t dst = (((int64_t)blk * num_kv_heads + kh) * BS + r) * D + dl * E;
+        const float4 k0 = *reinterpret_cast<const float4*>(k_new + src);
+        const float4 k1 = *reinterpret_cast<const float4*>(k_new + src + 4);
+        const float4 v0 = *reinterpret_cast<const float4*>(v_new + src);
+        const float4 v1 = *reinterpret_cast<const float4*>(v_new + src + 4);
+        *reinterpret_cast<uint4*>(const_cast<T*>(k_pool) + dst) =
+            make_uint4(pack_bf16x2(k0.x, k0.y), pack_bf16x2(k0.z, k0.w),
+                       pack_bf16x2(k1.x, k1.y), pack_bf16x2(k1.z, k1.w));
+        *reinterpret_cast<uint4*>(const_cast<T*>(v_pool) + dst) =
+            make_uint4(pack_bf16x2(v0.x, v0.y), pack_bf16x2(v0.z, v0.w),
+                       pack_bf16x2(v1.x, v1.y), pack_bf16x2(v1.z, v1.w));
+      }
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the stores are done in L2
+    }
+  }
 
   const int tok0 = lb0 * BS;  // first token of this wave's slice
   float acc[G][E];
@@ -1351,7 +1391,7 @@ struct Launch {
   int nw = 0;
   void (*kernel)(float*, float*, float*, const float*, const void*, const void*, const float*,
                  const float*, const int32_t*, int, const int32_t*, int, int, int64_t, float,
-                 int, int) = nullptr;
+                 int, int, const float*, const float*) = nullptr;
 };
 
 // Ring depth: RKV_DECODE_RING_LOADS 16-byte loads per lane in flight, at most
@@ -1365,9 +1405,18 @@ constexpr int ring_for() {
 }
 
 template <typename T, int D, int G, int FMT, int NTILE, int SPLIT = split_of<T>()>
-Launch make_launch() {
+Launch make_launch(bool append) {
   Launch l;
   l.nw = SPLIT;
+  if constexpr (FMT == RKV_BF16) {  // the fused append is built for bf16 pools only
+    if (append) {
+      l.kernel = &decode_stream_kernel<T, D, G, kBS, NTILE, ring_for<T, D, NTILE, SPLIT>(),
+                                       SPLIT, FMT, true>;
+      return l;
+    }
+  } else if (append) {
+    return Launch{};
+  }
   l.kernel = &decode_stream_kernel<T, D, G, kBS, NTILE, ring_for<T, D, NTILE, SPLIT>(), SPLIT,
                                    FMT>;
   return l;
@@ -1377,49 +1426,49 @@ Launch make_launch() {
 // pools), the smallest 8-wave build that holds them; else the 512-token
 // build when it holds them (16-bit and fp32 pools), else the largest.
 template <typename T, int D, int G, int FMT>
-Launch pick_p(int P) {
+Launch pick_p(int P, bool append) {
   if constexpr (FMT == RKV_BF16) {
     if (P > kP) {
-      if (P <= kWideP1) return make_launch<T, D, G, FMT, kWideP1 / kBS, kWideSplit>();
-      return make_launch<T, D, G, FMT, kWideP2 / kBS, kWideSplit>();
+      if (P <= kWideP1) return make_launch<T, D, G, FMT, kWideP1 / kBS, kWideSplit>(append);
+      return make_launch<T, D, G, FMT, kWideP2 / kBS, kWideSplit>(append);
     }
   }
   if constexpr (sizeof(T) != 1 && kSmallP < kP) {
-    if (P <= kSmallP) return make_launch<T, D, G, FMT, kSmallP / kBS>();
+    if (P <= kSmallP) return make_launch<T, D, G, FMT, kSmallP / kBS>(append);
   }
-  return make_launch<T, D, G, FMT, part_of<T>() / kBS>();
+  return make_launch<T, D, G, FMT, part_of<T>() / kBS>(append);
 }
 
 template <typename T, int D, int FMT>
-Launch pick_g(int G, int P) {
+Launch pick_g(int G, int P, bool append) {
   switch (G) {
-    case 1: return pick_p<T, D, 1, FMT>(P);
-    case 2: return pick_p<T, D, 2, FMT>(P);
-    case 4: return pick_p<T, D, 4, FMT>(P);
-    case 8: return pick_p<T, D, 8, FMT>(P);
+    case 1: return pick_p<T, D, 1, FMT>(P, append);
+    case 2: return pick_p<T, D, 2, FMT>(P, append);
+    case 4: return pick_p<T, D, 4, FMT>(P, append);
+    case 8: return pick_p<T, D, 8, FMT>(P, append);
     default: return Launch{};
   }
 }
 
 // 16-bit and fp32 pools: head_dim 32, 64, 128; 1-byte pools: 64, 128.
 template <typename T, int FMT>
-Launch pick_d(int D, int G, int P) {
+Launch pick_d(int D, int G, int P, bool append) {
   switch (D) {
     case 32:
       if constexpr (sizeof(T) == 1) return Launch{};
-      else return pick_g<T, 32, FMT>(G, P);
-    case 64: return pick_g<T, 64, FMT>(G, P);
-    case 128: return pick_g<T, 128, FMT>(G, P);
+      else return pick_g<T, 32, FMT>(G, P, append);
+    case 64: return pick_g<T, 64, FMT>(G, P, append);
+    case 128: return pick_g<T, 128, FMT>(G, P, append);
     default: return Launch{};
   }
 }
 
-Launch pick(int dtype, int D, int G, int P) {
+Launch pick(int dtype, int D, int G, int P, bool append) {
   switch (dtype) {
-    case RKV_F32: return pick_d<float, RKV_F32>(D, G, P);
-    case RKV_BF16: return pick_d<uint16_t, RKV_BF16>(D, G, P);
-    case RKV_I8: return pick_d<uint8_t, RKV_I8>(D, G, P);
-    case RKV_FP8: return pick_d<uint8_t, RKV_FP8>(D, G, P);
+    case RKV_F32: return pick_d<float, RKV_F32>(D, G, P, append);
+    case RKV_BF16: return pick_d<uint16_t, RKV_BF16>(D, G, P, append);
+    case RKV_I8: return pick_d<uint8_t, RKV_I8>(D, G, P, append);
+    case RKV_FP8: return pick_d<uint8_t, RKV_FP8>(D, G, P, append);
     default: return Launch{};
   }
 }
@@ -1442,6 +1491,8 @@ struct DecodeArgs {
   hipStream_t stream;
   const float* k_scale = nullptr;  // 1-byte pools: [num_blocks][Hkv][block_size] fp32
   const float* v_scale = nullptr;
+  const float* k_new = nullptr;  // fused append (bf16 pools): [num_seqs][Hkv][D] fp32
+  const float* v_new = nullptr;
 };
 
 size_t ws_bytes(int B, int Hq, int D, int max_parts) {
@@ -1512,7 +1563,7 @@ void split_ws(void* ws, int B, int Hq, int D, int max_parts, float*& acc, float*
 int launch_partitions(const DecodeArgs& a, int max_parts, int P) {
   const int G = a.num_q_heads / a.num_kv_heads;
 
-  Launch l = pick(a.dtype, a.head_dim, G, P);
+  Launch l = pick(a.dtype, a.head_dim, G, P, a.k_new != nullptr);
   if (!l.kernel) return fail(RKV_ERR_UNSUPPORTED, "no decode kernel for this shape");
   float *acc = nullptr, *ml = nullptr;
   if (max_parts > 1) split_ws(a.workspace, a.num_seqs, a.num_q_heads, a.head_dim, max_parts, acc, ml);
@@ -1524,7 +1575,7 @@ int launch_partitions(const DecodeArgs& a, int max_parts, int P) {
                      a.v_pool, a.k_scale, a.v_scale, a.block_tables, a.max_blocks_per_seq,
                      a.ctx_lens, cap,
                      a.num_kv_heads, a.num_blocks, a.scale * kLog2e, max_parts,
-                     P / (kBS * l.nw));
+                     P / (kBS * l.nw), a.k_new, a.v_new);
   return check_launch("decode_stream_kernel");
 }
 
@@ -1688,6 +1739,44 @@ extern "C" int rkv_decode_attention(float* out, const float* q, const void* k_po
   return rkv_decode_attention_merge(out, ctx_lens, max_blocks_per_seq, num_seqs, num_q_heads,
                                     head_dim, block_size, max_context, dtype, P, workspace,
                                     workspace_bytes, stream);
+}
+
+// Decode with the step's K/V append fused in (bf16 pools).  The partition
+// that holds position ctx_lens[b] - 1 stores the rounded new row into the
+// pools and stages the same bits in place of the pool's old row, so the
+// result equals rkv_append of those rows followed by rkv_decode_attention,
+// bit for bit, in one launch fewer and without reading the row back.
+extern "C" int rkv_decode_attention_append(
+    float* out, const float* q, void* k_pool, void* v_pool, const float* k_new,
+    const float* v_new, const int32_t* block_tables, int max_blocks_per_seq,
+    const int32_t* ctx_lens, int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int64_t num_blocks, int max_context, float scale, int dtype,
+    int partition_size, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, "rkv_decode_attention_append: RKV_BF16 pools only");
+  if (num_seqs > 0 && (!k_new || !v_new))
+    return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (num_seqs > 0 && (!aligned16(k_new) || !aligned16(v_new)))
+    return fail(RKV_ERR_INVALID_ARG, "k_new and v_new must be 16-byte aligned");
+  const int P =
+      partition_size > 0
+          ? partition_size
+          : shape_part(dtype, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                       ctx_cap_of(max_context < 0 ? 0 : max_context,
+                                  max_blocks_per_seq < 0 ? 0 : max_blocks_per_seq, block_size));
+  DecodeArgs a{out, q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens, num_seqs,
+               num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context, scale,
+               dtype, P, workspace, workspace_bytes, static_cast<hipStream_t>(stream)};
+  a.k_new = k_new;
+  a.v_new = v_new;
+  int max_parts = 1, P2 = 0;
+  if (int rc = validate(a, max_parts, P2)) return rc;
+  if (num_seqs == 0) return RKV_OK;
+  if (int rc = launch_partitions(a, max_parts, P2)) return rc;
+  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim,
+                      ctx_cap_of(max_context, max_blocks_per_seq, block_size), P2, max_parts,
+                      workspace, a.stream);
 }
 
 // ---- the entry point that allocates nothing -----------------------------------

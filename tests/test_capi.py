@@ -176,3 +176,31 @@ def test_noalloc_decode_refuses_partials_above_its_scratch():
     rc = L.rkv_decode_attention_noalloc(16, 16, 16, 16, 16, 256, 16, 4096, 32, 8, 128, 16, 10,
                                         4096, 0.1, RKV_BF16, 0, None)
     assert rc == RKV_ERR_WORKSPACE and b"16 MiB" in L.rkv_last_error()
+
+
+def _decode_append(**kw):
+    a = dict(out=16, q=16, k=16, v=16, kn=16, vn=16, bt=16, mbs=4, cl=16, B=2, hq=8, hkv=2,
+             d=128, bs=16, nb=10, maxc=64, scale=0.1, dt=RKV_BF16, ps=0, ws=None, wsb=0, s=None)
+    a.update(kw)
+    return _lib.lib().rkv_decode_attention_append(
+        a["out"], a["q"], a["k"], a["v"], a["kn"], a["vn"], a["bt"], a["mbs"], a["cl"], a["B"],
+        a["hq"], a["hkv"], a["d"], a["bs"], a["nb"], a["maxc"], a["scale"], a["dt"], a["ps"],
+        a["ws"], a["wsb"], a["s"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dt=RKV_F32), RKV_ERR_UNSUPPORTED),     # fused append: bf16 pools only
+    (dict(dt=RKV_I8), RKV_ERR_UNSUPPORTED),
+    (dict(kn=None), RKV_ERR_INVALID_ARG),
+    (dict(vn=8), RKV_ERR_INVALID_ARG),           # misaligned
+    (dict(d=48), RKV_ERR_UNSUPPORTED),
+    (dict(maxc=1000, mbs=100), RKV_ERR_WORKSPACE),
+    (dict(ps=100), RKV_ERR_UNSUPPORTED),
+])
+def test_decode_append_rejects_bad_arguments(kw, code):
+    assert _decode_append(**kw) == code
+    assert _lib.lib().rkv_last_error().decode()
+
+
+def test_decode_append_zero_sequences_is_a_no_op():
+    assert _decode_append(B=0, kn=None, vn=None, out=None, q=None) == 0

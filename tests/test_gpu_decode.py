@@ -301,3 +301,52 @@ def test_decode_wide_partitions_bf16(dev, P, hq, hkv, d):
     torch.cuda.synchronize()
     want = oracle.decode_attention(q, kp, vp, tables, ctx, scale)
     assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"wide partition {P} vs oracle")
+
+
+@pytest.mark.parametrize("max_context", [None, 1000])
+@pytest.mark.parametrize("P", [0, 256, 640, 768, 1280])
+@pytest.mark.parametrize("hq,hkv,d", [(4, 4, 32), (8, 4, 64), (32, 8, 128), (8, 1, 128),
+                                      (16, 2, 128)])
+def test_decode_append_fused_matches_append_then_decode(dev, max_context, P, hq, hkv, d):
+    """rkv_decode_attention_append == rkv_append of the new rows followed by
+    rkv_decode_attention, bit for bit in the pools and the output: new tokens
+    at the first row of a block, mid-block and at the last row, at partition
+    boundaries of every build, a sequence whose new block id is invalid (-1
+    and past the pool: nothing written, the tile masked), an empty sequence,
+    and (max_context 1000) sequences clamped below their length, whose rows
+    are not written.  P == 0 is also checked against the oracle on the
+    appended pool."""
+    bs = 16
+    ctx = np.array([1, 2, 16, 17, 640, 641, 768, 769, 1280, 1281, 4100, 0, 40, 50, 33],
+                   np.int32)
+    say(f"decode append fused P={P} hq={hq} hkv={hkv} d={d} max_context={max_context}")
+    q, kp, vp, kf, vf, tables = case(7 * P + hq + d, len(ctx), hq, hkv, d, ctx, "bf16")
+    nb = kp.shape[0]
+    tables[12, (40 - 1) // bs] = -1          # the new token's block: not a block
+    tables[13, (50 - 1) // bs] = nb + 3      # past the pool
+    rng = np.random.default_rng(P + d)
+    kn = rng.standard_normal((len(ctx), hkv, d)).astype(np.float32)
+    vn = rng.standard_normal((len(ctx), hkv, d)).astype(np.float32)
+    cap = min(max_context if max_context is not None else 1 << 30, tables.shape[1] * bs)
+    slots = np.full(len(ctx), -1, np.int64)
+    for b, L in enumerate(ctx):
+        if 0 < L <= cap:
+            blk = int(tables[b, (L - 1) // bs])
+            slots[b] = blk * bs + (L - 1) % bs if 0 <= blk < nb else -1
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    qd, td, cd = to_dev(q, dev), to_dev(tables, dev), to_dev(ctx, dev)
+    knd, vnd = to_dev(kn, dev), to_dev(vn, dev)
+    k1, v1 = to_dev(kp, dev), to_dev(vp, dev)
+    k2, v2 = k1.clone(), v1.clone()
+    kv.append(k1, v1, knd, vnd, to_dev(slots, dev))
+    want = kv.decode_attention(qd, k1, v1, td, cd, scale, max_context=max_context,
+                               partition_size=P)
+    got = kv.decode_attention_append(qd, k2, v2, knd, vnd, td, cd, scale,
+                                     max_context=max_context, partition_size=P)
+    torch.cuda.synchronize()
+    assert torch.equal(k2.view(torch.int16), k1.view(torch.int16)), "K pool differs"
+    assert torch.equal(v2.view(torch.int16), v1.view(torch.int16)), "V pool differs"
+    assert torch.equal(got, want), f"max diff {(got - want).abs().max().item()}"
+    if P == 0 and max_context is None:
+        ref = oracle.decode_attention(q, to_np(k1), to_np(v1), tables, ctx, scale)
+        assert_allclose_ref(to_np(got), ref, RTOL, ATOL, "fused append vs oracle")
