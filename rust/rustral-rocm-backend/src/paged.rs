@@ -291,6 +291,56 @@ impl RocmPagedKvCache {
         Ok(out)
     }
 
+    /// One decode step of layer `layer` with its K/V append fused in (bf16
+    /// pools): `ctx_lens` already counts the new token, whose rows `k_new` /
+    /// `v_new` `[B, Hkv, D]` f32 go to position `ctx_lens[b] - 1`.  Equals
+    /// `append` of those rows followed by `decode_attention`, in one launch
+    /// (`KVCache::append`, crates/nn/src/kv_cache.rs:172-216, then the
+    /// attention of crates/nn/src/tape_transformer.rs:87-139).
+    pub fn decode_attention_append(&self, layer: usize, q: &RocmTensor, k_new: &RocmTensor, v_new: &RocmTensor,
+                                   block_tables: &RocmTensor, ctx_lens: &RocmTensor, max_context: usize,
+                                   scale: f32) -> Result<RocmTensor> {
+        if self.cfg.dtype != KvDtype::Bf16 {
+            return Err(CoreError::InvalidArgument("the fused append + decode needs a bf16 pool".into()));
+        }
+        q.expect(DType::F32, 3, "q")?;
+        k_new.expect(DType::F32, 3, "k_new")?;
+        v_new.expect(DType::F32, 3, "v_new")?;
+        block_tables.expect(DType::I32, 2, "block_tables")?;
+        ctx_lens.expect(DType::I32, 1, "ctx_lens")?;
+        let (b, hq, d) = (q.shape[0], q.shape[1], q.shape[2]);
+        let rows = [b, self.cfg.num_kv_heads, d];
+        for t in [k_new, v_new] {
+            if t.shape[..] != rows[..] {
+                return Err(CoreError::ShapeMismatch { expected: rows.to_vec(), actual: t.shape.clone() });
+            }
+        }
+        let mb = block_tables.shape[1];
+        let need = unsafe {
+            // SAFETY: pure size computation in the library.
+            ffi::rkv_decode_workspace_bytes(ci(b, "B")?, ci(hq, "Hq")?, ci(d, "D")?, ci(max_context, "max_context")?, 0)
+        };
+        let mut ws = self.ws.lock().map_err(|_| CoreError::Backend("workspace lock poisoned".into()))?;
+        if ws.bytes() < need {
+            self.ctx.synchronize()?;
+            *ws = DeviceBuffer::new(need)?;
+        }
+        let out = RocmTensor::empty(&self.ctx, &q.shape, DType::F32)?;
+        let (kp, vp) = (self.layer_ptr(&self.k, layer)?, self.layer_ptr(&self.v, layer)?);
+        // SAFETY: live buffers of the checked shapes; the workspace holds `need` bytes.
+        let rc = unsafe {
+            ffi::rkv_decode_attention_append(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
+                                             k_new.device_ptr() as *const f32, v_new.device_ptr() as *const f32,
+                                             block_tables.device_ptr() as *const i32, ci(mb, "max_blocks")?,
+                                             ctx_lens.device_ptr() as *const i32, ci(b, "B")?, ci(hq, "Hq")?,
+                                             ci(self.cfg.num_kv_heads, "Hkv")?, ci(d, "D")?, BLOCK_SIZE as i32,
+                                             self.cfg.num_blocks as i64, ci(max_context, "max_context")?, scale,
+                                             ffi::RKV_BF16, 0, ws.ptr(), ws.bytes(), self.ctx.stream)
+        };
+        check(rc)?;
+        Ok(out)
+    }
+
     /// Causal prefill of new tokens already appended: sequence b's query rows
     /// `q_start[b]..q_start[b+1]` are its last tokens and attend to every
     /// cached position up to their own (`forward_tape_with_mask` with
