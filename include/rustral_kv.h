@@ -157,7 +157,7 @@ int rkv_decode_attention(float* out, const float* q, const void* k_pool, const v
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* One decode step's K/V append fused into rkv_decode_attention (RKV_BF16
- * pools only, else RKV_ERR_UNSUPPORTED).  Replaces the pair a decode step
+ * pools, else RKV_ERR_UNSUPPORTED; 1-byte pools: rkv_decode_attention_append_q).  Replaces the pair a decode step
  * makes per layer, KVCache::append (crates/nn/src/kv_cache.rs:172-216) of the
  * step's one token, then the attention over the cache
  * (crates/nn/src/tape_transformer.rs:87-139).  ctx_lens[b] already counts
@@ -268,6 +268,23 @@ int rkv_decode_attention_q(float* out, const float* q, const void* k_pool, const
                            int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
                            int max_context, float scale, int dtype, int partition_size,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* rkv_decode_attention_append for 1-byte pools (RKV_I8 / RKV_FP8): the new
+ * rows are quantized as rkv_append_q quantizes them (bytes and row scale);
+ * pools, scale pools and out equal rkv_append_q followed by
+ * rkv_decode_attention_q, bit for bit.  Replaces the same pair of reference
+ * calls as rkv_decode_attention_append (crates/nn/src/kv_cache.rs:172-216,
+ * crates/nn/src/tape_transformer.rs:87-139) for a cache whose
+ * CacheConfig::quantization (kv_cache.rs:38-63) is Int8 or Fp8.  Other
+ * arguments as rkv_decode_attention_q. */
+int rkv_decode_attention_append_q(float* out, const float* q, void* k_pool, void* v_pool,
+                                  float* k_scale, float* v_scale, const float* k_new,
+                                  const float* v_new, const int32_t* block_tables,
+                                  int max_blocks_per_seq, const int32_t* ctx_lens, int num_seqs,
+                                  int num_q_heads, int num_kv_heads, int head_dim,
+                                  int block_size, int64_t num_blocks, int max_context,
+                                  float scale, int dtype, int partition_size, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 
 /* Causal prefill attention over the paged pool (many new query tokens per
  * sequence).  Sequence b owns query rows q_start[b] .. q_start[b+1]-1 of q

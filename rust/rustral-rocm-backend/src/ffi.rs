@@ -319,6 +319,32 @@ extern "C" {
         workspace_bytes: usize,
         stream: Stream,
     ) -> c_int;
+    pub fn rkv_decode_attention_append_q(
+        out: *mut f32,
+        q: *const f32,
+        k_pool: *mut c_void,
+        v_pool: *mut c_void,
+        k_scale: *mut f32,
+        v_scale: *mut f32,
+        k_new: *const f32,
+        v_new: *const f32,
+        block_tables: *const i32,
+        max_blocks_per_seq: c_int,
+        ctx_lens: *const i32,
+        num_seqs: c_int,
+        num_q_heads: c_int,
+        num_kv_heads: c_int,
+        head_dim: c_int,
+        block_size: c_int,
+        num_blocks: i64,
+        max_context: c_int,
+        scale: f32,
+        dtype: c_int,
+        partition_size: c_int,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        stream: Stream,
+    ) -> c_int;
     pub fn rkv_prefill_attention(
         out: *mut f32,
         q: *const f32,

@@ -291,17 +291,18 @@ impl RocmPagedKvCache {
         Ok(out)
     }
 
-    /// One decode step of layer `layer` with its K/V append fused in (bf16
-    /// pools): `ctx_lens` already counts the new token, whose rows `k_new` /
-    /// `v_new` `[B, Hkv, D]` f32 go to position `ctx_lens[b] - 1`.  Equals
+    /// One decode step of layer `layer` with its K/V append fused in:
+    /// `ctx_lens` already counts the new token, whose rows `k_new` / `v_new`
+    /// `[B, Hkv, D]` f32 go to position `ctx_lens[b] - 1` (bf16 pools
+    /// rounded, 1-byte pools quantized with their row scale).  Equals
     /// `append` of those rows followed by `decode_attention`, in one launch
     /// (`KVCache::append`, crates/nn/src/kv_cache.rs:172-216, then the
     /// attention of crates/nn/src/tape_transformer.rs:87-139).
     pub fn decode_attention_append(&self, layer: usize, q: &RocmTensor, k_new: &RocmTensor, v_new: &RocmTensor,
                                    block_tables: &RocmTensor, ctx_lens: &RocmTensor, max_context: usize,
                                    scale: f32) -> Result<RocmTensor> {
-        if self.cfg.dtype != KvDtype::Bf16 {
-            return Err(CoreError::InvalidArgument("the fused append + decode needs a bf16 pool".into()));
+        if self.cfg.dtype == KvDtype::F32 {
+            return Err(CoreError::InvalidArgument("the fused append + decode needs a bf16 or 1-byte pool".into()));
         }
         q.expect(DType::F32, 3, "q")?;
         k_new.expect(DType::F32, 3, "k_new")?;
@@ -329,13 +330,25 @@ impl RocmPagedKvCache {
         let (kp, vp) = (self.layer_ptr(&self.k, layer)?, self.layer_ptr(&self.v, layer)?);
         // SAFETY: live buffers of the checked shapes; the workspace holds `need` bytes.
         let rc = unsafe {
-            ffi::rkv_decode_attention_append(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
-                                             k_new.device_ptr() as *const f32, v_new.device_ptr() as *const f32,
-                                             block_tables.device_ptr() as *const i32, ci(mb, "max_blocks")?,
-                                             ctx_lens.device_ptr() as *const i32, ci(b, "B")?, ci(hq, "Hq")?,
-                                             ci(self.cfg.num_kv_heads, "Hkv")?, ci(d, "D")?, BLOCK_SIZE as i32,
-                                             self.cfg.num_blocks as i64, ci(max_context, "max_context")?, scale,
-                                             ffi::RKV_BF16, 0, ws.ptr(), ws.bytes(), self.ctx.stream)
+            if self.cfg.dtype.one_byte() {
+                ffi::rkv_decode_attention_append_q(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
+                                                   self.scale_ptr(&self.k_scale, layer),
+                                                   self.scale_ptr(&self.v_scale, layer),
+                                                   k_new.device_ptr() as *const f32, v_new.device_ptr() as *const f32,
+                                                   block_tables.device_ptr() as *const i32, ci(mb, "max_blocks")?,
+                                                   ctx_lens.device_ptr() as *const i32, ci(b, "B")?, ci(hq, "Hq")?,
+                                                   ci(self.cfg.num_kv_heads, "Hkv")?, ci(d, "D")?, BLOCK_SIZE as i32,
+                                                   self.cfg.num_blocks as i64, ci(max_context, "max_context")?, scale,
+                                                   self.cfg.dtype.code(), 0, ws.ptr(), ws.bytes(), self.ctx.stream)
+            } else {
+                ffi::rkv_decode_attention_append(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
+                                                 k_new.device_ptr() as *const f32, v_new.device_ptr() as *const f32,
+                                                 block_tables.device_ptr() as *const i32, ci(mb, "max_blocks")?,
+                                                 ctx_lens.device_ptr() as *const i32, ci(b, "B")?, ci(hq, "Hq")?,
+                                                 ci(self.cfg.num_kv_heads, "Hkv")?, ci(d, "D")?, BLOCK_SIZE as i32,
+                                                 self.cfg.num_blocks as i64, ci(max_context, "max_context")?, scale,
+                                                 ffi::RKV_BF16, 0, ws.ptr(), ws.bytes(), self.ctx.stream)
+            }
         };
         check(rc)?;
         Ok(out)

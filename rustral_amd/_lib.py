@@ -45,6 +45,8 @@ SIGNATURES = {
                           _p]),
     "rkv_decode_attention_q": (_i, [_p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i64,
                                     _i, _f, _i, _i, _p, _sz, _p]),
+    "rkv_decode_attention_append_q": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _i, _i,
+                                           _i, _i, _i, _i64, _i, _f, _i, _i, _p, _sz, _p]),
     # include/rustral_serving.h (host memory)
     "rkv_dbm_create": (_p, [_i64, _i, _i, _i, _p]),
     "rkv_dbm_destroy": (None, [_p]),

@@ -420,8 +420,55 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // with no other change.  The stores wait only in this one wave of the
   // sequence's last partition.  A block id outside the pool (rkv_append
   // skips those slots) or a length clamped to ctx_cap stores nothing.
-  static_assert(!APPEND || sizeof(T) == 2, "the fused append is for bf16 pools");
-  if constexpr (APPEND) {
+  static_assert(!APPEND || sizeof(T) == 2 || QNT, "the fused append: bf16 and 1-byte pools");
+  if constexpr (APPEND && QNT) {
+    // 1-byte pools: rkv_append_q's quantization of the row (maximum |x| of
+    // the row over its LPT lanes, bytes of x * top / max, scale max / top)
+    const int tn = L - 1, ti = tn / BS;
+    if (L_raw == L && ti >= lb0 && ti < lb0 + tw) {  // wave-uniform
+      const int r = tn - ti * BS;
+      const int32_t blk = tab[ti];
+      if ((uint32_t)blk < nb32 && slot == r % TPL) {  // whole LPT-lane groups
+        constexpr float kTop = FMT == RKV_I8 ? 127.0f : 448.0f;
+        const int64_t src = ((int64_t)b * num_kv_heads + kh) * D + dl * E;
+        const int64_t row = ((int64_t)blk * num_kv_heads + kh) * BS + r;
+        float kx[E], vx[E];
+#pragma unroll
+        for (int e = 0; e < E; e += 4) {
+          const float4 k4 = *reinterpret_cast<const float4*>(k_new + src + e);
+          const float4 v4 = *reinterpret_cast<const float4*>(v_new + src + e);
+          kx[e] = k4.x, kx[e + 1] = k4.y, kx[e + 2] = k4.z, kx[e + 3] = k4.w;
+          vx[e] = v4.x, vx[e + 1] = v4.y, vx[e + 2] = v4.z, vx[e + 3] = v4.w;
+        }
+        float ka = 0.0f, va = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          ka = fmaxf(ka, fabsf(kx[e]));
+          va = fmaxf(va, fabsf(vx[e]));
+        }
+        ka = group_max<LPT>(ka);
+        va = group_max<LPT>(va);
+        const float kinv = ka > 0.0f ? kTop / ka : 0.0f, vinv = va > 0.0f ? kTop / va : 0.0f;
+        uint32_t kw[4] = {0u, 0u, 0u, 0u}, vw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const uint32_t kb = FMT == RKV_I8 ? i8_quant(kx[e], kinv) : e4m3_from_f32(kx[e] * kinv);
+          const uint32_t vb = FMT == RKV_I8 ? i8_quant(vx[e], vinv) : e4m3_from_f32(vx[e] * vinv);
+          kw[e >> 2] |= kb << (8 * (e & 3));
+          vw[e >> 2] |= vb << (8 * (e & 3));
+        }
+        *reinterpret_cast<uint4*>(const_cast<T*>(k_pool) + row * D + dl * E) =
+            make_uint4(kw[0], kw[1], kw[2], kw[3]);
+        *reinterpret_cast<uint4*>(const_cast<T*>(v_pool) + row * D + dl * E) =
+            make_uint4(vw[0], vw[1], vw[2], vw[3]);
+        if (dl == 0) {
+          const_cast<float*>(k_scale)[row] = ka / kTop;
+          const_cast<float*>(v_scale)[row] = va / kTop;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the stores are done in L2
+    }
+  } else if constexpr (APPEND) {
     const int tn = L - 1, ti = tn / BS;
     if (L_raw == L && ti >= lb0 && ti < lb0 + tw) {  // wave-uniform
       const int r = tn - ti * BS;
@@ -457,18 +504,25 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // 1-byte pools: the K scale of this lane's token in each K tile (MFMA column
   // kt), and the V scale of the tokens this lane folds into the
   // probabilities (x = lane + 64 j of the slice).  Issued with the ring loads.
+  // APPEND: a scale the wave stored is read by other lanes, and a 128-byte
+  // line of scales spans two KV heads' tiles, which another workgroup on the
+  // CU may have cached in L1: these loads read L2.
   constexpr int NX = QNT ? (NTW * BS + 63) / 64 : 1;
   float ksc[QNT ? NTW : 1], vsc[NX];
+  auto ld_scale = [](const float* p) __attribute__((always_inline)) {
+    if constexpr (APPEND) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+  };
   if constexpr (QNT) {
 #pragma unroll
-    for (int i = 0; i < NTW; ++i) ksc[i] = k_scale[base[i] / D + kt];
+    for (int i = 0; i < NTW; ++i) ksc[i] = ld_scale(k_scale + base[i] / D + kt);
 #pragma unroll
     for (int j = 0; j < NX; ++j) {
       const int x = lane + 64 * j, ix = x / BS;
       int64_t rb = base[0];  // base[ix] by selects (ix differs between lanes)
 #pragma unroll
       for (int i = 1; i < NTW; ++i) rb = ix == i ? base[i] : rb;
-      vsc[j] = x < NTW * BS ? v_scale[rb / D + x % BS] : 0.0f;
+      vsc[j] = x < NTW * BS ? ld_scale(v_scale + rb / D + x % BS) : 0.0f;
     }
   }
 
@@ -1408,7 +1462,7 @@ template <typename T, int D, int G, int FMT, int NTILE, int SPLIT = split_of<T>(
 Launch make_launch(bool append) {
   Launch l;
   l.nw = SPLIT;
-  if constexpr (FMT == RKV_BF16) {  // the fused append is built for bf16 pools only
+  if constexpr (FMT == RKV_BF16 || FMT == RKV_I8 || FMT == RKV_FP8) {  // fused append builds
     if (append) {
       l.kernel = &decode_stream_kernel<T, D, G, kBS, NTILE, ring_for<T, D, NTILE, SPLIT>(),
                                        SPLIT, FMT, true>;
@@ -1754,7 +1808,9 @@ extern "C" int rkv_decode_attention_append(
     int partition_size, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   if (dtype != RKV_BF16)
-    return fail(RKV_ERR_UNSUPPORTED, "rkv_decode_attention_append: RKV_BF16 pools only");
+    return fail(RKV_ERR_UNSUPPORTED,
+                "rkv_decode_attention_append: RKV_BF16 pools (1-byte pools: "
+                "rkv_decode_attention_append_q)");
   if (num_seqs > 0 && (!k_new || !v_new))
     return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
   if (num_seqs > 0 && (!aligned16(k_new) || !aligned16(v_new)))
@@ -1776,6 +1832,37 @@ extern "C" int rkv_decode_attention_append(
   if (int rc = launch_partitions(a, max_parts, P2)) return rc;
   return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim,
                       ctx_cap_of(max_context, max_blocks_per_seq, block_size), P2, max_parts,
+                      workspace, a.stream);
+}
+
+// rkv_decode_attention_append for 1-byte pools: the new rows quantized as
+// rkv_append_q quantizes them.
+extern "C" int rkv_decode_attention_append_q(
+    float* out, const float* q, void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+    const float* k_new, const float* v_new, const int32_t* block_tables, int max_blocks_per_seq,
+    const int32_t* ctx_lens, int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+    int block_size, int64_t num_blocks, int max_context, float scale, int dtype,
+    int partition_size, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (dtype != RKV_I8 && dtype != RKV_FP8)
+    return fail(RKV_ERR_INVALID_ARG,
+                "rkv_decode_attention_append_q: dtype must be RKV_I8 or RKV_FP8");
+  if (num_seqs > 0 && (!k_new || !v_new))
+    return fail(RKV_ERR_INVALID_ARG, "null pointer argument");
+  if (num_seqs > 0 && (!aligned16(k_new) || !aligned16(v_new)))
+    return fail(RKV_ERR_INVALID_ARG, "k_new and v_new must be 16-byte aligned");
+  DecodeArgs a{out, q, k_pool, v_pool, block_tables, max_blocks_per_seq, ctx_lens, num_seqs,
+               num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, max_context, scale,
+               dtype, partition_size, workspace, workspace_bytes,
+               static_cast<hipStream_t>(stream), k_scale, v_scale};
+  a.k_new = k_new;
+  a.v_new = v_new;
+  int max_parts = 1, P = 0;
+  if (int rc = validate(a, max_parts, P)) return rc;
+  if (num_seqs == 0) return RKV_OK;
+  if (int rc = launch_partitions(a, max_parts, P)) return rc;
+  return launch_merge(out, ctx_lens, num_seqs, num_q_heads, head_dim,
+                      ctx_cap_of(max_context, max_blocks_per_seq, block_size), P, max_parts,
                       workspace, a.stream);
 }
 

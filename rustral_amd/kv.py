@@ -308,6 +308,45 @@ def gather_q(k_pool: torch.Tensor, v_pool: torch.Tensor, k_scale: torch.Tensor,
     return k_out, v_out
 
 
+def decode_attention_append_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                              k_scale: torch.Tensor, v_scale: torch.Tensor, k_new: torch.Tensor,
+                              v_new: torch.Tensor, block_tables: torch.Tensor,
+                              ctx_lens: torch.Tensor, scale: float | None = None,
+                              fmt: str = "int8", *, max_context: int | None = None,
+                              out: torch.Tensor | None = None,
+                              workspace: torch.Tensor | None = None,
+                              partition_size: int = 0) -> torch.Tensor:
+    """decode_attention_append over 1-byte pools: the new rows quantized as
+    append_q quantizes them, then decode_attention_q, in one launch."""
+    _dev(q, "q", torch.float32), _dev(k_pool, "k_pool", torch.uint8)
+    _dev(v_pool, "v_pool", torch.uint8), _dev(k_scale, "k_scale", torch.float32)
+    _dev(v_scale, "v_scale", torch.float32)
+    _dev(k_new, "k_new", torch.float32), _dev(v_new, "v_new", torch.float32)
+    _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
+    nb, hkv, bs, d = k_pool.shape
+    B, hq, dq = q.shape
+    if dq != d or tuple(k_new.shape) != (B, hkv, d) or tuple(v_new.shape) != (B, hkv, d):
+        raise ValueError("q, k_new and v_new must be [B, Hq, D], [B, Hkv, D], [B, Hkv, D]")
+    mbs = block_tables.shape[1]
+    if max_context is None:
+        max_context = mbs * bs
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    need = workspace_bytes(B, hq, d, max_context, partition_size)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_len = workspace.numel() if workspace is not None else 0
+    check(lib().rkv_decode_attention_append_q(
+        out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(),
+        v_scale.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), block_tables.data_ptr(), mbs,
+        ctx_lens.data_ptr(), B, hq, hkv, d, bs, nb, max_context, float(scale), _qcode(fmt),
+        partition_size, ws_ptr, ws_len, _stream(q)))
+    return out
+
+
 def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                        k_scale: torch.Tensor, v_scale: torch.Tensor, block_tables: torch.Tensor,
                        ctx_lens: torch.Tensor, scale: float | None = None, fmt: str = "int8", *,
@@ -459,4 +498,5 @@ class DeviceBlockManager:
 
 __all__ = ["append", "gather", "copy_blocks", "decode_attention", "prefill_attention",
            "append_q", "gather_q", "decode_attention_q", "workspace_bytes",
-           "DeviceBlockManager", "_lib", "partition_size_for", "decode_attention_append"]
+           "DeviceBlockManager", "_lib", "partition_size_for", "decode_attention_append",
+           "decode_attention_append_q"]

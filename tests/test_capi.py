@@ -204,3 +204,16 @@ def test_decode_append_rejects_bad_arguments(kw, code):
 
 def test_decode_append_zero_sequences_is_a_no_op():
     assert _decode_append(B=0, kn=None, vn=None, out=None, q=None) == 0
+
+
+def test_decode_append_q_rejects_bad_arguments():
+    L = _lib.lib()
+
+    def call(dt=RKV_I8, kn=16, vn=16, d=128):
+        return L.rkv_decode_attention_append_q(16, 16, 16, 16, 16, 16, kn, vn, 16, 4, 16, 2, 8,
+                                               2, d, 16, 10, 64, 0.1, dt, 0, None, 0, None)
+    assert call(dt=RKV_BF16) == RKV_ERR_INVALID_ARG
+    assert call(kn=None) == RKV_ERR_INVALID_ARG
+    assert call(vn=8) == RKV_ERR_INVALID_ARG
+    assert call(d=32) == RKV_ERR_UNSUPPORTED
+    assert call(dt=RKV_FP8, d=48) == RKV_ERR_UNSUPPORTED

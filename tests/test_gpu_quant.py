@@ -319,3 +319,54 @@ def test_decode_q_caller_partition_sizes(dev, fmt, P):
     want = oracle.decode_attention(q, oracle.dequantize_pool(kp, ks, CODE[fmt]),
                                    oracle.dequantize_pool(vp, vs, CODE[fmt]), tables, ctx, scale)
     assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"1-byte partition {P} vs oracle")
+
+
+@pytest.mark.parametrize("P", [0, 256])
+@pytest.mark.parametrize("max_context", [None, 1000])
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64), (8, 1, 128), (16, 2, 64)])
+def test_decode_append_q_fused_matches_append_q_then_decode_q(dev, P, max_context, fmt, hq,
+                                                              hkv, d):
+    """rkv_decode_attention_append_q == rkv_append_q of the new rows followed
+    by rkv_decode_attention_q, bit for bit in the byte pools, the scale pools
+    and the output: new tokens at the first, middle and last row of a block
+    and at partition boundaries, an all-zero row (scale 0), a row with a
+    large value (fp8 saturation range), invalid block ids (-1 and past the
+    pool: nothing written), an empty sequence, and lengths clamped by
+    max_context 1000 (their rows not written)."""
+    bs = 16
+    ctx = np.array([1, 2, 16, 17, 640, 641, 1281, 0, 40, 50, 33, 256], np.int32)
+    say(f"decode append_q fused fmt={fmt} P={P} hq={hq} hkv={hkv} d={d} max_context={max_context}")
+    rng = np.random.default_rng(11 * P + hq + d)
+    nb = int(sum((int(c) + bs - 1) // bs for c in ctx)) + 3
+    kp, vp, ks, vs = quant_case(hq + d + P, nb, hkv, bs, d, fmt)
+    tables = make_tables(rng, ctx, bs, nb)
+    tables[8, (40 - 1) // bs] = -1
+    tables[9, (50 - 1) // bs] = nb + 3
+    kn = (rng.standard_normal((len(ctx), hkv, d)) * 2).astype(np.float32)
+    vn = rng.standard_normal((len(ctx), hkv, d)).astype(np.float32)
+    kn[10] = 0.0                      # scale 0
+    vn[11, :, 3] = 5e4                # one large element
+    cap = min(max_context if max_context is not None else 1 << 30, tables.shape[1] * bs)
+    slots = np.full(len(ctx), -1, np.int64)
+    for b, L in enumerate(ctx):
+        if 0 < L <= cap:
+            blk = int(tables[b, (L - 1) // bs])
+            slots[b] = blk * bs + (L - 1) % bs if 0 <= blk < nb else -1
+    q = rng.standard_normal((len(ctx), hq, d)).astype(np.float32)
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    qd, td, cd = to_dev(q, dev), to_dev(tables, dev), to_dev(ctx, dev)
+    knd, vnd = to_dev(kn, dev), to_dev(vn, dev)
+    k1, v1, s1, t1 = to_dev(kp, dev), to_dev(vp, dev), to_dev(ks, dev), to_dev(vs, dev)
+    k2, v2, s2, t2 = k1.clone(), v1.clone(), s1.clone(), t1.clone()
+    kv.append_q(k1, v1, s1, t1, knd, vnd, to_dev(slots, dev), fmt)
+    want = kv.decode_attention_q(qd, k1, v1, s1, t1, td, cd, scale, fmt,
+                                 max_context=max_context, partition_size=P)
+    got = kv.decode_attention_append_q(qd, k2, v2, s2, t2, knd, vnd, td, cd, scale, fmt,
+                                       max_context=max_context, partition_size=P)
+    torch.cuda.synchronize()
+    assert torch.equal(k2, k1) and torch.equal(v2, v1), "byte pools differ"
+    assert torch.equal(s2.view(torch.int32), s1.view(torch.int32)), "K scales differ"
+    assert torch.equal(t2.view(torch.int32), t1.view(torch.int32)), "V scales differ"
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32)), \
+        f"max diff {(got - want).abs().max().item()}"
