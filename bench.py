@@ -617,6 +617,38 @@ def run_decode_q(torch, dev, args):
         res[fmt] = {"us_per_call": round(us, 2), "bytes_per_call": nbytes,
                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                     "decode_tokens_per_s_b64": round(B / (ms * 1e-3), 1)}
+        # a model's per-layer order: the new token's quantizing append, then
+        # the attention, per layer -- as two launches, and fused (the new
+        # row rewrites position ctx - 1 of every sequence on each replay)
+        last = torch.from_numpy((ctx.astype(np.int64) - 1)).to(dev)
+        kn1 = torch.randn((B, HKV, D), generator=g, device=dev)
+        vn1 = torch.randn((B, HKV, D), generator=g, device=dev)
+        slot_l = [(t[torch.arange(B, device=dev), last // BS].to(torch.int64) * BS + last % BS)
+                  for (_, _, _, _, _, t, _) in layers]
+
+        def step_pl():
+            for (q, kp, vp, ks, vs, t, o), sl in zip(layers, slot_l):
+                kv.append_q(kp, vp, ks, vs, kn1, vn1, sl, fmt)
+                kv.decode_attention_q(q, kp, vp, ks, vs, t, ctx_d, scale, fmt,
+                                      max_context=CTX_HI, out=o, workspace=ws)
+
+        def step_fu():
+            for (q, kp, vp, ks, vs, t, o) in layers:
+                kv.decode_attention_append_q(q, kp, vp, ks, vs, kn1, vn1, t, ctx_d, scale, fmt,
+                                             max_context=CTX_HI, out=o, workspace=ws)
+        app1 = B * HKV * D * (4 + 1) * 2 + B * HKV * 4 * 2
+        for name, fn in (("per_layer_append_q_then_decode_q", step_pl),
+                         ("per_layer_fused_append_decode_q", step_fu)):
+            fn()
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                fn()
+            gr.replay()
+            m2 = _timed(torch, gr.replay, args.steps)
+            del gr
+            res[fmt][name] = {"ms_per_step": round(m2, 4),
+                              "GBps": round(32 * (nbytes + app1) / (m2 * 1e-3) / 1e9, 1)}
         # dequantizing gather into the packed KVCache layout, one layer per
         # call, rotating over the 32 layer pools
         n_tok = int(ctx.astype(np.int64).sum())
