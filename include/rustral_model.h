@@ -73,6 +73,30 @@ int rkv_gelu(float* y, const float* x, int64_t n, void* stream);
 /* y = a + b element-wise.  Replaces TensorOps::add (lib.rs:283-315). */
 int rkv_add(float* y, const float* a, const float* b, int64_t n, void* stream);
 
+/* y = x * s element-wise.  Replaces TensorOps::mul_scalar (lib.rs:747-756). */
+int rkv_mul_scalar(float* y, const float* x, float s, int64_t n, void* stream);
+
+/* Softmax along one axis of a tensor viewed as [outer][axis][inner]: per
+ * line, max (NaN skipped, as f32::max), e = exp(x - max), sum = the e added
+ * serially in axis order, y = e * (1 / sum).  Replaces TensorOps::softmax_dim
+ * (crates/ndarray-backend/src/lib.rs:1188-1227; dim d of shape s gives
+ * outer = prod s[..d], axis = s[d], inner = prod s[d+1..]).  axis == 0 is
+ * RKV_ERR_INVALID_ARG, the reference's "axis size is 0".  exp is the device
+ * library's expf (within 2 ulp of the host's). */
+int rkv_softmax_dim(float* y, const float* x, int64_t outer, int64_t axis, int64_t inner,
+                    void* stream);
+
+/* y[m][n] = sum_j a[m][j] * b[j][n] (row-major), each sum serial in j without
+ * fused multiply-add: the order of TensorOps::matmul's naive loop
+ * (lib.rs:191-267; the reference hands products with m*k*n >= 64 to the
+ * matrixmultiply crate's sgemm, whose blocked order is not reproduced).
+ * m <= 1048560. */
+int rkv_matmul(float* y, const float* a, const float* b, int m, int k, int n, void* stream);
+
+/* y[n][m] = x[m][n] (y must not alias x).  Replaces TensorOps::transpose
+ * (lib.rs:270-281).  m <= 2097120. */
+int rkv_transpose(float* y, const float* x, int m, int n, void* stream);
+
 /* out[r] = index of the maximum of row r (n columns), the LAST one among
  * equal maxima; NaN compares equal to everything, as in TensorOps::argmax
  * (lib.rs:430-437) and Sampler::greedy (crates/nn/src/continuous_batching.rs:

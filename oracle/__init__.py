@@ -53,6 +53,11 @@ def _declare(L):
                              C.c_int, _i64, C.c_int, C.c_int, C.c_int]
     L.orc_copy_blocks.argtypes = [_p, _p, _i64, C.c_int, _p, C.c_int, _i64, _i64]
     L.orc_softmax_rows.argtypes = [_p, _p, C.c_int, C.c_int]
+    L.orc_softmax_dim.restype = C.c_int
+    L.orc_softmax_dim.argtypes = [_p, _p, _i64, _i64, _i64]
+    L.orc_matmul.argtypes = [_p, _p, _p, C.c_int, C.c_int, C.c_int]
+    L.orc_transpose.argtypes = [_p, _p, C.c_int, C.c_int]
+    L.orc_mul_scalar.argtypes = [_p, _p, _f32, _i64]
     L.orc_argmax.restype = _i64
     L.orc_argmax.argtypes = [_p, _i64]
     dec = [_p, _p, _p, _p, _p, C.c_int, _p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _i64,
@@ -190,6 +195,44 @@ def softmax_rows(x: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().orc_softmax_rows(_ptr(x), _ptr(y), x.shape[0], x.shape[1])
+    return y
+
+
+def softmax_dim(x: np.ndarray, dim: int) -> np.ndarray:
+    """CpuOps::softmax_dim of x along dim (any rank)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if not 0 <= dim < x.ndim:
+        raise ValueError(f"softmax_dim: dim {dim} out of range for shape {x.shape}")
+    outer = int(np.prod(x.shape[:dim], dtype=np.int64))
+    inner = int(np.prod(x.shape[dim + 1:], dtype=np.int64))
+    y = np.empty_like(x)
+    if lib().orc_softmax_dim(_ptr(x), _ptr(y), outer, x.shape[dim], inner) != 0:
+        raise ValueError("softmax_dim: axis size is 0")
+    return y
+
+
+def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    (m, k), (k2, n) = a.shape, b.shape
+    if k != k2:
+        raise ValueError(f"matmul: inner sizes {k} and {k2} differ")
+    y = np.empty((m, n), np.float32)
+    lib().orc_matmul(_ptr(a), _ptr(b), _ptr(y), m, k, n)
+    return y
+
+
+def transpose(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty((x.shape[1], x.shape[0]), np.float32)
+    lib().orc_transpose(_ptr(x), _ptr(y), x.shape[0], x.shape[1])
+    return y
+
+
+def mul_scalar(x: np.ndarray, s: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_mul_scalar(_ptr(x), _ptr(y), s, x.size)
     return y
 
 

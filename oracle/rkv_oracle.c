@@ -225,21 +225,53 @@ int orc_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int 
 
 /* ---- softmax / argmax -------------------------------------------------- */
 
-void orc_softmax_rows(const float* x, float* y, int rows, int cols) {
-  for (int r = 0; r < rows; ++r) {
-    const float* xr = x + (int64_t)r * cols;
-    float* yr = y + (int64_t)r * cols;
-    float mx = -INFINITY;
-    for (int c = 0; c < cols; ++c) mx = fmaxf(mx, xr[c]);
-    float sum = 0.0f;
-    for (int c = 0; c < cols; ++c) {
-      const float e = expf(xr[c] - mx);
-      yr[c] = e;
-      sum += e;
+/* CpuOps::softmax_dim (crates/ndarray-backend/src/lib.rs:1188-1227): the
+ * loops over (o, i), each line's max from -inf by f32::max (fmaxf: a NaN
+ * operand is skipped), exp, serial sum and the 1/sum scale, in that order. */
+int orc_softmax_dim(const float* x, float* y, int64_t outer, int64_t axis, int64_t inner) {
+  if (axis <= 0 || outer < 0 || inner < 0) return -1; /* lib.rs:1200-1202 */
+  for (int64_t o = 0; o < outer; ++o) {
+    for (int64_t i = 0; i < inner; ++i) {
+      const int64_t base = o * axis * inner + i;
+      float mx = -INFINITY;
+      for (int64_t a = 0; a < axis; ++a) mx = fmaxf(mx, x[base + a * inner]);
+      float sum = 0.0f;
+      for (int64_t a = 0; a < axis; ++a) {
+        const float e = expf(x[base + a * inner] - mx);
+        y[base + a * inner] = e;
+        sum += e;
+      }
+      const float inv = 1.0f / sum;
+      for (int64_t a = 0; a < axis; ++a) y[base + a * inner] *= inv;
     }
-    const float inv = 1.0f / sum;
-    for (int c = 0; c < cols; ++c) yr[c] *= inv;
   }
+  return 0;
+}
+
+void orc_softmax_rows(const float* x, float* y, int rows, int cols) {
+  orc_softmax_dim(x, y, rows, cols, 1);
+}
+
+/* CpuOps::matmul's naive loop (lib.rs:208-219): out[i][j] = sum over kk of
+ * a[i][kk] * b[kk][j], serial in kk from 0.0. */
+void orc_matmul(const float* a, const float* b, float* y, int m, int k, int n) {
+  for (int i = 0; i < m; ++i)
+    for (int j = 0; j < n; ++j) {
+      float sum = 0.0f;
+      for (int kk = 0; kk < k; ++kk) sum += a[(int64_t)i * k + kk] * b[(int64_t)kk * n + j];
+      y[(int64_t)i * n + j] = sum;
+    }
+}
+
+/* CpuOps::transpose (lib.rs:270-281): out[j][i] = x[i][j]. */
+void orc_transpose(const float* x, float* y, int m, int n) {
+  for (int i = 0; i < m; ++i)
+    for (int j = 0; j < n; ++j) y[(int64_t)j * m + i] = x[(int64_t)i * n + j];
+}
+
+/* CpuOps::mul_scalar (lib.rs:747-756): v * scalar per element. */
+void orc_mul_scalar(const float* x, float* y, float s, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = x[i] * s;
 }
 
 int64_t orc_argmax(const float* x, int64_t n) {

@@ -77,6 +77,19 @@ int orc_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int 
  * multiply by 1/sum. */
 void orc_softmax_rows(const float* x, float* y, int rows, int cols);
 
+/* CpuOps::softmax_dim on any axis of a tensor viewed as [outer][axis][inner]
+ * (lib.rs:1188-1227); axis <= 0 -> -1 (the reference's InvalidArgument). */
+int orc_softmax_dim(const float* x, float* y, int64_t outer, int64_t axis, int64_t inner);
+
+/* CpuOps::matmul's naive order (lib.rs:208-219), rank 2, row-major. */
+void orc_matmul(const float* a, const float* b, float* y, int m, int k, int n);
+
+/* CpuOps::transpose (lib.rs:270-281), rank 2. */
+void orc_transpose(const float* x, float* y, int m, int n);
+
+/* CpuOps::mul_scalar (lib.rs:747-756). */
+void orc_mul_scalar(const float* x, float* y, float s, int64_t n);
+
 /* Greedy argmax: last index among equal maxima, as Iterator::max_by in
  * CpuOps::argmax (ndarray-backend/src/lib.rs:430-437) and Sampler::greedy
  * (crates/nn/src/continuous_batching.rs:458-462).  n == 0 -> -1. */

@@ -425,6 +425,11 @@ extern "C" {
     ) -> c_int;
     pub fn rkv_gelu(y: *mut f32, x: *const f32, n: i64, stream: Stream) -> c_int;
     pub fn rkv_add(y: *mut f32, a: *const f32, b: *const f32, n: i64, stream: Stream) -> c_int;
+    pub fn rkv_mul_scalar(y: *mut f32, x: *const f32, s: f32, n: i64, stream: Stream) -> c_int;
+    pub fn rkv_softmax_dim(y: *mut f32, x: *const f32, outer: i64, axis: i64, inner: i64, stream: Stream) -> c_int;
+    pub fn rkv_matmul(y: *mut f32, a: *const f32, b: *const f32, m: c_int, k: c_int, n: c_int, stream: Stream)
+        -> c_int;
+    pub fn rkv_transpose(y: *mut f32, x: *const f32, m: c_int, n: c_int, stream: Stream) -> c_int;
     pub fn rkv_argmax(out: *mut i32, x: *const f32, rows: c_int, n: c_int, stream: Stream) -> c_int;
     pub fn rkv_decoder_param_count(cfg: *const RkvDecoderConfig) -> i64;
     pub fn rkv_decoder_init_params(

@@ -19,11 +19,16 @@
 //!   step by [`batch_to_device`]).
 //! * [`BlockManager`] / [`DeviceBlockManager`] are `PagedCache` on the host
 //!   and in device memory.
+//! * [`RocmDecoder`] runs the config-0 decoder end to end (greedy
+//!   `generate_token`, crates/nn/src/transformer.rs:837-862) and
+//!   [`RocmServingEngine`] is `ServingEngine` (crates/nn/src/
+//!   continuous_batching.rs:493-545) with the model in its step.
 
 pub mod ffi;
 
 mod device;
 mod error;
+mod model;
 mod ops;
 mod paged;
 mod serving;
@@ -35,6 +40,7 @@ use rustral_core::{AttentionOps, Backend, BackendCapabilities, CoreError, Parame
 
 pub use device::{Ctx, DeviceBuffer};
 pub use error::{check, last_error};
+pub use model::{DecoderConfig, Priority, RocmDecoder, RocmServingEngine, SchedulerStats};
 pub use ops::RocmOps;
 pub use paged::{batch_to_device, KvDtype, PagedKvConfig, RocmPagedKvCache, BLOCK_SIZE};
 pub use serving::{BlockManager, DeviceBlockManager};

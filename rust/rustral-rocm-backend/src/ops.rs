@@ -1,8 +1,10 @@
 //! `TensorOps` and `AttentionOps` of the ROCm backend.
 //!
 //! The subset the KV path and the config-0 model need runs on the device
-//! through the C ABI (`linear`, `gelu`, `add`, `argmax`, `gather_rows`, data
-//! movement for `zeros` / `slice` / `concat` / `reshape`); the other methods
+//! through the C ABI (`linear`, `gelu`, `add`, `argmax`, `gather_rows`, the
+//! per-head attention recipe's `matmul` / `transpose` / `mul_scalar` /
+//! `softmax` / `softmax_dim`, data movement for `zeros` / `slice` / `concat`
+//! / `reshape`); the other methods
 //! return `CoreError::Backend("<op>: unsupported on rocm backend")`.  There
 //! is no host fallback.
 
@@ -45,6 +47,17 @@ impl RocmOps {
         self.ctx.stream
     }
 
+    /// `rkv_softmax_dim` over x viewed as `[outer][axis][inner]`.
+    fn softmax_lines(&self, x: &RocmTensor, outer: usize, axis: usize, inner: usize) -> Result<RocmTensor> {
+        let y = RocmTensor::empty(&self.ctx, &x.shape, DType::F32)?;
+        // SAFETY: x and y hold outer * axis * inner floats.
+        check(unsafe {
+            ffi::rkv_softmax_dim(y.device_ptr() as *mut f32, x.device_ptr() as *const f32, outer as i64,
+                                 axis as i64, inner as i64, self.s())
+        })?;
+        Ok(y)
+    }
+
     fn d2d(&self, dst: *mut c_void, src: *const c_void, bytes: usize) -> Result<()> {
         if bytes == 0 {
             return Ok(());
@@ -76,12 +89,35 @@ impl TensorOps<RocmBackend> for RocmOps {
         Ok(RocmTensor::from_buffer(&self.ctx, buf, shape, DType::F32))
     }
 
-    fn matmul(&self, _a: &RocmTensor, _b: &RocmTensor) -> Result<RocmTensor> {
-        Err(unsupported("matmul"))
+    /// Rank-2 product (crates/ndarray-backend/src/lib.rs:191-267) by
+    /// `rkv_matmul`: every sum serial in k, the naive loop's order.
+    fn matmul(&self, a: &RocmTensor, b: &RocmTensor) -> Result<RocmTensor> {
+        a.expect(DType::F32, 2, "matmul a")?;
+        b.expect(DType::F32, 2, "matmul b")?;
+        let (m, k, n) = (a.shape[0], a.shape[1], b.shape[1]);
+        if b.shape[0] != k {
+            return Err(CoreError::ShapeMismatch { expected: vec![k], actual: vec![b.shape[0]] });
+        }
+        let y = RocmTensor::empty(&self.ctx, &[m, n], DType::F32)?;
+        // SAFETY: a [m][k], b [k][n] and y [m][n] are live device buffers.
+        check(unsafe {
+            ffi::rkv_matmul(y.device_ptr() as *mut f32, a.device_ptr() as *const f32, b.device_ptr() as *const f32,
+                            to_c_int(m, "m")?, to_c_int(k, "k")?, to_c_int(n, "n")?, self.s())
+        })?;
+        Ok(y)
     }
 
-    fn transpose(&self, _x: &RocmTensor) -> Result<RocmTensor> {
-        Err(unsupported("transpose"))
+    /// Rank-2 transpose (lib.rs:270-281) by `rkv_transpose`.
+    fn transpose(&self, x: &RocmTensor) -> Result<RocmTensor> {
+        x.expect(DType::F32, 2, "transpose")?;
+        let (m, n) = (x.shape[0], x.shape[1]);
+        let y = RocmTensor::empty(&self.ctx, &[n, m], DType::F32)?;
+        // SAFETY: x [m][n] and y [n][m] are distinct live device buffers.
+        check(unsafe {
+            ffi::rkv_transpose(y.device_ptr() as *mut f32, x.device_ptr() as *const f32, to_c_int(m, "m")?,
+                               to_c_int(n, "n")?, self.s())
+        })?;
+        Ok(y)
     }
 
     /// Element-wise sum (crates/ndarray-backend/src/lib.rs:283-315) by `rkv_add`.
@@ -106,8 +142,31 @@ impl TensorOps<RocmBackend> for RocmOps {
         Err(unsupported("relu"))
     }
 
-    fn softmax(&self, _x: &RocmTensor) -> Result<RocmTensor> {
-        Err(unsupported("softmax"))
+    /// Softmax over all values (lib.rs:373-427) as one line of
+    /// `rkv_softmax_dim`; the reference's `wide` SIMD exp is not reproduced
+    /// (the device expf is within 2 ulp of the host's).
+    fn softmax(&self, x: &RocmTensor) -> Result<RocmTensor> {
+        f32_tensor(x, "softmax")?;
+        if x.numel() == 0 {
+            return Err(CoreError::InvalidArgument("softmax of empty tensor".into()));
+        }
+        self.softmax_lines(x, 1, x.numel(), 1)
+    }
+
+    /// Softmax along `dim` (lib.rs:1188-1227) by `rkv_softmax_dim`: per line
+    /// max, `exp(x - max)`, the serial sum and `* (1 / sum)`.
+    fn softmax_dim(&self, x: &RocmTensor, dim: usize) -> Result<RocmTensor> {
+        f32_tensor(x, "softmax_dim")?;
+        if dim >= x.shape.len() {
+            return Err(CoreError::InvalidArgument(format!(
+                "softmax_dim: dim {dim} out of range for shape {:?}", x.shape
+            )));
+        }
+        let axis = x.shape[dim];
+        if axis == 0 {
+            return Err(CoreError::InvalidArgument("softmax_dim: axis size is 0".into()));
+        }
+        self.softmax_lines(x, numel(&x.shape[..dim]), axis, numel(&x.shape[dim + 1..]))
     }
 
     fn log_softmax(&self, _x: &RocmTensor) -> Result<RocmTensor> {
@@ -271,8 +330,16 @@ impl TensorOps<RocmBackend> for RocmOps {
         Err(unsupported("add_scalar"))
     }
 
-    fn mul_scalar(&self, _x: &RocmTensor, _s: f32) -> Result<RocmTensor> {
-        Err(unsupported("mul_scalar"))
+    /// `x * s` per element (lib.rs:747-756) by `rkv_mul_scalar`.
+    fn mul_scalar(&self, x: &RocmTensor, s: f32) -> Result<RocmTensor> {
+        f32_tensor(x, "mul_scalar")?;
+        let y = RocmTensor::empty(&self.ctx, &x.shape, DType::F32)?;
+        // SAFETY: x and y hold numel floats.
+        check(unsafe {
+            ffi::rkv_mul_scalar(y.device_ptr() as *mut f32, x.device_ptr() as *const f32, s, x.numel() as i64,
+                                self.s())
+        })?;
+        Ok(y)
     }
 
     fn broadcast(&self, _x: &RocmTensor, _shape: &[usize]) -> Result<RocmTensor> {

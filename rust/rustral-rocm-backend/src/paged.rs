@@ -87,6 +87,38 @@ fn ci(v: usize, what: &str) -> Result<i32> {
     i32::try_from(v).map_err(|_| CoreError::InvalidArgument(format!("{what} = {v} exceeds i32")))
 }
 
+/// The shapes an attention call's kernels index by: q rows `[n, Hq, D]`
+/// with `D` the pool's head_dim and `Hq` a multiple of its KV heads, and one
+/// table row and one length per sequence (`seqs` of them; `q_start` when
+/// given holds `seqs + 1` offsets).  The kernels take sizes, not buffer
+/// lengths, so a mismatch here would read past the tables or write rows of
+/// the wrong width into the pools: it is rejected before any launch.
+pub(crate) fn check_attention_shapes(cfg: &PagedKvConfig, q: &[usize], block_tables: &[usize], ctx_lens: &[usize],
+                                     q_start: Option<&[usize]>) -> Result<()> {
+    let bad = |m: String| Err(CoreError::InvalidArgument(m));
+    if q.len() != 3 || block_tables.len() != 2 || ctx_lens.len() != 1 {
+        let ranks = (q.len(), block_tables.len(), ctx_lens.len());
+        return bad(format!("attention: q, block_tables and ctx_lens have ranks {ranks:?}, not (3, 2, 1)"));
+    }
+    if q[2] != cfg.head_dim {
+        return bad(format!("attention: q head_dim {} differs from the pool's {}", q[2], cfg.head_dim));
+    }
+    if q[1] == 0 || q[1] % cfg.num_kv_heads != 0 {
+        return bad(format!("attention: {} query heads are not a multiple of {} KV heads", q[1], cfg.num_kv_heads));
+    }
+    let seqs = ctx_lens[0];
+    if block_tables[0] != seqs {
+        return bad(format!("attention: {} block-table rows for {seqs} sequences", block_tables[0]));
+    }
+    match q_start {
+        Some(qs) if qs.len() != 1 || qs[0] != seqs + 1 => {
+            bad(format!("attention: q_start {qs:?} must hold {} offsets", seqs + 1))
+        }
+        None if q[0] != seqs => bad(format!("attention: {} q rows for {seqs} sequences", q[0])),
+        _ => Ok(()),
+    }
+}
+
 impl RocmPagedKvCache {
     pub fn new(backend: &RocmBackend, cfg: PagedKvConfig) -> Result<Self> {
         let ctx = backend.ctx.clone();
@@ -190,6 +222,11 @@ impl RocmPagedKvCache {
         -> Result<(RocmTensor, RocmTensor)> {
         block_tables.expect(DType::I32, 2, "block_tables")?;
         ctx_lens.expect(DType::I32, 1, "ctx_lens")?;
+        if ctx_lens.shape[0] != block_tables.shape[0] {
+            return Err(CoreError::InvalidArgument(format!(
+                "gather: {} block-table rows for {} lengths", block_tables.shape[0], ctx_lens.shape[0]
+            )));
+        }
         let (b, mb) = (block_tables.shape[0], block_tables.shape[1]);
         let (h, d) = (self.cfg.num_kv_heads, self.cfg.head_dim);
         let out_dt = if self.cfg.dtype == KvDtype::Bf16 { DType::Bf16 } else { DType::F32 };
@@ -197,7 +234,8 @@ impl RocmPagedKvCache {
         let ko = RocmTensor::empty(&self.ctx, &shape, out_dt)?;
         let vo = RocmTensor::empty(&self.ctx, &shape, out_dt)?;
         let (kp, vp) = (self.layer_ptr(&self.k, layer)?, self.layer_ptr(&self.v, layer)?);
-        // SAFETY: live buffers of the checked shapes.
+        // SAFETY: live buffers: one table row per length, outputs allocated here
+        // at [b, h, max_ctx, d] (the kernel clamps each length to max_ctx).
         let rc = unsafe {
             if self.cfg.dtype.one_byte() {
                 ffi::rkv_gather_q(ko.device_ptr() as *mut f32, vo.device_ptr() as *mut f32, kp, vp,
@@ -224,6 +262,9 @@ impl RocmPagedKvCache {
     /// Sources and destinations must be disjoint.
     pub fn copy_blocks(&mut self, pairs: &RocmTensor) -> Result<()> {
         pairs.expect(DType::I32, 2, "pairs")?;
+        if pairs.shape[1] != 2 {
+            return Err(CoreError::InvalidArgument(format!("copy_blocks: pairs {:?} must be [n, 2]", pairs.shape)));
+        }
         let n = ci(pairs.shape[0], "pairs")?;
         let block_bytes = (self.cfg.num_kv_heads * BLOCK_SIZE * self.cfg.head_dim * self.cfg.dtype.size()) as i64;
         let ls = self.layer_elems() as i64 * self.cfg.dtype.size() as i64;
@@ -254,6 +295,7 @@ impl RocmPagedKvCache {
         q.expect(DType::F32, 3, "q")?;
         block_tables.expect(DType::I32, 2, "block_tables")?;
         ctx_lens.expect(DType::I32, 1, "ctx_lens")?;
+        check_attention_shapes(&self.cfg, &q.shape, &block_tables.shape, &ctx_lens.shape, None)?;
         let (b, hq, d) = (q.shape[0], q.shape[1], q.shape[2]);
         let mb = block_tables.shape[1];
         let need = unsafe {
@@ -268,7 +310,8 @@ impl RocmPagedKvCache {
         }
         let out = RocmTensor::empty(&self.ctx, &q.shape, DType::F32)?;
         let (kp, vp) = (self.layer_ptr(&self.k, layer)?, self.layer_ptr(&self.v, layer)?);
-        // SAFETY: live buffers of the checked shapes; the workspace holds `need` bytes.
+        // SAFETY: live buffers whose shapes check_attention_shapes has matched to
+        // the pool; the workspace holds `need` bytes.
         let rc = unsafe {
             if self.cfg.dtype.one_byte() {
                 ffi::rkv_decode_attention_q(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
@@ -309,6 +352,7 @@ impl RocmPagedKvCache {
         v_new.expect(DType::F32, 3, "v_new")?;
         block_tables.expect(DType::I32, 2, "block_tables")?;
         ctx_lens.expect(DType::I32, 1, "ctx_lens")?;
+        check_attention_shapes(&self.cfg, &q.shape, &block_tables.shape, &ctx_lens.shape, None)?;
         let (b, hq, d) = (q.shape[0], q.shape[1], q.shape[2]);
         let rows = [b, self.cfg.num_kv_heads, d];
         for t in [k_new, v_new] {
@@ -328,7 +372,8 @@ impl RocmPagedKvCache {
         }
         let out = RocmTensor::empty(&self.ctx, &q.shape, DType::F32)?;
         let (kp, vp) = (self.layer_ptr(&self.k, layer)?, self.layer_ptr(&self.v, layer)?);
-        // SAFETY: live buffers of the checked shapes; the workspace holds `need` bytes.
+        // SAFETY: live buffers whose shapes check_attention_shapes and the row
+        // check above have matched to the pool; the workspace holds `need` bytes.
         let rc = unsafe {
             if self.cfg.dtype.one_byte() {
                 ffi::rkv_decode_attention_append_q(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
@@ -365,13 +410,17 @@ impl RocmPagedKvCache {
         block_tables.expect(DType::I32, 2, "block_tables")?;
         q_start.expect(DType::I32, 1, "q_start")?;
         ctx_lens.expect(DType::I32, 1, "ctx_lens")?;
+        check_attention_shapes(&self.cfg, &q.shape, &block_tables.shape, &ctx_lens.shape, Some(&q_start.shape))?;
         if self.cfg.dtype.one_byte() {
             return Err(CoreError::Backend("prefill_attention: 1-byte pools are not built".into()));
         }
         let b = ctx_lens.shape[0];
         let out = RocmTensor::empty(&self.ctx, &q.shape, DType::F32)?;
         let (kp, vp) = (self.layer_ptr(&self.k, layer)?, self.layer_ptr(&self.v, layer)?);
-        // SAFETY: live buffers of the checked shapes.
+        // SAFETY: live buffers whose shapes check_attention_shapes has matched to
+        // the pool; q_start's values are device data the caller vouches for
+        // (rows q_start[b]..q_start[b + 1] lie inside q, rkv_prefill_attention's
+        // contract).
         check(unsafe {
             ffi::rkv_prefill_attention(out.device_ptr() as *mut f32, q.device_ptr() as *const f32, kp, vp,
                                        block_tables.device_ptr() as *const i32, ci(block_tables.shape[1], "max_blocks")?,
@@ -401,4 +450,40 @@ pub fn batch_to_device(backend: &RocmBackend, batch: &Batch) -> Result<(RocmTens
         RocmTensor::upload(&backend.ctx, &tab, &[b, mb], DType::I32)?,
         RocmTensor::upload(&backend.ctx, &lens, &[lens.len()], DType::I32)?,
     ))
+}
+
+#[cfg(test)]
+mod tests {
+    use super::*;
+
+    fn cfg() -> PagedKvConfig {
+        PagedKvConfig { layers: 2, num_blocks: 64, num_kv_heads: 8, head_dim: 128, dtype: KvDtype::Bf16 }
+    }
+
+    #[test]
+    fn matching_decode_and_prefill_shapes_pass() {
+        let c = cfg();
+        assert!(check_attention_shapes(&c, &[4, 32, 128], &[4, 16], &[4], None).is_ok());
+        assert!(check_attention_shapes(&c, &[300, 32, 128], &[4, 16], &[4], Some(&[5])).is_ok());
+    }
+
+    #[test]
+    fn mismatched_shapes_are_rejected_before_a_launch() {
+        let c = cfg();
+        let err = |r: Result<()>| matches!(r, Err(CoreError::InvalidArgument(_)));
+        // a head_dim other than the pool's: rows of the wrong width into the pool
+        assert!(err(check_attention_shapes(&c, &[4, 32, 256], &[4, 16], &[4], None)));
+        assert!(err(check_attention_shapes(&c, &[4, 32, 64], &[4, 16], &[4], None)));
+        // query heads not a multiple of the KV heads
+        assert!(err(check_attention_shapes(&c, &[4, 12, 128], &[4, 16], &[4], None)));
+        assert!(err(check_attention_shapes(&c, &[4, 0, 128], &[4, 16], &[4], None)));
+        // short tables or lengths: the kernel would read past them
+        assert!(err(check_attention_shapes(&c, &[4, 32, 128], &[3, 16], &[4], None)));
+        assert!(err(check_attention_shapes(&c, &[4, 32, 128], &[4, 16], &[3], None)));
+        assert!(err(check_attention_shapes(&c, &[5, 32, 128], &[4, 16], &[4], None)));
+        // prefill offsets: B + 1 of them
+        assert!(err(check_attention_shapes(&c, &[300, 32, 128], &[4, 16], &[4], Some(&[4]))));
+        // ranks
+        assert!(err(check_attention_shapes(&c, &[4, 32], &[4, 16], &[4], None)));
+    }
 }

@@ -88,6 +88,10 @@ SIGNATURES = {
                             _i, _i, _i, _i64, _i, _p]),
     "rkv_gelu": (_i, [_p, _p, _i64, _p]),
     "rkv_add": (_i, [_p, _p, _p, _i64, _p]),
+    "rkv_mul_scalar": (_i, [_p, _p, _f, _i64, _p]),
+    "rkv_softmax_dim": (_i, [_p, _p, _i64, _i64, _i64, _p]),
+    "rkv_matmul": (_i, [_p, _p, _p, _i, _i, _i, _p]),
+    "rkv_transpose": (_i, [_p, _p, _i, _i, _p]),
     "rkv_argmax": (_i, [_p, _p, _i, _i, _p]),
     "rkv_decoder_param_count": (_i64, [_p]),
     "rkv_decoder_init_params": (_i, [_p, C.c_uint64, _f, _p]),

@@ -1,6 +1,7 @@
 // model_ops.hip -- the fp32 TensorOps subset a decoder step needs on gfx950
 // (include/rustral_model.h): embedding + positional term, linear, layer norm,
-// gelu, add, argmax.
+// gelu, add, argmax, and the per-head attention recipe's matmul, transpose,
+// mul_scalar and softmax_dim.
 //
 // These are not the hot path (the KV cache and decode attention are); they
 // exist so a whole decoder step runs on the device.  Each op keeps the
@@ -170,6 +171,126 @@ __global__ __launch_bounds__(256) void add_kernel(float* y, const float* a, cons
                                                   int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void mul_scalar_kernel(float* y, const float* x, float s,
+                                                         int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = x[i] * s;
+}
+
+// Softmax along an axis of `axis` elements at stride `inner` (CpuOps::
+// softmax_dim's loops): max over the line with NaN skipped (f32::max /
+// fmaxf), e = exp(x - max) written out and added serially in axis order,
+// then every e scaled by 1 / sum.
+//
+// Strided lines (inner > 1): one thread per line, lanes on consecutive i, so
+// every step of the three serial loops is a coalesced row access.
+__global__ __launch_bounds__(256) void softmax_strided_kernel(float* y, const float* x,
+                                                              int64_t lines, int64_t axis,
+                                                              int64_t inner) {
+#pragma clang fp contract(off)
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= lines) return;
+  const int64_t o = g / inner, i = g - o * inner;
+  const float* xl = x + o * axis * inner + i;
+  float* yl = y + o * axis * inner + i;
+  float mx = -INFINITY;
+  for (int64_t a = 0; a < axis; ++a) mx = fmaxf(mx, xl[a * inner]);
+  float sum = 0.0f;
+  for (int64_t a = 0; a < axis; ++a) {
+    const float e = expf(xl[a * inner] - mx);
+    yl[a * inner] = e;
+    sum += e;
+  }
+  const float inv = 1.0f / sum;
+  for (int64_t a = 0; a < axis; ++a) yl[a * inner] *= inv;
+}
+
+// Contiguous lines (inner == 1): one 256-thread workgroup per row.  The max
+// is a tree over the workgroup (max is exact, so any order gives the serial
+// scan's value); the exps are computed in parallel, kChunk at a time, into
+// LDS and y, and lane 0 adds each chunk in index order, so the sum is the
+// reference's serial sum.  Each thread scales the entries it wrote itself.
+constexpr int kSoftmaxChunk = 2048;
+
+__global__ __launch_bounds__(256) void softmax_rows_kernel(float* y, const float* x,
+                                                           int64_t axis) {
+#pragma clang fp contract(off)
+  __shared__ float s_e[kSoftmaxChunk];
+  __shared__ float s_red[4];
+  __shared__ float s_sum;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const float* xr = x + (int64_t)blockIdx.x * axis;
+  float* yr = y + (int64_t)blockIdx.x * axis;
+  float mx = -INFINITY;
+  for (int64_t a = t; a < axis; a += 256) mx = fmaxf(mx, xr[a]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) s_red[w] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  float sum = 0.0f;  // lane 0 of wave 0 only
+  for (int64_t c0 = 0; c0 < axis; c0 += kSoftmaxChunk) {
+    const int n = (int)((axis - c0) < kSoftmaxChunk ? (axis - c0) : kSoftmaxChunk);
+    for (int j = t; j < n; j += 256) {
+      const float e = expf(xr[c0 + j] - mx);
+      s_e[j] = e;
+      yr[c0 + j] = e;
+    }
+    __syncthreads();
+    if (t == 0)
+      for (int j = 0; j < n; ++j) sum += s_e[j];
+    __syncthreads();
+  }
+  if (t == 0) s_sum = sum;
+  __syncthreads();
+  const float inv = 1.0f / s_sum;
+  for (int64_t c0 = 0; c0 < axis; c0 += kSoftmaxChunk) {
+    const int n = (int)((axis - c0) < kSoftmaxChunk ? (axis - c0) : kSoftmaxChunk);
+    for (int j = t; j < n; j += 256) yr[c0 + j] *= inv;
+  }
+}
+
+// y[m][n] = sum_k a[m][k] * b[k][n], the sum serial in k (the reference's
+// naive loop order) and without contraction.  16 x 16 outputs per workgroup,
+// one per thread; k advances through 16-wide tiles of a and b staged in LDS.
+constexpr int kMmTile = 16;
+
+__global__ __launch_bounds__(256) void matmul_kernel(float* __restrict__ y,
+                                                     const float* __restrict__ a,
+                                                     const float* __restrict__ b, int m, int k,
+                                                     int n) {
+#pragma clang fp contract(off)
+  __shared__ float s_a[kMmTile][kMmTile + 1];
+  __shared__ float s_b[kMmTile][kMmTile + 1];
+  const int tx = threadIdx.x & (kMmTile - 1), ty = threadIdx.x / kMmTile;
+  const int row = blockIdx.y * kMmTile + ty, col = blockIdx.x * kMmTile + tx;
+  float sum = 0.0f;
+  for (int k0 = 0; k0 < k; k0 += kMmTile) {
+    s_a[ty][tx] = (row < m && k0 + tx < k) ? a[(int64_t)row * k + k0 + tx] : 0.0f;
+    s_b[ty][tx] = (k0 + ty < k && col < n) ? b[(int64_t)(k0 + ty) * n + col] : 0.0f;
+    __syncthreads();
+    const int kt = (k - k0) < kMmTile ? (k - k0) : kMmTile;
+    for (int j = 0; j < kt; ++j) sum += s_a[ty][j] * s_b[j][tx];
+    __syncthreads();
+  }
+  if (row < m && col < n) y[(int64_t)row * n + col] = sum;
+}
+
+// y[n][m] = x[m][n]: 32 x 32 tiles through LDS (one padding column keeps the
+// transposed reads off a single bank), both sides coalesced.
+__global__ __launch_bounds__(256) void transpose_kernel(float* __restrict__ y,
+                                                        const float* __restrict__ x, int m,
+                                                        int n) {
+  __shared__ float s_t[32][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+  const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+  for (int r = ty; r < 32; r += 8)
+    if (r0 + r < m && c0 + tx < n) s_t[r][tx] = x[(int64_t)(r0 + r) * n + c0 + tx];
+  __syncthreads();
+  for (int c = ty; c < 32; c += 8)
+    if (c0 + c < n && r0 + tx < m) y[(int64_t)(c0 + c) * m + r0 + tx] = s_t[tx][c];
 }
 
 // One wave per row.  Without NaN: each lane scans its elements (i = lane,
@@ -419,6 +540,64 @@ extern "C" int rkv_add(float* y, const float* a, const float* b, int64_t n, void
   if (!y || !a || !b) return fail(RKV_ERR_INVALID_ARG, "rkv_add: null pointer argument");
   add_kernel<<<blocks_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(y, a, b, n);
   return check_launch("rkv_add");
+}
+
+extern "C" int rkv_mul_scalar(float* y, const float* x, float s, int64_t n, void* stream) {
+  clear_error();
+  if (n < 0) return fail(RKV_ERR_INVALID_ARG, "rkv_mul_scalar: n < 0");
+  if (n == 0) return RKV_OK;
+  if (!y || !x) return fail(RKV_ERR_INVALID_ARG, "rkv_mul_scalar: null pointer argument");
+  if (n > (int64_t)INT32_MAX * 256) return fail(RKV_ERR_INVALID_ARG, "rkv_mul_scalar: n too large");
+  mul_scalar_kernel<<<blocks_for(n, 256), 256, 0, static_cast<hipStream_t>(stream)>>>(y, x, s, n);
+  return check_launch("rkv_mul_scalar");
+}
+
+extern "C" int rkv_softmax_dim(float* y, const float* x, int64_t outer, int64_t axis,
+                               int64_t inner, void* stream) {
+  clear_error();
+  if (outer < 0 || inner < 0 || axis <= 0)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_softmax_dim: bad size argument (axis size must be > 0)");
+  if (outer == 0 || inner == 0) return RKV_OK;
+  if (!y || !x) return fail(RKV_ERR_INVALID_ARG, "rkv_softmax_dim: null pointer argument");
+  if (outer > INT64_MAX / axis || outer * axis > INT64_MAX / inner)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_softmax_dim: element count overflows int64");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (inner == 1) {
+    if (outer > INT32_MAX) return fail(RKV_ERR_INVALID_ARG, "rkv_softmax_dim: too many rows");
+    softmax_rows_kernel<<<(unsigned)outer, 256, 0, s>>>(y, x, axis);
+  } else {
+    const int64_t lines = outer * inner;
+    if (lines > (int64_t)INT32_MAX * 256)
+      return fail(RKV_ERR_INVALID_ARG, "rkv_softmax_dim: too many lines");
+    softmax_strided_kernel<<<blocks_for(lines, 256), 256, 0, s>>>(y, x, lines, axis, inner);
+  }
+  return check_launch("rkv_softmax_dim");
+}
+
+extern "C" int rkv_matmul(float* y, const float* a, const float* b, int m, int k, int n,
+                          void* stream) {
+  clear_error();
+  if (m < 0 || k < 0 || n < 0) return fail(RKV_ERR_INVALID_ARG, "rkv_matmul: bad size argument");
+  if (m == 0 || n == 0) return RKV_OK;
+  if (!y || (k > 0 && (!a || !b)))
+    return fail(RKV_ERR_INVALID_ARG, "rkv_matmul: null pointer argument");
+  if ((m + kMmTile - 1) / kMmTile > 65535)
+    return fail(RKV_ERR_INVALID_ARG, "rkv_matmul: m must be <= 1048560");
+  const dim3 grid(blocks_for(n, kMmTile), (unsigned)((m + kMmTile - 1) / kMmTile));
+  matmul_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(y, a, b, m, k, n);
+  return check_launch("rkv_matmul");
+}
+
+extern "C" int rkv_transpose(float* y, const float* x, int m, int n, void* stream) {
+  clear_error();
+  if (m < 0 || n < 0) return fail(RKV_ERR_INVALID_ARG, "rkv_transpose: bad size argument");
+  if (m == 0 || n == 0) return RKV_OK;
+  if (!y || !x) return fail(RKV_ERR_INVALID_ARG, "rkv_transpose: null pointer argument");
+  if (y == x) return fail(RKV_ERR_INVALID_ARG, "rkv_transpose: y must not alias x");
+  if ((m + 31) / 32 > 65535) return fail(RKV_ERR_INVALID_ARG, "rkv_transpose: m must be <= 2097120");
+  const dim3 grid(blocks_for(n, 32), (unsigned)((m + 31) / 32));
+  transpose_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(y, x, m, n);
+  return check_launch("rkv_transpose");
 }
 
 extern "C" int rkv_argmax(int32_t* out, const float* x, int rows, int n, void* stream) {

@@ -37,6 +37,31 @@ def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
     return t
 
 
+def check_attention_shapes(q_shape, pool_shape, tables_shape, lens_shape,
+                           q_start_shape=None) -> None:
+    """The shapes an attention call's kernels index by, checked before any
+    launch: q [rows, Hq, D] with D the pool's head_dim and Hq a multiple of
+    its KV heads; one block-table row and one length per sequence; q rows one
+    per sequence (decode) or q_start of B + 1 offsets (prefill).  The kernels
+    take sizes, not buffer lengths, so a mismatch would read past the tables
+    or write rows of the wrong width into the pools."""
+    hkv, d = pool_shape[1], pool_shape[3]
+    if len(q_shape) != 3 or len(tables_shape) != 2 or len(lens_shape) != 1:
+        raise ValueError("q, block_tables and ctx_lens must be rank 3, 2 and 1")
+    if q_shape[2] != d:
+        raise ValueError(f"q head_dim {q_shape[2]} does not match the pool's {d}")
+    if q_shape[1] == 0 or q_shape[1] % hkv:
+        raise ValueError(f"{q_shape[1]} query heads are not a multiple of {hkv} KV heads")
+    seqs = lens_shape[0]
+    if tables_shape[0] != seqs:
+        raise ValueError(f"{tables_shape[0]} block-table rows for {seqs} sequences")
+    if q_start_shape is None:
+        if q_shape[0] != seqs:
+            raise ValueError(f"{q_shape[0]} q rows for {seqs} sequences")
+    elif tuple(q_start_shape) != (seqs + 1,):
+        raise ValueError(f"q_start must hold {seqs + 1} offsets")
+
+
 def append(k_pool: torch.Tensor, v_pool: torch.Tensor, k_new: torch.Tensor,
            v_new: torch.Tensor, slot_mapping: torch.Tensor) -> None:
     """Scatter new K/V rows into the pools (every layer in one launch).
@@ -159,9 +184,8 @@ def decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     _dev(q, "q", torch.float32), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
     _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
     nb, hkv, bs, d = k_pool.shape
+    check_attention_shapes(q.shape, k_pool.shape, block_tables.shape, ctx_lens.shape)
     B, hq, dq = q.shape
-    if dq != d:
-        raise ValueError("q head_dim does not match the pool")
     mbs = block_tables.shape[1]
     if max_context is None:
         max_context = mbs * bs
@@ -211,8 +235,9 @@ def decode_attention_append(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch
     _dev(k_new, "k_new", torch.float32), _dev(v_new, "v_new", torch.float32)
     _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
     nb, hkv, bs, d = k_pool.shape
+    check_attention_shapes(q.shape, k_pool.shape, block_tables.shape, ctx_lens.shape)
     B, hq, dq = q.shape
-    if dq != d or tuple(k_new.shape) != (B, hkv, d) or tuple(v_new.shape) != (B, hkv, d):
+    if tuple(k_new.shape) != (B, hkv, d) or tuple(v_new.shape) != (B, hkv, d):
         raise ValueError("q, k_new and v_new must be [B, Hq, D], [B, Hkv, D], [B, Hkv, D]")
     mbs = block_tables.shape[1]
     if max_context is None:
@@ -324,8 +349,9 @@ def decode_attention_append_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: tor
     _dev(k_new, "k_new", torch.float32), _dev(v_new, "v_new", torch.float32)
     _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
     nb, hkv, bs, d = k_pool.shape
+    check_attention_shapes(q.shape, k_pool.shape, block_tables.shape, ctx_lens.shape)
     B, hq, dq = q.shape
-    if dq != d or tuple(k_new.shape) != (B, hkv, d) or tuple(v_new.shape) != (B, hkv, d):
+    if tuple(k_new.shape) != (B, hkv, d) or tuple(v_new.shape) != (B, hkv, d):
         raise ValueError("q, k_new and v_new must be [B, Hq, D], [B, Hkv, D], [B, Hkv, D]")
     mbs = block_tables.shape[1]
     if max_context is None:
@@ -338,7 +364,7 @@ def decode_attention_append_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: tor
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
-    ws_len = workspace.numel() if workspace is not None else 0
+    ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
     check(lib().rkv_decode_attention_append_q(
         out.data_ptr(), q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), k_scale.data_ptr(),
         v_scale.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), block_tables.data_ptr(), mbs,
@@ -358,6 +384,7 @@ def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tens
     _dev(v_scale, "v_scale", torch.float32)
     _dev(block_tables, "block_tables", torch.int32), _dev(ctx_lens, "ctx_lens", torch.int32)
     nb, hkv, bs, d = k_pool.shape
+    check_attention_shapes(q.shape, k_pool.shape, block_tables.shape, ctx_lens.shape)
     B, hq, _ = q.shape
     mbs = block_tables.shape[1]
     if max_context is None:
@@ -370,7 +397,7 @@ def decode_attention_q(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tens
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
-    ws_len = workspace.numel() if workspace is not None else 0
+    ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
     check(lib().rkv_decode_attention_q(out.data_ptr(), q.data_ptr(), k_pool.data_ptr(),
                                        v_pool.data_ptr(), k_scale.data_ptr(), v_scale.data_ptr(),
                                        block_tables.data_ptr(), mbs, ctx_lens.data_ptr(), B, hq,
@@ -396,10 +423,8 @@ def prefill_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tenso
     nb, hkv, bs, d = k_pool.shape
     total, hq, dq = q.shape
     B = ctx_lens.shape[0]
-    if dq != d:
-        raise ValueError("q head_dim does not match the pool")
-    if q_start.shape != (B + 1,) or block_tables.shape[0] != B:
-        raise ValueError("q_start must be [B+1] and block_tables [B, max_blocks]")
+    check_attention_shapes(q.shape, k_pool.shape, block_tables.shape, ctx_lens.shape,
+                           q_start.shape)
     if max_q_len is None:
         max_q_len = int((q_start[1:] - q_start[:-1]).max().item()) if B else 0
     if scale is None:

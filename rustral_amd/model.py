@@ -6,6 +6,7 @@ csrc/decoder.hip).
 from __future__ import annotations
 
 import ctypes as C
+import math
 
 import numpy as np
 import torch
@@ -311,6 +312,44 @@ def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def mul_scalar(x: torch.Tensor, s: float) -> torch.Tensor:
+    _dev(x, "x", torch.float32)
+    y = torch.empty_like(x)
+    check(lib().rkv_mul_scalar(y.data_ptr(), x.data_ptr(), s, x.numel(), _stream(x)))
+    return y
+
+
+def softmax_dim(x: torch.Tensor, dim: int) -> torch.Tensor:
+    """TensorOps::softmax_dim: softmax of x along dim (any rank; contiguous)."""
+    _dev(x, "x", torch.float32)
+    if not 0 <= dim < x.dim():
+        raise ValueError(f"softmax_dim: dim {dim} out of range for shape {tuple(x.shape)}")
+    outer = math.prod(x.shape[:dim])
+    inner = math.prod(x.shape[dim + 1:])
+    y = torch.empty_like(x)
+    check(lib().rkv_softmax_dim(y.data_ptr(), x.data_ptr(), outer, x.shape[dim], inner,
+                                _stream(x)))
+    return y
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    _dev(a, "a", torch.float32), _dev(b, "b", torch.float32)
+    (m, k), (k2, n) = a.shape, b.shape
+    if k != k2:
+        raise ValueError(f"matmul: inner sizes {k} and {k2} differ")
+    y = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    check(lib().rkv_matmul(y.data_ptr(), a.data_ptr(), b.data_ptr(), m, k, n, _stream(a)))
+    return y
+
+
+def transpose(x: torch.Tensor) -> torch.Tensor:
+    _dev(x, "x", torch.float32)
+    m, n = x.shape
+    y = torch.empty((n, m), dtype=torch.float32, device=x.device)
+    check(lib().rkv_transpose(y.data_ptr(), x.data_ptr(), m, n, _stream(x)))
+    return y
+
+
 def argmax(x: torch.Tensor) -> torch.Tensor:
     _dev(x, "x", torch.float32)
     rows, n = x.shape
@@ -333,4 +372,4 @@ def embed(table: torch.Tensor, ids: torch.Tensor, pe: torch.Tensor | None = None
 
 __all__ = ["DecoderConfig", "CONFIG0", "config", "param_count", "init_params", "rng_raw",
            "fill_normal", "Decoder", "linear", "layer_norm", "qkv_append", "gelu", "add", "argmax",
-           "embed"]
+           "embed", "mul_scalar", "softmax_dim", "matmul", "transpose"]

@@ -160,6 +160,45 @@ def test_prefill_rejects_bad_arguments():
                                    0.1, RKV_BF16, None) == RKV_ERR_INVALID_ARG
 
 
+def test_recipe_ops_reject_bad_arguments():
+    """rkv_softmax_dim / rkv_matmul / rkv_transpose / rkv_mul_scalar check
+    sizes and pointers before any launch; empty shapes are no-ops."""
+    L = _lib.lib()
+    assert L.rkv_softmax_dim(16, 16, 2, 0, 1, None) == RKV_ERR_INVALID_ARG  # axis size 0
+    assert "axis" in L.rkv_last_error().decode()
+    assert L.rkv_softmax_dim(16, 16, -1, 4, 1, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_softmax_dim(None, 16, 2, 4, 1, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_softmax_dim(16, 16, 1 << 40, 1 << 20, 1 << 10, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_softmax_dim(None, None, 0, 4, 1, None) == 0
+    assert L.rkv_matmul(16, 16, 16, -1, 2, 2, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_matmul(16, None, 16, 2, 2, 2, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_matmul(None, None, None, 0, 5, 3, None) == 0
+    assert L.rkv_transpose(16, 16, 4, 4, None) == RKV_ERR_INVALID_ARG  # aliasing
+    assert L.rkv_transpose(16, 32, -4, 4, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_mul_scalar(16, 16, 2.0, -1, None) == RKV_ERR_INVALID_ARG
+    assert L.rkv_mul_scalar(None, None, 2.0, 0, None) == 0
+
+
+def test_attention_shape_check_rejects_mismatches_before_a_launch():
+    """The host wrappers' shape check (the Rust crate's check_attention_shapes
+    states the same rules): the pool's head_dim, Hq a multiple of Hkv, one
+    table row and one length per sequence, B + 1 prefill offsets."""
+    from rustral_amd.kv import check_attention_shapes as chk
+    pool = (64, 8, 16, 128)
+    chk((4, 32, 128), pool, (4, 16), (4,))
+    chk((300, 32, 128), pool, (4, 16), (4,), (5,))
+    for q, t, n, qs in [((4, 32, 256), (4, 16), (4,), None),   # wider rows than the pool's
+                        ((4, 32, 64), (4, 16), (4,), None),
+                        ((4, 12, 128), (4, 16), (4,), None),   # Hq not a multiple of Hkv
+                        ((4, 32, 128), (3, 16), (4,), None),   # short tables
+                        ((4, 32, 128), (4, 16), (3,), None),   # short lengths
+                        ((5, 32, 128), (4, 16), (4,), None),
+                        ((300, 32, 128), (4, 16), (4,), (4,)),
+                        ((4, 32), (4, 16), (4,), None)]:
+        with pytest.raises(ValueError):
+            chk(q, pool, t, n, qs)
+
+
 def test_linear_rejects_rows_too_wide_for_staging():
     L = _lib.lib()
     assert L.rkv_linear(16, 16, 16, None, 1, 8193, 4, None) == RKV_ERR_UNSUPPORTED

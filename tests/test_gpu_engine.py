@@ -118,3 +118,40 @@ def test_engine_steps_on_after_an_out_of_memory_update(dev):
     for rid, (p, m) in zip(ids, reqs):
         want, _ = expected(params, p, m)
         assert eng.generated(rid) == want, f"request {rid}"
+
+
+def _config0_fixture():
+    import os
+    rows = {}
+    for line in open(os.path.join(os.path.dirname(__file__), "golden", "config0_tokens.txt")):
+        if not line.startswith("#"):
+            key, *vals = line.split()
+            rows[key] = [int(v) for v in vals]
+    return np.array(rows["prompt"], np.int32), rows["tokens"]
+
+
+def test_config0_fixture_through_decoder_and_engine(dev):
+    """What rust/rustral-rocm-backend/tests/model_parity.rs asserts, through
+    the same entry points: the decoder's tokens equal the committed oracle
+    fixture, one token at a time over a growing prefix too, and the engine
+    generates them for the same request beside a second one."""
+    say("config0 fixture: decoder, generate_token, engine")
+    cfg = model.config()
+    params = model.init_params(cfg, seed=0, std=0.02)
+    prompt, want = _config0_fixture()
+    dec = model.Decoder(cfg, params)
+    assert dec.generate(prompt, 64).tolist() == want
+    assert dec.generate(prompt, 64).tolist() == want
+    prefix = prompt.tolist()
+    for t in want[:8]:
+        assert int(dec.generate(np.array(prefix, np.int32), 1)[0]) == t
+        prefix.append(t)
+    eng = model.Engine(cfg, params, num_blocks=64, max_batch_size=4)
+    rid = eng.submit(prompt, 64)
+    other = eng.submit(prompt[:5], 10)
+    assert eng.run() >= 64
+    st = eng.scheduler.stats()
+    assert st["pending"] == st["running"] == st["paused"] == 0
+    assert eng.generated(rid) == want
+    assert len(eng.generated(other)) == 10
+    assert (st["completed"], st["total_tokens_generated"]) == (2, 74)

@@ -347,6 +347,102 @@ def test_gpu_argmax_matches_reference_rule(torch_dev):
 
 
 @pytest.mark.gpu
+def test_gpu_softmax_dim_matches_oracle(torch_dev):
+    """rkv_softmax_dim against the oracle's softmax_dim: the reference's golden
+    rows at its tolerance (crates/core/tests/golden_microblock_ops.rs:14-26,
+    rtol 1e-5 / atol 1e-6), random rows up to 4096 columns and past the
+    2048-entry sum chunk, every axis of a 3-d tensor, and the NaN / -inf rules."""
+    torch, dev = torch_dev
+    import json
+    import os
+    kat = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                      "reference_kats.json")))["softmax_dim1"]
+    rtol, atol = kat["tolerance"]["rtol"], kat["tolerance"]["atol"]
+
+    def close(got, want, what):
+        d = np.abs(got.astype(np.float64) - want)
+        assert (d <= atol + rtol * np.abs(want)).all(), f"{what}: max abs diff {d.max()}"
+
+    x = np.array(kat["input"], np.float32).reshape(kat["rows"], kat["cols"])
+    close(model.softmax_dim(torch.from_numpy(x).to(dev), 1).cpu().numpy(),
+          oracle.softmax_dim(x, 1), "golden")
+    rng = np.random.default_rng(9)
+    for rows, cols in [(1, 1), (3, 7), (64, 128), (5, 2048), (4, 2049), (2, 4096), (1, 70001)]:
+        x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+        got = model.softmax_dim(torch.from_numpy(x).to(dev), 1).cpu().numpy()
+        close(got, oracle.softmax_dim(x, 1), f"rows {rows} cols {cols}")
+    x = (rng.standard_normal((6, 33, 5)) * 3).astype(np.float32)
+    for dim in range(3):
+        got = model.softmax_dim(torch.from_numpy(x).to(dev), dim).cpu().numpy()
+        close(got, oracle.softmax_dim(x, dim), f"3-d dim {dim}")
+    odd = np.float32([[1.0, np.nan, 2.0, 0.5], [0.0, -np.inf, 3.0, 1.0],
+                      [-np.inf] * 4, [np.inf, 0.0, 1.0, 2.0]])
+    got = model.softmax_dim(torch.from_numpy(odd).to(dev), 1).cpu().numpy()
+    want = oracle.softmax_dim(odd, 1)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    close(got[fin], want[fin], "nan / inf rows")
+    with pytest.raises(Exception):
+        model.softmax_dim(torch.zeros((2, 0), device=dev), 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (2, 2, 2), (1, 128, 37), (33, 47, 129),
+                                   (64, 128, 2304), (5, 0, 3)])
+def test_gpu_matmul_transpose_mul_scalar_bit_exact(torch_dev, m, k, n):
+    """matmul in the naive loop's serial order, transpose and mul_scalar give
+    the oracle's bits (crates/ndarray-backend/src/lib.rs:208-219, :270-281,
+    :747-756)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(m * 1000 + k * 10 + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    ta, tb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    y = model.matmul(ta, tb).cpu().numpy()
+    assert np.array_equal(y.view(np.uint32), oracle.matmul(a, b).view(np.uint32))
+    if k:
+        assert np.array_equal(model.transpose(ta).cpu().numpy(), a.T)
+        assert np.array_equal(model.mul_scalar(ta, -0.0883883).cpu().numpy(),
+                              oracle.mul_scalar(a, -0.0883883))
+
+
+@pytest.mark.gpu
+def test_gpu_per_head_recipe_on_device_ops_matches_paged_decode(torch_dev):
+    """The reference's per-head recipe (tape_transformer.rs:87-139: q K^T,
+    * scale, softmax, @ V) composed from the device ops equals the oracle's
+    paged decode attention over the same K / V within 1e-4 / 1e-3."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(11)
+    hq, hkv, d, bs = 8, 2, 64, 16
+    ctx = np.array([1, 37, 300], np.int32)
+    need = (ctx + bs - 1) // bs
+    nb = int(need.sum())
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.full((len(ctx), int(need.max())), -1, np.int32)
+    o = 0
+    for i, c in enumerate(need):
+        tables[i, :c] = perm[o:o + c]
+        o += c
+    kp = rng.standard_normal((nb, hkv, bs, d)).astype(np.float32)
+    vp = rng.standard_normal((nb, hkv, bs, d)).astype(np.float32)
+    q = rng.standard_normal((len(ctx), hq, d)).astype(np.float32)
+    scale = 1 / math.sqrt(d)
+    want = oracle.decode_attention(q, kp, vp, tables, ctx, scale)
+    for b, L in enumerate(ctx):
+        rows = tables[b, np.arange(L) // bs], np.arange(L) % bs
+        for h in range(hq):
+            g = h // (hq // hkv)
+            k = np.ascontiguousarray(kp[rows[0], g, rows[1]])  # [L, D]
+            v = np.ascontiguousarray(vp[rows[0], g, rows[1]])
+            tq = torch.from_numpy(q[b, h][None]).to(dev)
+            s = model.matmul(tq, model.transpose(torch.from_numpy(k).to(dev)))
+            p = model.softmax_dim(model.mul_scalar(s, scale), 1)
+            out = model.matmul(p, torch.from_numpy(v).to(dev)).cpu().numpy()[0]
+            diff = np.abs(out - want[b, h])
+            assert ((diff <= 1e-4) | (diff <= 1e-3 * np.abs(want[b, h]))).all(), (b, h)
+
+
+@pytest.mark.gpu
 def test_gpu_decoder_pool_size_does_not_change_tokens(dev):
     """The same weights in decoders of max_seq 1024 and 128 (64 and 8 KV
     blocks per layer, other attention grids): tokens equal the CPU
@@ -396,3 +492,19 @@ def test_gpu_decoder_config0_tokens_equal_oracle(dev):
         got = dec.generate(p2, n_new)
         ref = oracle.decoder_generate(oracle.decoder_config(), params, p2, n_new)
         assert got.tolist() == ref.tolist(), (n_prompt, n_new)
+
+
+def test_config0_token_fixture_is_the_oracles():
+    """tests/golden/config0_tokens.txt (read by the Rust crate's test) holds
+    the oracle decoder's configs[0] tokens."""
+    import os
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_config0_tokens as mk
+    prompt, want = mk.tokens()
+    rows = {}
+    for line in open(os.path.join(os.path.dirname(__file__), "golden", "config0_tokens.txt")):
+        if not line.startswith("#"):
+            key, *vals = line.split()
+            rows[key] = [int(v) for v in vals]
+    assert rows["prompt"] == prompt.tolist() and rows["tokens"] == want.tolist()

@@ -61,6 +61,64 @@ def test_softmax_rows_reference_golden():
     assert np.allclose(got.sum(axis=1), 1.0, atol=1e-6)
 
 
+def _softmax_f64(x, axis):
+    x64 = x.astype(np.float64)
+    e = np.exp(x64 - x64.max(axis=axis, keepdims=True))
+    return e / e.sum(axis=axis, keepdims=True)
+
+
+def test_softmax_dim_reference_golden_and_every_axis():
+    k = KATS["softmax_dim1"]
+    x = np.array(k["input"], np.float32).reshape(k["rows"], k["cols"])
+    tol = (k["tolerance"]["rtol"], k["tolerance"]["atol"])
+    assert_allclose_ref(oracle.softmax_dim(x, 1), _softmax_f64(x, 1).astype(np.float32), *tol,
+                        "softmax_dim golden")
+    # a 3-d tensor of distinct sizes: each axis against numpy's along that axis,
+    # so an outer/inner stride slip or a wrong axis fails
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3, 5, 7)) * 4).astype(np.float32)
+    for dim in range(3):
+        got = oracle.softmax_dim(x, dim)
+        assert_allclose_ref(got, _softmax_f64(x, dim).astype(np.float32), *tol, f"dim {dim}")
+        assert np.allclose(got.sum(axis=dim), 1.0, atol=1e-6)
+    with pytest.raises(ValueError):
+        oracle.softmax_dim(np.zeros((2, 0), np.float32), 1)  # axis size 0 (lib.rs:1200-1202)
+
+
+def test_softmax_dim_nan_and_infinity_rules():
+    # f32::max skips a NaN operand, so the max is that of the other entries;
+    # exp(NaN - max) then makes the sum, and the whole line, NaN
+    y = oracle.softmax_dim(np.float32([[1.0, np.nan, 2.0]]), 1)
+    assert np.isnan(y).all()
+    # an all -inf line: max -inf, exp(-inf - -inf) = NaN
+    assert np.isnan(oracle.softmax_dim(np.full((1, 4), -np.inf, np.float32), 1)).all()
+    # a -inf entry among finite ones gets weight exactly 0
+    y = oracle.softmax_dim(np.float32([[0.0, -np.inf, 3.0]]), 1)
+    assert y[0, 1] == 0.0 and np.isclose(y[0].sum(), 1.0)
+
+
+def test_matmul_transpose_mul_scalar():
+    k = KATS["matmul_2x2"]
+    a = np.array(k["a"], np.float32).reshape(k["shape"])
+    b = np.array(k["b"], np.float32).reshape(k["shape"])
+    assert oracle.matmul(a, b).ravel().tolist() == k["expected"]
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((9, 37)).astype(np.float32)
+    b = rng.standard_normal((37, 13)).astype(np.float32)
+    y = oracle.matmul(a, b)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(y - want).max() < 1e-4 * np.abs(want).max()
+    # the serial order: row i of y is the float32 left-to-right sum of its products
+    for i, j in [(0, 0), (8, 12), (4, 7)]:
+        s = np.float32(0)
+        for kk in range(37):
+            s = np.float32(s + np.float32(a[i, kk] * b[kk, j]))
+        assert y[i, j] == s
+    assert np.array_equal(oracle.matmul(a, np.eye(37, dtype=np.float32)), a)  # identity
+    assert np.array_equal(oracle.transpose(a), a.T)
+    assert np.array_equal(oracle.mul_scalar(a, 0.125), a * np.float32(0.125))
+
+
 def test_argmax_reference_and_ties():
     g = KATS["greedy"]
     assert oracle.argmax(g["logits"]) == g["expected"]

@@ -192,3 +192,61 @@ def test_tensor_ops_implements_every_required_method(trait_method):
     text = open(os.path.join(CRATE, "src", "ops.rs")).read()
     impl = text[text.index("impl TensorOps<RocmBackend> for RocmOps"):text.index("impl AttentionOps")]
     assert re.search(rf"\b{trait_method}\(", impl), trait_method
+
+
+# The TensorOps the paged path, the config-0 model and the reference's
+# per-head attention recipe (crates/nn/src/tape_transformer.rs:87-139) call:
+# each must run on the device, i.e. be implemented by RocmOps (not left to a
+# trait default such as softmax_dim's "not supported", crates/core/src/
+# backend.rs:256-258) and not return the crate's `unsupported(..)` error.
+PATH_OPS = {
+    "zeros": None, "tensor_from_vec": None, "tensor_to_vec": None, "shape": None,
+    "reshape": None, "argmax": "rkv_argmax", "linear": "rkv_linear",
+    "gather_rows": "rkv_embed", "gelu": "rkv_gelu", "add": "rkv_add",
+    "softmax_dim": "rkv_softmax_dim", "softmax": "rkv_softmax_dim",
+    "matmul": "rkv_matmul", "transpose": "rkv_transpose", "mul_scalar": "rkv_mul_scalar",
+}
+
+
+def _method_bodies(impl: str) -> dict:
+    """Method name -> body text of every `fn` in an impl block."""
+    out = {}
+    for m in re.finditer(r"\n    fn (\w+)\s*[(<]", impl):
+        start = m.start()
+        nxt = re.search(r"\n    (?:///[^\n]*\n    )*fn \w+", impl[m.end():])
+        end = m.end() + nxt.start() if nxt else len(impl)
+        out[m.group(1)] = impl[start:end]
+    return out
+
+
+@pytest.mark.parametrize("op", sorted(PATH_OPS))
+def test_path_ops_run_on_the_device(op):
+    text = open(os.path.join(CRATE, "src", "ops.rs")).read()
+    impl = text[text.index("impl TensorOps<RocmBackend> for RocmOps"):text.index("impl AttentionOps")]
+    helpers = text[text.index("impl RocmOps"):text.index("impl TensorOps<RocmBackend>")]
+    bodies = _method_bodies(impl)
+    assert op in bodies, f"TensorOps::{op} is left to the trait default"
+    body = bodies[op]
+    assert "unsupported(" not in body, f"TensorOps::{op} returns the unsupported error"
+    entry = PATH_OPS[op]
+    if entry:
+        # the entry point is called in the body or in the RocmOps helper it uses
+        called = f"ffi::{entry}(" in body or any(
+            f"self.{h}(" in body and f"ffi::{entry}(" in hb
+            for h, hb in _method_bodies(helpers).items())
+        assert called, f"TensorOps::{op} does not call {entry}"
+
+
+def test_paged_calls_check_shapes_before_the_ffi_call():
+    """Every attention call of RocmPagedKvCache runs check_attention_shapes
+    before its first ffi:: call (a q of another head_dim, or short tables
+    or lengths, would otherwise reach the kernels)."""
+    text = open(os.path.join(CRATE, "src", "paged.rs")).read()
+    for fn in ("decode_attention", "decode_attention_append", "prefill_attention"):
+        m = re.search(rf"\n    pub fn {fn}\(", text)
+        assert m, fn
+        body = text[m.end():]
+        body = body[:body.index("\n    }\n")]
+        assert "check_attention_shapes(" in body, fn
+        assert body.index("check_attention_shapes(") < body.index("ffi::rkv_"), fn
+    assert "#[test]\n    fn mismatched_shapes_are_rejected_before_a_launch" in text
