@@ -3,7 +3,7 @@
 //! bit-exact, and decode attention over the paged cache matches the
 //! per-head recipe of tape_transformer.rs:87-139 computed with the ndarray
 //! backend's ops (matmul, mul_scalar, softmax_dim) within max-abs 1e-4 /
-//! rel 1e-3.
+//! rel 1e-3; the same recipe on this backend's device ops agrees too.
 use rustral_core::{Backend, TensorOps};
 use rustral_ndarray_backend::CpuBackend;
 use rustral_rocm_backend::{KvDtype, PagedKvConfig, RocmBackend, RocmPagedKvCache};
@@ -81,11 +81,22 @@ fn paged_append_gather_and_decode_match_the_cpu_backend() {
                 .map(|(p, e)| v[((row + p) * hkv + g) * d + e]).collect();
             let s = c.matmul(&qv, &c.tensor_from_vec(kt, &[d, l]).unwrap()).unwrap();
             let p = c.softmax_dim(&c.mul_scalar(&s, scale).unwrap(), 1).unwrap();
-            let o = c.tensor_to_vec(&c.matmul(&p, &c.tensor_from_vec(vm, &[l, d]).unwrap()).unwrap()).unwrap();
+            let o = c.tensor_to_vec(&c.matmul(&p, &c.tensor_from_vec(vm.clone(), &[l, d]).unwrap()).unwrap()).unwrap();
+            // the same recipe on the ROCm backend's own ops (matmul, transpose,
+            // mul_scalar, softmax_dim on the device)
+            let gqv = ops.tensor_from_vec(q[(b * hq + h) * d..(b * hq + h + 1) * d].to_vec(), &[1, d]).unwrap();
+            let gk_rows: Vec<f32> = (0..l).flat_map(|p| (0..d).map(move |e| (p, e)))
+                .map(|(p, e)| k[((row + p) * hkv + g) * d + e]).collect();
+            let gkt = ops.transpose(&ops.tensor_from_vec(gk_rows, &[l, d]).unwrap()).unwrap();
+            let gs = ops.mul_scalar(&ops.matmul(&gqv, &gkt).unwrap(), scale).unwrap();
+            let gp = ops.softmax_dim(&gs, 1).unwrap();
+            let go = ops.tensor_to_vec(&ops.matmul(&gp, &ops.tensor_from_vec(vm, &[l, d]).unwrap()).unwrap()).unwrap();
             for e in 0..d {
-                let (x, y) = (out[(b * hq + h) * d + e], o[e]);
-                let diff = (x - y).abs();
-                assert!(diff <= 1e-4 || diff <= 1e-3 * x.abs().max(y.abs()), "b {b} h {h} e {e}: {x} vs {y}");
+                let (x, y, z) = (out[(b * hq + h) * d + e], o[e], go[e]);
+                for (a, c2) in [(x, y), (z, y)] {
+                    let diff = (a - c2).abs();
+                    assert!(diff <= 1e-4 || diff <= 1e-3 * a.abs().max(c2.abs()), "b {b} h {h} e {e}: {a} vs {c2}");
+                }
             }
         }
         row += l;

@@ -1795,11 +1795,13 @@ extern "C" int rkv_decode_attention(float* out, const float* q, const void* k_po
                                     workspace_bytes, stream);
 }
 
-// Decode with the step's K/V append fused in (bf16 pools).  The partition
-// that holds position ctx_lens[b] - 1 stores the rounded new row into the
-// pools and stages the same bits in place of the pool's old row, so the
+// Decode with the step's K/V append fused in (bf16 pools).  In the partition
+// that holds position ctx_lens[b] - 1, the wave whose slice covers it stores
+// the rounded new row into the pools from the lanes whose ring loads read
+// that row, waits for the stores (vmcnt(0), that wave only), and then
+// streams its tiles as usual, reading the new row back with them; so the
 // result equals rkv_append of those rows followed by rkv_decode_attention,
-// bit for bit, in one launch fewer and without reading the row back.
+// bit for bit, in one launch fewer.
 extern "C" int rkv_decode_attention_append(
     float* out, const float* q, void* k_pool, void* v_pool, const float* k_new,
     const float* v_new, const int32_t* block_tables, int max_blocks_per_seq,

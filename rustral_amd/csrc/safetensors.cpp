@@ -8,6 +8,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cerrno>
 #include <cstdint>
 #include <cstdio>
@@ -242,6 +243,11 @@ std::unique_ptr<File> open(const char* path, std::string& err) {
     err = "safetensors: header is not a JSON object";
     return nullptr;
   }
+  ps.ws();  // the writer pads the header with spaces; anything else after it is an error
+  if (ps.p != ps.end) {
+    err = "safetensors: trailing characters after the header object";
+    return nullptr;
+  }
   f->data = bytes + 8 + hlen;
   f->data_len = size - 8 - hlen;
   std::set<std::string> seen;
@@ -289,6 +295,29 @@ std::unique_ptr<File> open(const char* path, std::string& err) {
     t.begin = (uint64_t)o0.num;
     t.end = (uint64_t)o1.num;
     f->tensors.push_back(std::move(t));
+  }
+  // The byte buffer is exactly the tensors' ranges laid end to end (the
+  // safetensors format's validation): sorted by offset, each begins where the
+  // previous ends, the first at 0 and the last at the end of the data -- no
+  // overlap, no gap, no trailing bytes.
+  std::vector<const Tensor*> order;
+  for (const Tensor& t : f->tensors) order.push_back(&t);
+  std::stable_sort(order.begin(), order.end(), [](const Tensor* a, const Tensor* b) {
+    return a->begin != b->begin ? a->begin < b->begin : a->end < b->end;
+  });
+  uint64_t at = 0;
+  for (const Tensor* t : order) {
+    if (t->begin != at) {
+      err = "safetensors: data of '" + t->name + "' " +
+            (t->begin < at ? "overlaps the previous tensor" : "leaves a gap after the previous tensor");
+      return nullptr;
+    }
+    at = t->end;
+  }
+  if (at != f->data_len) {
+    err = "safetensors: " + std::to_string(f->data_len - at) +
+          " data bytes past the last tensor";
+    return nullptr;
   }
   return f;
 }

@@ -314,8 +314,8 @@ def test_decode_append_fused_matches_append_then_decode(dev, max_context, P, hq,
     boundaries of every build, a sequence whose new block id is invalid (-1
     and past the pool: nothing written, the tile masked), an empty sequence,
     and (max_context 1000) sequences clamped below their length, whose rows
-    are not written.  P == 0 is also checked against the oracle on the
-    appended pool."""
+    are not written.  Every case is also checked against the oracle on the
+    appended pool, over the lengths clamped to max_context."""
     bs = 16
     ctx = np.array([1, 2, 16, 17, 640, 641, 768, 769, 1280, 1281, 4100, 0, 40, 50, 33],
                    np.int32)
@@ -347,6 +347,5 @@ def test_decode_append_fused_matches_append_then_decode(dev, max_context, P, hq,
     assert torch.equal(k2.view(torch.int16), k1.view(torch.int16)), "K pool differs"
     assert torch.equal(v2.view(torch.int16), v1.view(torch.int16)), "V pool differs"
     assert torch.equal(got, want), f"max diff {(got - want).abs().max().item()}"
-    if P == 0 and max_context is None:
-        ref = oracle.decode_attention(q, to_np(k1), to_np(v1), tables, ctx, scale)
-        assert_allclose_ref(to_np(got), ref, RTOL, ATOL, "fused append vs oracle")
+    ref = oracle.decode_attention(q, to_np(k1), to_np(v1), tables, np.minimum(ctx, cap), scale)
+    assert_allclose_ref(to_np(got), ref, RTOL, ATOL, "fused append vs oracle")

@@ -321,10 +321,11 @@ def test_decode_q_caller_partition_sizes(dev, fmt, P):
     assert_allclose_ref(to_np(out), want, RTOL, ATOL, f"1-byte partition {P} vs oracle")
 
 
-@pytest.mark.parametrize("P", [0, 256])
+@pytest.mark.parametrize("P", [0, 256, 640])
 @pytest.mark.parametrize("max_context", [None, 1000])
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64), (8, 1, 128), (16, 2, 64)])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 2, 64), (8, 1, 128), (16, 2, 64),
+                                      (8, 8, 128), (16, 8, 64)])
 def test_decode_append_q_fused_matches_append_q_then_decode_q(dev, P, max_context, fmt, hq,
                                                               hkv, d):
     """rkv_decode_attention_append_q == rkv_append_q of the new rows followed
@@ -333,7 +334,9 @@ def test_decode_append_q_fused_matches_append_q_then_decode_q(dev, P, max_contex
     and at partition boundaries, an all-zero row (scale 0), a row with a
     large value (fp8 saturation range), invalid block ids (-1 and past the
     pool: nothing written), an empty sequence, and lengths clamped by
-    max_context 1000 (their rows not written)."""
+    max_context 1000 (their rows not written); every G the kernels build
+    (1, 2, 4, 8).  The output is also checked against the oracle on the
+    dequantized appended pools, over the lengths clamped to max_context."""
     bs = 16
     ctx = np.array([1, 2, 16, 17, 640, 641, 1281, 0, 40, 50, 33, 256], np.int32)
     say(f"decode append_q fused fmt={fmt} P={P} hq={hq} hkv={hkv} d={d} max_context={max_context}")
@@ -370,3 +373,7 @@ def test_decode_append_q_fused_matches_append_q_then_decode_q(dev, P, max_contex
     assert torch.equal(t2.view(torch.int32), t1.view(torch.int32)), "V scales differ"
     assert torch.equal(got.view(torch.int32), want.view(torch.int32)), \
         f"max diff {(got - want).abs().max().item()}"
+    ref = oracle.decode_attention(q, oracle.dequantize_pool(to_np(k1), to_np(s1), CODE[fmt]),
+                                  oracle.dequantize_pool(to_np(v1), to_np(t1), CODE[fmt]), tables,
+                                  np.minimum(ctx, cap), scale)
+    assert_allclose_ref(to_np(got), ref, RTOL, ATOL, "fused 1-byte append vs oracle")

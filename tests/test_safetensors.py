@@ -161,6 +161,21 @@ def test_reader_rejects_malformed_headers(tmp_path):
         (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]},'
          b'"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}', b"\0" * 8, "duplicate entry"),
         (b'[1,2]', b"", "not a JSON object"),
+        # the data section is the tensors' ranges end to end, as the
+        # safetensors package's validation requires (crates/io/src/lib.rs:150
+        # loads through SafeTensors::deserialize)
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]},'
+         b'"b":{"dtype":"F32","shape":[2],"data_offsets":[4,12]}}', b"\0" * 12, "overlaps"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]},'
+         b'"b":{"dtype":"F32","shape":[2],"data_offsets":[12,20]}}', b"\0" * 20, "leaves a gap"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[4,12]}}', b"\0" * 12, "leaves a gap"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}', b"\0" * 12,
+         "4 data bytes past the last tensor"),
+        (b'{}', b"\0", "1 data bytes past the last tensor"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}x', b"\0" * 8,
+         "trailing characters"),
+        (b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}} {}', b"\0" * 8,
+         "trailing characters"),
     ]
     for i, (h, body, msg) in enumerate(cases):
         with pytest.raises(RkvError, match=msg):
@@ -169,3 +184,19 @@ def test_reader_rejects_malformed_headers(tmp_path):
     short.write_bytes(b"\x01\x02")
     with pytest.raises(RkvError, match="shorter than 8 bytes"):
         model.SafetensorsFile(short)
+
+
+def test_reader_accepts_space_padding_and_out_of_order_entries(tmp_path):
+    """Spaces after the header object (the writer's 8-byte padding) are
+    allowed, and header order need not be offset order: only the byte ranges
+    must tile the data section."""
+    h = (b'{"b":{"dtype":"F32","shape":[1],"data_offsets":[8,12]},'
+         b'"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}   ')
+    body = np.float32([1.0, 2.0, 3.0]).tobytes()
+    p = tmp_path / "ok.safetensors"
+    p.write_bytes(len(h).to_bytes(8, "little") + h + body)
+    with model.SafetensorsFile(p) as f:
+        assert set(f.entries()) == {"a", "b"}
+        out = {"a": np.empty(2, np.float32), "b": np.empty(1, np.float32)}
+        f.load(out)
+    assert out["a"].tolist() == [1.0, 2.0] and out["b"].tolist() == [3.0]
