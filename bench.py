@@ -50,7 +50,7 @@ def parse():
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
                    choices=["config0", "config1", "config2", "config3", "config4", "prefill",
-                            "decode_q", "device_step", "ceilings"],
+                            "decode_q", "device_step", "ceilings", "store_variants"],
                    help="config2 (default): the headline decode line; the others print "
                         "their own line (benchmark configs[0], [1], [3], [4])")
     return p.parse_args()
@@ -707,9 +707,9 @@ def run_config4(torch, dev, args):
     176 GB), blocks handed out one at a time round-robin by the host block
     manager (so finished sequences leave holes).  One step: 10% of the
     sequences finish (blocks freed), the block manager plans the relocation of
-    25% of the live blocks (rkv_bm_plan_migration: highest ids first into the
-    lowest free ids) and copy_blocks moves them (all layers, K and V, one
-    launch), 10% new sequences are admitted with 128-token prefills
+    25% of the live blocks (rkv_bm_plan_relocation: highest ids first into the
+    longest runs of free ids, both sides ascending) and copy_blocks moves them
+    (all layers, K and V, one launch), 10% new sequences are admitted with 128-token prefills
     appended in bulk (one launch for all layers) and run through causal
     prefill attention (one call per layer), then one decode token for every
     running sequence: append (one launch) + 32 decode-attention calls.
@@ -761,7 +761,7 @@ def run_config4(torch, dev, args):
             cache.free(i)
             del ctx[i]
         live = sum(len(cache.table(i)) for i in ctx)
-        pairs = cache.plan_migration(live // 4)
+        pairs = cache.plan_relocation(live // 4)
         assert len(pairs) == live // 4, "the pool is too small to relocate 25% of the live blocks"
         admitted = []
         for _ in range(n_fin):
@@ -1084,6 +1084,112 @@ def run_ceilings(torch, dev, args):
                  decode_int8_over_stream_1byte=round(d8["GBps"] / st8["GBps"], 4), results=res)
 
 
+def run_store_variants(torch, dev, args):
+    """Write and copy ceilings from writers other than the library's own
+    stream kernels: hipMemsetD32Async (eager), torch's fill_ and zero_,
+    hipMemcpyAsync device to device, and the store variants of
+    rustral_amd/ceiling (default or nontemporal store policy, one or two
+    16-byte vectors per lane, grid-stride interleave or one contiguous chunk
+    per workgroup, grids from one workgroup per CU to one-shot) over 4 GiB
+    buffers.  Rates count the bytes moved (a copy: read + written)."""
+    import ctypes
+    from rustral_amd import ceiling as C
+    reps = max(args.steps // 4, 5)
+    nbytes = 4 << 30
+    a = torch.full((nbytes // 4,), 1, dtype=torch.int32, device=dev)
+    b = torch.empty_like(a)
+    hip = ctypes.CDLL("libamdhip64.so.7")           # torch's runtime, already loaded
+    hip.hipMemsetD32Async.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t,
+                                      ctypes.c_void_p]
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                   ctypes.c_void_p]
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def rate(fn, moved):
+        fn()
+        ms = _timed(torch, fn, reps)
+        return round(moved / (ms * 1e-3) / 1e9, 1)
+
+    def memset():
+        assert hip.hipMemsetD32Async(b.data_ptr(), 0x3F800000, nbytes // 4, stream) == 0
+
+    def memcpy():
+        assert hip.hipMemcpyAsync(b.data_ptr(), a.data_ptr(), nbytes, 3, stream) == 0  # D2D
+    res = {"independent": {
+        "hipMemsetD32Async": rate(memset, nbytes),
+        "torch_fill_": rate(lambda: b.fill_(7), nbytes),
+        "torch_zero_": rate(lambda: b.zero_(), nbytes),
+        "hipMemcpyAsync_d2d": rate(memcpy, 2 * nbytes),
+        "torch_copy_": rate(lambda: b.copy_(a), 2 * nbytes),
+    }}
+    grids = [256, 512, 1024, 2048, 8192, 65536, 131072]   # the last two: one round per
+                                                           # workgroup for 2 / 1 vectors a lane
+    names = {0: "default", 1: "nt", 2: "x2", 3: "nt_x2", 4: "chunk", 5: "nt_chunk",
+             6: "x2_chunk", 7: "nt_x2_chunk"}
+    res["write"] = {f"{names[v]}@{g}": rate(lambda: C.write_var(torch, b, g, v), nbytes)
+                    for v in range(8) for g in grids}
+    # work per workgroup: unr x 4 KiB, one round each (2 GiB launches as
+    # torch's fill makes them, and 4 GiB), or grid-stride over 1-8 per CU
+    half = b[: b.numel() // 2]
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    res["read"] = {}
+    for unr in (1, 2, 4, 8, 16):
+        res["read"][f"unr{unr}_oneshot"] = rate(lambda: C.read_unr(torch, a, sink, unr), nbytes)
+        for g in (1024, 4096):
+            res["read"][f"unr{unr}@{g}"] = rate(lambda: C.read_unr(torch, a, sink, unr, g), nbytes)
+    for unr in (1, 2, 4, 8):
+        res["write"][f"unr{unr}_oneshot"] = rate(lambda: C.write_unr(torch, b, unr), nbytes)
+        res["write"][f"unr{unr}_oneshot_2GiB"] = rate(lambda: C.write_unr(torch, half, unr),
+                                                      nbytes // 2)
+        for g in (256, 1024, 2048):
+            res["write"][f"unr{unr}@{g}"] = rate(lambda: C.write_unr(torch, b, unr, g), nbytes)
+        for nt in (0, 1):
+            res.setdefault("copy_unr", {})[f"unr{unr}_oneshot{'_nt' if nt else ''}"] = rate(
+                lambda: C.copy_unr(torch, a, b, unr, 0, bool(nt)), 2 * nbytes)
+    res["copy"] = {}
+    for v in range(16):
+        nm = ("ntload_" if v & 8 else "") + names[v & 7]
+        for g in grids[3:]:
+            res["copy"][f"{nm}@{g}"] = rate(lambda: C.copy_var(torch, a, b, g, v), 2 * nbytes)
+    # 32 KiB block copies inside the 4 GiB buffer: which side's locality
+    # matters (a quarter of the blocks move; sources and destinations
+    # disjoint)
+    import numpy as np
+    blk = 32768
+    nblk = nbytes // blk
+    npairs = nblk // 4
+    rng = np.random.default_rng(3)
+    perm = rng.permutation(nblk).astype(np.int32)
+    lo = np.arange(npairs, dtype=np.int32)                       # a contiguous run
+    hi = np.arange(nblk // 2, nblk // 2 + npairs, dtype=np.int32)
+    rs, rd = perm[:npairs], perm[npairs:2 * npairs]              # random, disjoint
+    rs_hi = rs[(rs >= npairs)][:npairs // 2]                     # random, outside lo
+    patterns = {
+        "seq_src_seq_dst": (hi, lo),
+        "rand_src_seq_dst": (np.sort(rs_hi), lo[:len(rs_hi)]),
+        "rand_unsorted_src_seq_dst": (rs_hi, lo[:len(rs_hi)]),
+        "seq_src_rand_dst": (lo[:len(rs_hi)], np.sort(rs_hi)),
+        "rand_src_sorted_dst": (rs[np.argsort(rd)], np.sort(rd)),
+        "rand_src_rand_dst": (rs, rd),
+    }
+    res["block_copy"] = {}
+    a.fill_(1)
+    for name, (src, dst) in patterns.items():
+        pd = torch.from_numpy(np.ascontiguousarray(np.stack([src, dst], 1), dtype=np.int32)).to(dev)
+        moved = 2 * len(src) * blk
+        res["block_copy"][name] = rate(lambda: C.block_copy(torch, a, pd, blk), moved)
+        for unr in (1, 2, 4):
+            res["block_copy"][f"{name}_piece{4 * unr}k"] = rate(
+                lambda: C.block_copy_unr(torch, a, pd, blk, unr), moved)
+    best_w = max(res["write"].items(), key=lambda kv: kv[1])
+    best_c = max(res["copy"].items(), key=lambda kv: kv[1])
+    return _line("HBM write and copy ceilings: independent writers and store variants (4 GiB)",
+                 best_w[1], "GB/s", nbytes / best_w[1] / 1e6, args, "u8",
+                 {"workload": "flat 4 GiB writes and 4 GiB -> 4 GiB copies"},
+                 best_write=best_w[0], best_copy=best_c[0], best_copy_GBps=best_c[1],
+                 results=res)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1099,7 +1205,7 @@ def main():
         line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
                 "prefill": run_prefill, "decode_q": run_decode_q,
                 "config4": run_config4, "device_step": run_device_step,
-                "ceilings": run_ceilings}[args.workload](
+                "ceilings": run_ceilings, "store_variants": run_store_variants}[args.workload](
                     torch, dev, args)
         print(json.dumps(line), flush=True)
         return

@@ -92,6 +92,20 @@ int64_t rkv_bm_plan_compaction(rkv_block_manager* bm, int64_t max_moves, int32_t
 int64_t rkv_bm_plan_migration(rkv_block_manager* bm, int64_t max_moves, int32_t* pairs,
                               int64_t cap_pairs);
 
+/* Relocation plan: the blocks rkv_bm_plan_migration would move (the
+ * min(max_moves, live, free) highest live ids) go into the longest runs of
+ * consecutive free ids -- runs longest first, the lower start on ties, each
+ * filled from its low end -- and the i-th lowest source to the i-th lowest
+ * destination, so the pairs ascend on both sides.  rkv_copy_blocks then
+ * writes runs of consecutive blocks, which this part streams faster than
+ * scattered destinations (the writes, not the reads, decide a copy's rate).
+ * The free list afterwards holds the unused free ids and the vacated
+ * sources, sorted ascending.  Pairs and tables as for rkv_bm_plan_migration;
+ * sources and destinations are disjoint.  No reference counterpart (the
+ * reference only frees, crates/nn/src/continuous_batching.rs:380-386). */
+int64_t rkv_bm_plan_relocation(rkv_block_manager* bm, int64_t max_moves, int32_t* pairs,
+                               int64_t cap_pairs);
+
 /* ---- device-side block manager ----------------------------------------------
  * The same FIFO manager with its state in device memory: the free list is a
  * ring of block ids, the tables are an int32 [max_seqs][max_blocks_per_seq]

@@ -61,6 +61,31 @@ class PagedCacheRef:
     def plan_migration(self, max_moves: int):
         return self.plan_compaction(max_moves, below_only=False)
 
+    def plan_relocation(self, max_moves: int):
+        """plan_migration's sources into the longest free runs (longest first,
+        lower start on ties), i-th lowest source to i-th lowest destination."""
+        owner = {}
+        for s, t in self.block_tables.items():
+            for i, b in enumerate(t):
+                owner[b] = (s, i)
+        free = sorted(self.free_blocks)
+        n = min(max_moves, len(owner), len(free))
+        src = sorted(sorted(owner, reverse=True)[:n])
+        runs = []
+        for f in free:
+            if runs and runs[-1][0] + runs[-1][1] == f:
+                runs[-1][1] += 1
+            else:
+                runs.append([f, 1])
+        runs.sort(key=lambda r: (-r[1], r[0]))
+        dst = sorted([r[0] + x for r in runs for x in range(r[1])][:n])
+        for b, d in zip(src, dst):
+            s, i = owner[b]
+            self.block_tables[s][i] = d
+        taken = set(dst)
+        self.free_blocks = sorted([f for f in free if f not in taken] + src)
+        return list(zip(src, dst))
+
     def plan_compaction(self, max_moves: int, below_only: bool = True):
         owner = {}
         for s, t in self.block_tables.items():

@@ -550,6 +550,12 @@ extern "C" {
         pairs: *mut i32,
         cap_pairs: i64,
     ) -> i64;
+    pub fn rkv_bm_plan_relocation(
+        bm: *mut RkvBlockManager,
+        max_moves: i64,
+        pairs: *mut i32,
+        cap_pairs: i64,
+    ) -> i64;
     pub fn rkv_dbm_create(
         num_blocks: i64,
         block_size: c_int,

@@ -96,6 +96,18 @@ impl BlockManager {
     }
 }
 
+impl BlockManager {
+    /// Relocation plan: the blocks `plan_migration` would move, into the
+    /// longest runs of free ids (longest first), pairs ascending on both
+    /// sides so `copy_blocks` writes runs of consecutive blocks.
+    pub fn plan_relocation(&mut self, max_moves: usize) -> Vec<(usize, usize)> {
+        let mut pairs = vec![0i32; 2 * max_moves.max(1)];
+        // SAFETY: pairs holds 2 * max_moves entries.
+        let n = unsafe { ffi::rkv_bm_plan_relocation(self.h, max_moves as i64, pairs.as_mut_ptr(), max_moves as i64) };
+        (0..n.max(0) as usize).map(|i| (pairs[2 * i] as usize, pairs[2 * i + 1] as usize)).collect()
+    }
+}
+
 impl Drop for BlockManager {
     fn drop(&mut self) {
         // SAFETY: created by rkv_bm_create, destroyed once.

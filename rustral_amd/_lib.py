@@ -69,6 +69,7 @@ SIGNATURES = {
     "rkv_bm_fill_tables": (_i, [_p, _p, _i, _p, _i]),
     "rkv_bm_plan_compaction": (_i64, [_p, _i64, _p, _i64]),
     "rkv_bm_plan_migration": (_i64, [_p, _i64, _p, _i64]),
+    "rkv_bm_plan_relocation": (_i64, [_p, _i64, _p, _i64]),
     "rkv_sched_create": (_p, [_i64, _i, _i, _i]),
     "rkv_sched_destroy": (None, [_p]),
     "rkv_sched_add_request": (_i64, [_p, _p, _i, _i, _i]),

@@ -17,6 +17,14 @@ _SIG = {
     "rkvc_read": [C.c_void_p, C.c_int64, C.c_void_p, C.c_uint, C.c_int, C.c_void_p],
     "rkvc_write": [C.c_void_p, C.c_int64, C.c_int, C.c_void_p],
     "rkvc_copy": [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p],
+    "rkvc_write_var": [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p],
+    "rkvc_copy_var": [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p],
+    "rkvc_block_copy_pipe": [C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int, C.c_void_p],
+    "rkvc_read_unr": [C.c_void_p, C.c_int64, C.c_void_p, C.c_uint, C.c_int, C.c_int, C.c_void_p],
+    "rkvc_write_unr": [C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_void_p],
+    "rkvc_copy_unr": [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_void_p],
+    "rkvc_block_copy_unr": [C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_int,
+                            C.c_void_p],
     "rkvc_block_copy": [C.c_void_p, C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p],
     "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                          C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_void_p,
@@ -71,11 +79,64 @@ def copy(torch, src, dst, grid: int = 8192) -> None:
         "rkvc_copy")
 
 
+WRITE_NT, TWO_PER_LANE, CHUNKED, LOAD_NT = 1, 2, 4, 8
+
+
+def write_var(torch, buf, grid: int, variant: int) -> None:
+    """Flat write of buf with the variant bits WRITE_NT | TWO_PER_LANE | CHUNKED."""
+    _ok(lib().rkvc_write_var(buf.data_ptr(), buf.numel() * buf.element_size(), grid, variant,
+                             _stream(torch, buf.device)), "rkvc_write_var")
+
+
+def copy_var(torch, src, dst, grid: int, variant: int) -> None:
+    """Flat copy with the variant bits of write_var plus LOAD_NT."""
+    n = src.numel() * src.element_size()
+    assert dst.numel() * dst.element_size() >= n
+    _ok(lib().rkvc_copy_var(src.data_ptr(), dst.data_ptr(), n, grid, variant,
+                            _stream(torch, src.device)), "rkvc_copy_var")
+
+
 def block_copy(torch, pool, pairs, block_bytes: int) -> None:
     """pairs: int32 [n, 2] (src, dst) on the device; pool: the blocks."""
     nb = pool.numel() * pool.element_size() // block_bytes
     _ok(lib().rkvc_block_copy(pool.data_ptr(), pairs.data_ptr(), pairs.shape[0], block_bytes, nb,
                               _stream(torch, pool.device)), "rkvc_block_copy")
+
+
+def read_unr(torch, buf, sink, unr: int, grid: int = 0) -> None:
+    """Flat nontemporal read, unr 16-byte units a thread per round (grid 0:
+    one round per workgroup)."""
+    _ok(lib().rkvc_read_unr(buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
+                            0x9E3779B9, unr, grid, _stream(torch, buf.device)), "rkvc_read_unr")
+
+
+def write_unr(torch, buf, unr: int, grid: int = 0) -> None:
+    """Flat write, unr 16-byte units a thread per round (grid 0: one round
+    per workgroup)."""
+    _ok(lib().rkvc_write_unr(buf.data_ptr(), buf.numel() * buf.element_size(), unr, grid,
+                             _stream(torch, buf.device)), "rkvc_write_unr")
+
+
+def copy_unr(torch, src, dst, unr: int, grid: int = 0, nt: bool = True) -> None:
+    n = src.numel() * src.element_size()
+    assert dst.numel() * dst.element_size() >= n
+    _ok(lib().rkvc_copy_unr(src.data_ptr(), dst.data_ptr(), n, unr, grid, int(nt),
+                            _stream(torch, src.device)), "rkvc_copy_unr")
+
+
+def block_copy_unr(torch, pool, pairs, block_bytes: int, unr: int) -> None:
+    """Block copies split into (unr * 4 KiB)-byte pieces, one workgroup each."""
+    nb = pool.numel() * pool.element_size() // block_bytes
+    _ok(lib().rkvc_block_copy_unr(pool.data_ptr(), pairs.data_ptr(), pairs.shape[0], block_bytes,
+                                  nb, unr, _stream(torch, pool.device)), "rkvc_block_copy_unr")
+
+
+def block_copy_pipe(torch, pool, pairs, grid: int) -> None:
+    """32 KiB block copies, each workgroup a grid-stride run of pairs with the
+    next pair's loads issued before the current pair's stores."""
+    nb = pool.numel() * pool.element_size() // 32768
+    _ok(lib().rkvc_block_copy_pipe(pool.data_ptr(), pairs.data_ptr(), pairs.shape[0], nb, grid,
+                                   _stream(torch, pool.device)), "rkvc_block_copy_pipe")
 
 
 def tile_stream(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int,

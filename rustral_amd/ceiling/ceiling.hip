@@ -7,6 +7,9 @@
 //   rkvc_read         flat read, nontemporal 16-byte loads, grid-stride
 //   rkvc_write        flat write, 16-byte stores, grid-stride
 //   rkvc_copy         flat copy, nontemporal loads and stores
+//   rkvc_write_var    flat write variants: store policy, vectors per lane,
+//   rkvc_copy_var     interleaved or contiguous per workgroup (and load
+//                     policy for copies), at any grid size
 //   rkvc_block_copy   one workgroup per (src, dst) pair of fixed-size blocks
 //                     within one pool (the copy_blocks pattern)
 //   rkvc_tile_stream  the decode kernel's loads alone: grid (Hkv, partitions,
@@ -185,6 +188,176 @@ __global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
   if (acc == magic) sink[0] = acc;
 }
 
+// Block copies with the next pair's loads in flight while the current
+// pair's stores drain: workgroup g copies pairs g, g + grid, g + 2 grid, ...
+// (32 KiB blocks: 256 threads x 8 x 16 bytes, one round per block).
+__global__ __launch_bounds__(256) void block_copy_pipe_kernel(char* __restrict__ pool,
+                                                              const int32_t* __restrict__ pairs,
+                                                              int n_pairs, int64_t num_blocks) {
+  constexpr int64_t kBlk = 32768;
+  auto load = [&](int i, u32x4 (&x)[kUnr]) __attribute__((always_inline)) {
+    int32_t src = pairs[2 * i];
+    src = src >= 0 && src < num_blocks ? src : 0;
+    const u32x4* s = reinterpret_cast<const u32x4*>(pool + src * kBlk);
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) x[k] = ld<true>(s + k * 256 + threadIdx.x);
+  };
+  int i = blockIdx.x;
+  if (i >= n_pairs) return;
+  u32x4 cur[kUnr], nxt[kUnr];
+  load(i, cur);
+  for (; i < n_pairs; i += gridDim.x) {
+    const int j = i + gridDim.x;
+    if (j < n_pairs) load(j, nxt);
+    const int32_t src = pairs[2 * i], dst = pairs[2 * i + 1];
+    if (src >= 0 && src < num_blocks && dst >= 0 && dst < num_blocks) {
+      u32x4* d = reinterpret_cast<u32x4*>(pool + dst * kBlk);
+#pragma unroll
+      for (int k = 0; k < kUnr; ++k) st<true>(d + k * 256 + threadIdx.x, cur[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) cur[k] = nxt[k];
+  }
+}
+
+// Work per workgroup: UNR 16-byte units a thread (UNR * 4 KiB a workgroup),
+// wave-contiguous 1 KiB stores; grid-stride, so a grid of n / (256 UNR)
+// workgroups is one round each.
+template <int UNR>
+__global__ __launch_bounds__(256) void write_unr_kernel(u32x4* __restrict__ d, int64_t n) {
+  const u32x4 v = {threadIdx.x, blockIdx.x, 0x3f800000u, 0u};
+  const int64_t stride = (int64_t)gridDim.x * 256 * UNR;
+  for (int64_t u0 = (int64_t)blockIdx.x * 256 * UNR + threadIdx.x; u0 < n; u0 += stride) {
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) st<false>(d + u, v);
+    }
+  }
+}
+
+template <int UNR>
+__global__ __launch_bounds__(256) void read_unr_kernel(const u32x4* __restrict__ s, int64_t n,
+                                                       unsigned* sink, unsigned magic) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * UNR;
+  unsigned acc = 0;
+  for (int64_t u0 = (int64_t)blockIdx.x * 256 * UNR + threadIdx.x; u0 < n; u0 += stride) {
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) acc ^= fold(ld<true>(s + u));
+    }
+  }
+  if (acc == magic) sink[0] = acc;
+}
+
+template <int UNR, bool NT>
+__global__ __launch_bounds__(256) void copy_unr_kernel(const u32x4* __restrict__ s,
+                                                       u32x4* __restrict__ d, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256 * UNR;
+  for (int64_t u0 = (int64_t)blockIdx.x * 256 * UNR + threadIdx.x; u0 < n; u0 += stride) {
+    u32x4 x[UNR];
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) x[k] = ld<true>(s + u);
+    }
+#pragma unroll
+    for (int k = 0; k < UNR; ++k) {
+      const int64_t u = u0 + k * 256;
+      if (u < n) st<NT>(d + u, x[k]);
+    }
+  }
+}
+
+// Block copies with B-byte pieces per workgroup: grid (pieces of a block,
+// pairs), each workgroup one round of UNR units a thread.
+template <int UNR>
+__global__ __launch_bounds__(256) void block_copy_unr_kernel(char* __restrict__ pool,
+                                                             const int32_t* __restrict__ pairs,
+                                                             int64_t block_bytes,
+                                                             int64_t num_blocks) {
+  const int32_t src = pairs[2 * blockIdx.y], dst = pairs[2 * blockIdx.y + 1];
+  if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) return;
+  const int64_t off = (int64_t)blockIdx.x * 256 * UNR;
+  const u32x4* sp = reinterpret_cast<const u32x4*>(pool + src * block_bytes) + off;
+  u32x4* dp = reinterpret_cast<u32x4*>(pool + dst * block_bytes) + off;
+  u32x4 x[UNR];
+#pragma unroll
+  for (int k = 0; k < UNR; ++k) x[k] = ld<true>(sp + k * 256 + threadIdx.x);
+#pragma unroll
+  for (int k = 0; k < UNR; ++k) st<true>(dp + k * 256 + threadIdx.x, x[k]);
+}
+
+// Store and copy variants (the write side of every copy):
+//   NT      nontemporal (streaming) stores instead of the default policy
+//   VPL     16-byte vectors per lane per step: 1, or 2 adjacent (32 bytes)
+//   CHUNK   each workgroup owns one contiguous 1/grid of the buffer instead
+//           of the grid-stride interleave (a persistent grid of one or a few
+//           workgroups per CU then walks long sequential runs)
+// NTL (copies) selects nontemporal loads.  Every variant writes every
+// 16-byte unit of the buffer exactly once.
+template <bool NT, int VPL, bool CHUNK>
+__global__ __launch_bounds__(256) void write_var_kernel(u32x4* __restrict__ d, int64_t n) {
+  const u32x4 v = {threadIdx.x, blockIdx.x, 0x3f800000u, 0u};
+  constexpr int64_t STEP = 256 * kUnr * VPL;  // units per workgroup round
+  int64_t lo, hi, stride;
+  if constexpr (CHUNK) {
+    const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+    lo = (int64_t)blockIdx.x * per;
+    hi = lo + per < n ? lo + per : n;
+    stride = STEP;
+  } else {
+    lo = (int64_t)blockIdx.x * STEP;
+    hi = n;
+    stride = (int64_t)gridDim.x * STEP;
+  }
+  for (int64_t r = lo; r < hi; r += stride) {
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int64_t u = r + ((int64_t)k * 256 + threadIdx.x) * VPL + j;
+        if (u < hi) st<NT>(d + u, v);
+      }
+    }
+  }
+}
+
+template <bool NTL, bool NTS, int VPL, bool CHUNK>
+__global__ __launch_bounds__(256) void copy_var_kernel(const u32x4* __restrict__ s,
+                                                       u32x4* __restrict__ d, int64_t n) {
+  constexpr int64_t STEP = 256 * kUnr * VPL;
+  int64_t lo, hi, stride;
+  if constexpr (CHUNK) {
+    const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+    lo = (int64_t)blockIdx.x * per;
+    hi = lo + per < n ? lo + per : n;
+    stride = STEP;
+  } else {
+    lo = (int64_t)blockIdx.x * STEP;
+    hi = n;
+    stride = (int64_t)gridDim.x * STEP;
+  }
+  for (int64_t r = lo; r < hi; r += stride) {
+    u32x4 x[kUnr][VPL];
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k)
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int64_t u = r + ((int64_t)k * 256 + threadIdx.x) * VPL + j;
+        if (u < hi) x[k][j] = ld<NTL>(s + u);
+      }
+#pragma unroll
+    for (int k = 0; k < kUnr; ++k)
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int64_t u = r + ((int64_t)k * 256 + threadIdx.x) * VPL + j;
+        if (u < hi) st<NTS>(d + u, x[k][j]);
+      }
+  }
+}
+
 // The launch's own status: an error left by an earlier runtime call of the
 // process is cleared before the launch (clear_errors), so it is not
 // reported as this launch's.  Returns 0 or the positive hipError_t code.
@@ -217,6 +390,145 @@ int rkvc_copy(const void* src, void* dst, int64_t bytes, int grid, void* stream)
   clear_errors();
   copy_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), bytes >> 4);
+  return launched();
+}
+
+// variant bits: 1 NT stores, 2 two vectors per lane, 4 contiguous chunk per
+// workgroup; copies add 8 for nontemporal loads.
+int rkvc_write_var(void* dst, int64_t bytes, int grid, int variant, void* stream) {
+  if (!dst || bytes < 16 || (bytes & 15) || grid <= 0 || variant < 0 || variant > 7) return -1;
+  clear_errors();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  u32x4* d = static_cast<u32x4*>(dst);
+  const int64_t n = bytes >> 4;
+  switch (variant) {
+    case 0: write_var_kernel<false, 1, false><<<grid, 256, 0, st>>>(d, n); break;
+    case 1: write_var_kernel<true, 1, false><<<grid, 256, 0, st>>>(d, n); break;
+    case 2: write_var_kernel<false, 2, false><<<grid, 256, 0, st>>>(d, n); break;
+    case 3: write_var_kernel<true, 2, false><<<grid, 256, 0, st>>>(d, n); break;
+    case 4: write_var_kernel<false, 1, true><<<grid, 256, 0, st>>>(d, n); break;
+    case 5: write_var_kernel<true, 1, true><<<grid, 256, 0, st>>>(d, n); break;
+    case 6: write_var_kernel<false, 2, true><<<grid, 256, 0, st>>>(d, n); break;
+    default: write_var_kernel<true, 2, true><<<grid, 256, 0, st>>>(d, n); break;
+  }
+  return launched();
+}
+
+int rkvc_copy_var(const void* src, void* dst, int64_t bytes, int grid, int variant,
+                  void* stream) {
+  if (!src || !dst || bytes < 16 || (bytes & 15) || grid <= 0 || variant < 0 || variant > 15)
+    return -1;
+  clear_errors();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const u32x4* s = static_cast<const u32x4*>(src);
+  u32x4* d = static_cast<u32x4*>(dst);
+  const int64_t n = bytes >> 4;
+#define RKVC_COPY(V, NTL, NTS, VPL, CH) \
+  case V: copy_var_kernel<NTL, NTS, VPL, CH><<<grid, 256, 0, st>>>(s, d, n); break;
+  switch (variant) {
+    RKVC_COPY(0, false, false, 1, false) RKVC_COPY(1, false, true, 1, false)
+    RKVC_COPY(2, false, false, 2, false) RKVC_COPY(3, false, true, 2, false)
+    RKVC_COPY(4, false, false, 1, true) RKVC_COPY(5, false, true, 1, true)
+    RKVC_COPY(6, false, false, 2, true) RKVC_COPY(7, false, true, 2, true)
+    RKVC_COPY(8, true, false, 1, false) RKVC_COPY(9, true, true, 1, false)
+    RKVC_COPY(10, true, false, 2, false) RKVC_COPY(11, true, true, 2, false)
+    RKVC_COPY(12, true, false, 1, true) RKVC_COPY(13, true, true, 1, true)
+    RKVC_COPY(14, true, false, 2, true) default: copy_var_kernel<true, true, 2, true>
+        <<<grid, 256, 0, st>>>(s, d, n); break;
+  }
+#undef RKVC_COPY
+  return launched();
+}
+
+int rkvc_block_copy_pipe(void* pool, const int32_t* pairs, int n_pairs, int64_t num_blocks,
+                         int grid, void* stream) {
+  if (!pool || !pairs || n_pairs <= 0 || num_blocks <= 0 || grid <= 0) return -1;
+  clear_errors();
+  block_copy_pipe_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<char*>(pool), pairs, n_pairs, num_blocks);
+  return launched();
+}
+
+// unr in {1, 2, 4, 8}; grid 0: one round per workgroup.  copy: nt stores when
+// variant & 1.
+int rkvc_write_unr(void* dst, int64_t bytes, int unr, int grid, void* stream) {
+  if (!dst || bytes < 16 || (bytes & 15) || grid < 0) return -1;
+  const int64_t n = bytes >> 4;
+  const int64_t g = grid ? grid : (n + 256 * unr - 1) / (256 * unr);
+  if (g > INT32_MAX) return -1;
+  clear_errors();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  u32x4* d = static_cast<u32x4*>(dst);
+  switch (unr) {
+    case 1: write_unr_kernel<1><<<(unsigned)g, 256, 0, st>>>(d, n); break;
+    case 2: write_unr_kernel<2><<<(unsigned)g, 256, 0, st>>>(d, n); break;
+    case 4: write_unr_kernel<4><<<(unsigned)g, 256, 0, st>>>(d, n); break;
+    case 8: write_unr_kernel<8><<<(unsigned)g, 256, 0, st>>>(d, n); break;
+    default: return -1;
+  }
+  return launched();
+}
+
+int rkvc_read_unr(const void* src, int64_t bytes, unsigned* sink, unsigned magic, int unr,
+                  int grid, void* stream) {
+  if (!src || !sink || bytes < 16 || (bytes & 15) || grid < 0) return -1;
+  const int64_t n = bytes >> 4;
+  const int64_t g = grid ? grid : (n + 256 * unr - 1) / (256 * unr);
+  if (g > INT32_MAX) return -1;
+  clear_errors();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const u32x4* s = static_cast<const u32x4*>(src);
+  switch (unr) {
+    case 1: read_unr_kernel<1><<<(unsigned)g, 256, 0, st>>>(s, n, sink, magic); break;
+    case 2: read_unr_kernel<2><<<(unsigned)g, 256, 0, st>>>(s, n, sink, magic); break;
+    case 4: read_unr_kernel<4><<<(unsigned)g, 256, 0, st>>>(s, n, sink, magic); break;
+    case 8: read_unr_kernel<8><<<(unsigned)g, 256, 0, st>>>(s, n, sink, magic); break;
+    case 16: read_unr_kernel<16><<<(unsigned)g, 256, 0, st>>>(s, n, sink, magic); break;
+    default: return -1;
+  }
+  return launched();
+}
+
+int rkvc_copy_unr(const void* src, void* dst, int64_t bytes, int unr, int grid, int nt,
+                  void* stream) {
+  if (!src || !dst || bytes < 16 || (bytes & 15) || grid < 0) return -1;
+  const int64_t n = bytes >> 4;
+  const int64_t g = grid ? grid : (n + 256 * unr - 1) / (256 * unr);
+  if (g > INT32_MAX) return -1;
+  clear_errors();
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const u32x4* s = static_cast<const u32x4*>(src);
+  u32x4* d = static_cast<u32x4*>(dst);
+#define RKVC_CU(U) \
+  case U: \
+    if (nt) copy_unr_kernel<U, true><<<(unsigned)g, 256, 0, st>>>(s, d, n); \
+    else copy_unr_kernel<U, false><<<(unsigned)g, 256, 0, st>>>(s, d, n); \
+    break;
+  switch (unr) {
+    RKVC_CU(1) RKVC_CU(2) RKVC_CU(4) RKVC_CU(8)
+    default: return -1;
+  }
+#undef RKVC_CU
+  return launched();
+}
+
+// block_bytes a multiple of 4096 * unr.
+int rkvc_block_copy_unr(void* pool, const int32_t* pairs, int n_pairs, int64_t block_bytes,
+                        int64_t num_blocks, int unr, void* stream) {
+  if (!pool || !pairs || n_pairs <= 0 || n_pairs > 65535 || block_bytes <= 0 ||
+      num_blocks <= 0 || (unr != 1 && unr != 2 && unr != 4 && unr != 8) ||
+      block_bytes % (4096 * unr))
+    return -1;
+  clear_errors();
+  const dim3 grid((unsigned)(block_bytes / (4096 * unr)), (unsigned)n_pairs);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* p = static_cast<char*>(pool);
+  switch (unr) {
+    case 1: block_copy_unr_kernel<1><<<grid, 256, 0, st>>>(p, pairs, block_bytes, num_blocks); break;
+    case 2: block_copy_unr_kernel<2><<<grid, 256, 0, st>>>(p, pairs, block_bytes, num_blocks); break;
+    case 4: block_copy_unr_kernel<4><<<grid, 256, 0, st>>>(p, pairs, block_bytes, num_blocks); break;
+    default: block_copy_unr_kernel<8><<<grid, 256, 0, st>>>(p, pairs, block_bytes, num_blocks); break;
+  }
   return launched();
 }
 

@@ -81,11 +81,6 @@ __device__ __forceinline__ uint4 f8_to_bf16x8(const F8& x) {
                     pack_bf16x2(x.b.x, x.b.y), pack_bf16x2(x.b.z, x.b.w));
 }
 
-__device__ __forceinline__ F8 bf16x8_to_f8(const uint4& w) {
-  return F8{make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)),
-            make_float4(bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w))};
-}
-
 // ---- append -----------------------------------------------------------------
 // grid = (n_tokens, n_layers); each thread moves 8 elements of K and of V.
 // The source rows do not depend on the slot, so the first chunk's K/V loads
@@ -137,26 +132,44 @@ __global__ __launch_bounds__(256) void append_kernel(
 }
 
 // ---- gather -----------------------------------------------------------------
-// grid = (max_blocks_per_seq, num_seqs, 2 [K,V]).  One workgroup copies the
-// valid rows of logical block j of sequence b for every head.  The block's
-// (block, head) tiles are consecutive in the pool, so its rows (every head)
-// are one run of num_kv_heads * block_size rows; rows past the context (the
-// sequence's last block) are skipped.  A unit is 16 bytes of output (8
-// elements of a 16-bit output, 4 of an fp32 one) and its source elements:
-// consecutive lanes take consecutive units, so both the loads and the stores
-// of a wave are contiguous runs (an fp32 output from a bf16 pool: 512-byte
-// wave-loads, 1 KiB wave-stores).  DT is head_dim for the 32 / 64 / 128
-// builds (shifts), 0 for any other multiple of 8.
-template <typename TIn, typename TOut, int DT>
+// grid = (max_blocks_per_seq * (Hkv / HPW) * ppt, num_seqs, 2 [K,V]).  A
+// unit is 16 bytes of output (8 elements of a 16-bit output, 4 of an fp32
+// one) and its source elements; a (block, head) tile of block_size rows is
+// ppt pieces of 256 units.  One workgroup moves piece `piece` of HPW
+// consecutive heads' tiles of one block: HPW units a thread, every load
+// issued before the first store.  Consecutive lanes take consecutive units
+// of a tile, so loads and stores of a wave are contiguous runs: a tile's
+// rows are contiguous in the pool and, for one head, in the output.  Rows
+// past the context (the sequence's last block) are not stored.  DT is
+// head_dim for the 32 / 64 / 128 builds (shifts), 0 for any other multiple
+// of 8.  configs[1]'s gather (us per call; bf16 -> bf16, bf16 -> fp32,
+// fp32 -> fp32) by heads per workgroup HPW and pieces PPW: HPW 1 212 /
+// 421 / 480, 2 194 / 299 / 404, 4 198 / 332 / 433, 8 207 / 314 / 426; PPW 2
+// (a whole fp32 tile) with HPW 1 303 / 401, with HPW 2 307 / 425.  So 8 KiB
+// of output per workgroup; the previous kernel, a whole block (8 heads, 8-16
+// units a thread), ran 195 / 301 / 430.
+#ifndef RKV_GATHER_HPW
+#define RKV_GATHER_HPW 2  // heads (tiles) per workgroup, up to num_kv_heads
+#endif
+#ifndef RKV_GATHER_PPW
+#define RKV_GATHER_PPW 1  // pieces of each tile per workgroup
+#endif
+template <typename TIn, typename TOut, int DT, int HPW, int PPW>
 __global__ __launch_bounds__(256) void gather_kernel(
     TOut* __restrict__ k_out, TOut* __restrict__ v_out, const TIn* __restrict__ k_pool,
     const TIn* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
     const int64_t* __restrict__ out_offsets, int num_kv_heads, int head_dim, int block_size,
-    int bs_log2, int64_t num_blocks, int max_ctx) {
+    int ppt, int64_t num_blocks, int max_ctx) {
   constexpr int EPU = 16 / sizeof(TOut);  // elements per unit
   const int D = DT ? DT : head_dim;
-  const int j = blockIdx.x, b = blockIdx.y;
+  const int hg = num_kv_heads / HPW;   // head groups
+  const int ppb = hg * ppt;            // workgroups per block (ppt: this launch's pieces
+                                       // per tile, each PPW of the tile's 256-unit pieces)
+  const int j = blockIdx.x / ppb;
+  const int rem = blockIdx.x - j * ppb;
+  const int h0 = (rem / ppt) * HPW, piece = rem - (rem / ppt) * ppt;
+  const int b = blockIdx.y;
   const bool is_v = blockIdx.z != 0;
   // the three per-sequence reads are independent: issued together
   int L = ctx_lens[b];
@@ -178,105 +191,77 @@ __global__ __launch_bounds__(256) void gather_kernel(
   if (p0 >= L) return;
   if (blk < 0 || blk >= num_blocks) return;
   const int nt = (L - p0) < block_size ? (L - p0) : block_size;
-  const int upr = D / EPU;  // units per row
-  const int rows = num_kv_heads * block_size;
-  const int units = rows * upr;
-  const TIn* __restrict__ src = (is_v ? v_pool : k_pool) + (int64_t)blk * rows * D;
-  TOut* __restrict__ dst = (is_v ? v_out : k_out) + seq_base + (int64_t)p0 * D;
-  // Up to UNR units per thread per round: every load of the round is issued
-  // before the first store, so a thread keeps UNR loads in flight.
-  constexpr int UNR = sizeof(TIn) < sizeof(TOut) ? 16 : 8;
+  const int upr = D / EPU;          // units per row
+  const int tu = block_size * upr;  // units per tile
   constexpr int LB = EPU * sizeof(TIn);  // bytes loaded per unit: 16, or 8 (bf16 -> fp32)
   using In = typename std::conditional<LB == 16, uint4, uint2>::type;
   constexpr bool NTL = RKV_GATHER_NT && sizeof(TIn) == 2;
   constexpr bool NTS = RKV_GATHER_NT && (sizeof(TOut) == 2 || RKV_GATHER_NTS_F32);
-  // P2: the block size is a power of two (unit -> head and row by shifts;
-  // the choice is made once, outside the unrolled loops)
-  auto run = [&](auto p2, auto masked) __attribute__((always_inline)) {
-    constexpr bool P2 = decltype(p2)::value;
-    constexpr bool MASKED = decltype(masked)::value;
-    // unit -> (head, row within the block, unit within the row)
-    auto split = [&](int u, int& h, int& rr, int& c) __attribute__((always_inline)) {
-      const int row = u / upr;
-      c = u - row * upr;
-      h = P2 ? row >> bs_log2 : row / block_size;
-      rr = row - h * block_size;
-    };
-    for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {  // 256 threads
-      // Loads without branches: a unit past the block (u >= units) reads the
-      // block's last unit instead, and rows past the context are rows of the
-      // same block, so every load is in bounds; only the stores are
-      // conditional.  (Loads under branches left the compiler unable to
-      // count them, and it waited for all memory operations before every
-      // store.)
-      uint4 y[UNR];  // the 16 output bytes of each unit
+  const TIn* base = (is_v ? v_pool : k_pool) + ((int64_t)blk * num_kv_heads + h0) * block_size * D;
+  const int64_t tile = (int64_t)block_size * D;  // elements per tile
+  uint4 y[PPW][HPW];
 #pragma unroll
-      for (int k = 0; k < UNR; ++k) {
-        const int u = u0 + k * 256;
-        const int uc = u < units ? u : units - 1;
-        const In* p = reinterpret_cast<const In*>(src + (int64_t)uc * EPU);
-        In x;
-        if constexpr (LB == 16)
-          x = ld16<NTL>(p);
-        else if constexpr (NTL)
-          x = __builtin_bit_cast(In,
-                                 __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p)));
-        else
-          x = *p;
-        if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4)
-          y[k] = make_uint4(x.x << 16, x.x & 0xffff0000u, x.y << 16, x.y & 0xffff0000u);
-        else
-          y[k] = x;
-      }
+  for (int q = 0; q < PPW; ++q) {
+    const int u = (piece * PPW + q) * 256 + threadIdx.x;
+    // loads are unconditional (a unit past the tile re-reads its last
+    // unit) so each store waits for its own load only
+    const int uc = u < tu ? u : tu - 1;
 #pragma unroll
-      for (int k = 0; k < UNR; ++k) {
-        const int u = u0 + k * 256;
-        int h, rr, c;
-        split(u, h, rr, c);
-        if (!MASKED || (u < units && rr < nt))
-          store16<NTS>(dst + ((int64_t)h * row_stride + rr) * D + c * EPU, y[k]);
-      }
+    for (int k = 0; k < HPW; ++k) {
+      const TIn* src = base + k * tile + (int64_t)uc * EPU;
+      In x;
+      if constexpr (LB == 16)
+        x = ld16<NTL>(src);
+      else if constexpr (NTL)
+        x = __builtin_bit_cast(In, __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(src)));
+      else
+        x = *reinterpret_cast<const In*>(src);
+      if constexpr (sizeof(TIn) == 2 && sizeof(TOut) == 4)
+        y[q][k] = make_uint4(x.x << 16, x.x & 0xffff0000u, x.y << 16, x.y & 0xffff0000u);
+      else
+        y[q][k] = x;
     }
-  };
-  // A full block whose units fill whole rounds stores without conditions,
-  // so the compiler's wait counts follow the loads and stores in order (a
-  // store under a branch made it wait for every earlier store at the end
-  // of a round).
-  if (nt == block_size && units % (UNR * 256) == 0) {
-    if (bs_log2 >= 0) run(std::true_type{}, std::false_type{});
-    else run(std::false_type{}, std::false_type{});
-  } else {
-    if (bs_log2 >= 0) run(std::true_type{}, std::true_type{});
-    else run(std::false_type{}, std::true_type{});
+  }
+  TOut* out = (is_v ? v_out : k_out) + seq_base + ((int64_t)h0 * row_stride + p0) * D;
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    const int u = (piece * PPW + q) * 256 + threadIdx.x;
+    const int rr = u / upr, c = u - rr * upr;
+    if (u < tu && rr < nt) {
+#pragma unroll
+      for (int k = 0; k < HPW; ++k)
+        store16<NTS>(out + ((int64_t)k * row_stride + rr) * D + c * EPU, y[q][k]);
+    }
   }
 }
 
 // ---- copy_blocks --------------------------------------------------------------
-// grid = (n_pairs, n_layers, 2 [K,V]); each workgroup copies one block.
+// grid = (n_pairs * pieces, n_layers, 2 [K,V]); a piece is 4 KiB of a block
+// (pieces = ceil(block_bytes / 4096): a bf16 block of 8 heads x 16 rows x
+// 128 dims is 8 pieces, one per (block, head) tile) and each workgroup moves
+// one piece: one 16-byte load and one 16-byte store per thread, one round.
+// Measured on this part (32 KiB blocks in a 4 GiB pool, GB/s moved): the
+// same pairs copied 32 KiB per workgroup (8 loads then 8 stores a thread)
+// ran 5.97-6.06 with contiguous destinations and 5.28 with sparse sorted
+// ones; in 4 KiB pieces 6.37-6.41 and 5.67 (flat 4 GiB copies: 8 units a
+// thread 5.29, one 6.43).  The smaller the work per workgroup, the fewer
+// bytes the resident workgroups have in flight at once, and the fewer DRAM
+// rows the writes keep open.
+constexpr int kCopyPiece = 4096;  // bytes per workgroup
+
 __global__ __launch_bounds__(256) void copy_blocks_kernel(
     char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t layer_stride_bytes,
-    const int32_t* __restrict__ pairs, int64_t block_bytes, int64_t num_blocks) {
-  const int i = blockIdx.x, layer = blockIdx.y;
+    const int32_t* __restrict__ pairs, int64_t block_bytes, int pieces, int64_t num_blocks) {
+  const int64_t g = blockIdx.x;
+  const int64_t i = g / pieces;
+  const int piece = (int)(g - i * pieces);
   const int32_t src = pairs[2 * i], dst = pairs[2 * i + 1];
   if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) return;
-  char* base = (blockIdx.z ? v_pool : k_pool) + layer * layer_stride_bytes;
-  const uint4* s = reinterpret_cast<const uint4*>(base + src * block_bytes);
-  uint4* d = reinterpret_cast<uint4*>(base + dst * block_bytes);
-  const int64_t n = block_bytes >> 4;
-  constexpr int UNR = 8;  // loads in flight per thread before the stores
-  for (int64_t u0 = threadIdx.x; u0 < n; u0 += UNR * blockDim.x) {
-    uint4 x[UNR];
-#pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int64_t u = u0 + k * blockDim.x;
-      if (u < n) x[k] = ld16<RKV_COPY_NTL>(s + u);
-    }
-#pragma unroll
-    for (int k = 0; k < UNR; ++k) {
-      const int64_t u = u0 + k * blockDim.x;
-      if (u < n) store16<RKV_COPY_NTS>(d + u, x[k]);
-    }
-  }
+  const int64_t off = (int64_t)piece * kCopyPiece + threadIdx.x * 16;
+  if (off >= block_bytes) return;  // the last piece of a block of another size
+  char* base = (blockIdx.z ? v_pool : k_pool) + blockIdx.y * layer_stride_bytes;
+  const uint4 x = ld16<RKV_COPY_NTL>(base + src * block_bytes + off);
+  store16<RKV_COPY_NTS>(base + dst * block_bytes + off, x);
 }
 
 // ---- 1-byte storage (int8 / fp8 e4m3, one fp32 scale per row) ---------------
@@ -345,34 +330,43 @@ __global__ __launch_bounds__(256) void append_q_kernel(
   }
 }
 
-// gather_q: grid = (max_blocks_per_seq, num_seqs, 2 [K,V]); like gather_kernel,
-// one workgroup per logical block of a sequence, K or V.  The block's
-// (block, head) tiles are consecutive in the pool, so its rows (every head)
-// are one run of num_kv_heads * block_size rows of D bytes, with their scales
-// one run of floats.  A thread turns one 4-byte word of a row into one
-// float4 (byte value * row scale): consecutive lanes take consecutive words,
-// so a wave-load reads 256 contiguous bytes and a wave-store writes 1 KiB of
-// one head's contiguous output rows (writing 16 floats per lane, the stores
-// of a wave were 64 bytes apart and the kernel streamed at half the rate).
-// Every load of a thread's share is issued before its first store; rows
-// past the context (the sequence's last block) are skipped.
-// Ordinary loads and nontemporal stores: 302-310 us at configs[2] (int8 /
-// fp8) against 314-324 us for the other three combinations.
+// gather_q: a thread turns one 4-byte word of a row into one float4 (byte
+// value * row scale): consecutive lanes take consecutive words, so a
+// wave-load reads 256 contiguous bytes and a wave-store writes 1 KiB of one
+// head's contiguous output rows (writing 16 floats per lane, the stores of
+// a wave were 64 bytes apart and the kernel streamed at half the rate).
+// Rows past the context (the sequence's last block) are skipped.  Ordinary
+// loads and nontemporal stores: 302-310 us at configs[2] (int8 / fp8)
+// against 314-324 us for the other three combinations, with a whole block
+// (16 words a thread) per workgroup.
 #ifndef RKV_GATHER_Q_NTL
 #define RKV_GATHER_Q_NTL 0
 #endif
 #ifndef RKV_GATHER_Q_NTS
 #define RKV_GATHER_Q_NTS 1
 #endif
-template <int D, int FMT>
+// grid = (max_blocks_per_seq * (Hkv / HPW) * ppt, num_seqs, 2 [K,V]): one
+// piece of 256 words of HPW consecutive heads' (block, head) tiles per
+// workgroup, HPW words (4 bytes in, 16 bytes of fp32 out each) per thread,
+// one round (a 16 x 128 tile is two pieces).  configs[1]'s gather over
+// 1-byte pools (us per call, int8 / fp8): HPW 1 493 / 505, 2 288 / 293,
+// 4 262 / 257, 8 271 / 276.
+#ifndef RKV_GATHER_Q_HPW
+#define RKV_GATHER_Q_HPW 4
+#endif
+template <int D, int FMT, int HPW>
 __global__ __launch_bounds__(256) void gather_q_kernel(
     float* __restrict__ k_out, float* __restrict__ v_out, const uint8_t* __restrict__ k_pool,
     const uint8_t* __restrict__ v_pool, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
-    const int64_t* __restrict__ out_offsets, int num_kv_heads, int block_size, int bs_log2,
+    const int64_t* __restrict__ out_offsets, int num_kv_heads, int block_size, int ppt,
     int64_t num_blocks, int max_ctx) {
-  const int j = blockIdx.x, b = blockIdx.y;
+  const int ppb = (num_kv_heads / HPW) * ppt;
+  const int j = blockIdx.x / ppb;
+  const int rem = blockIdx.x - j * ppb;
+  const int h0 = (rem / ppt) * HPW, piece = rem - (rem / ppt) * ppt;
+  const int b = blockIdx.y;
   const bool is_v = blockIdx.z != 0;
   int L = ctx_lens[b];
   const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + j];
@@ -394,68 +388,35 @@ __global__ __launch_bounds__(256) void gather_q_kernel(
   if (blk < 0 || blk >= num_blocks) return;
   const int nt = (L - p0) < block_size ? (L - p0) : block_size;
   constexpr int U = D / 4;  // words per row
-  const int rows = num_kv_heads * block_size;
-  const int units = rows * U;
-  const uint32_t* __restrict__ src =
-      reinterpret_cast<const uint32_t*>((is_v ? v_pool : k_pool) + (int64_t)blk * rows * D);
-  const float* __restrict__ sc = (is_v ? v_scale : k_scale) + (int64_t)blk * rows;
-  float* __restrict__ dst = (is_v ? v_out : k_out) + seq_base + (int64_t)p0 * D;
-  constexpr int UNR = 16;  // words in flight per thread
-  // Loads without branches (a unit past the block reads the block's last
-  // word; rows past the context are rows of the same block), and the
-  // power-of-two test made once.  For int8 pools a full block that fills
-  // whole rounds also stores without conditions: branches around the loads
-  // or stores left the compiler waiting for every earlier memory operation
-  // before each store (the fp8 decode, ~8 VALU per byte, measured faster
-  // with each conversion kept beside its conditional store).
-  auto run = [&](auto p2, auto masked) __attribute__((always_inline)) {
-    constexpr bool P2 = decltype(p2)::value;
-    constexpr bool MASKED = decltype(masked)::value;
-    // row -> (head, row within the block)
-    auto split = [&](int row, int& h, int& rr) __attribute__((always_inline)) {
-      h = P2 ? row >> bs_log2 : row / block_size;
-      rr = row - h * block_size;
-    };
-    for (int u0 = threadIdx.x; u0 < units; u0 += UNR * 256) {  // 256 threads
-      uint32_t w[UNR];
-      float sk[UNR];
+  const int tu = block_size * U;  // words per tile
+  const int64_t row0 = ((int64_t)blk * num_kv_heads + h0) * block_size;  // first row of head h0
+  const int u = piece * 256 + threadIdx.x;
+  const int uc = u < tu ? u : tu - 1;  // loads are unconditional (the tile's last word)
+  const uint32_t* src = reinterpret_cast<const uint32_t*>((is_v ? v_pool : k_pool) + row0 * D);
+  const float* sc = (is_v ? v_scale : k_scale) + row0;
+  uint32_t w[HPW];
+  float sk[HPW];
 #pragma unroll
-      for (int k = 0; k < UNR; ++k) {
-        const int u = u0 + k * 256;
-        const int uc = u < units ? u : units - 1;
-        if constexpr (RKV_GATHER_Q_NTL) w[k] = __builtin_nontemporal_load(src + uc);
-        else w[k] = src[uc];
-        sk[k] = sc[uc / U];
+  for (int k = 0; k < HPW; ++k) {
+    if constexpr (RKV_GATHER_Q_NTL) w[k] = __builtin_nontemporal_load(src + k * tu + uc);
+    else w[k] = src[k * tu + uc];
+    sk[k] = sc[k * block_size + uc / U];
+  }
+  const int rr = u / U, c = u - rr * U;
+  if (u < tu && rr < nt) {
+    float* dst = (is_v ? v_out : k_out) + seq_base + ((int64_t)h0 * row_stride + p0 + rr) * D + 4 * c;
+#pragma unroll
+    for (int k = 0; k < HPW; ++k) {
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t byte = (w[k] >> (8 * e)) & 0xffu;
+        f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3((uint8_t)byte)) * sk[k];
       }
-#pragma unroll
-      for (int k = 0; k < UNR; ++k) {
-        const int u = u0 + k * 256;
-        const int row = u / U, c = u - row * U;
-        int h, rr;
-        split(row, h, rr);
-        if (!MASKED || (u < units && rr < nt)) {
-          float f[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t byte = (w[k] >> (8 * e)) & 0xffu;
-            f[e] = (FMT == RKV_I8 ? (float)(int8_t)byte : f32_from_e4m3((uint8_t)byte)) * sk[k];
-          }
-          store16<RKV_GATHER_Q_NTS>(dst + ((int64_t)h * row_stride + rr) * D + 4 * c,
-                                    make_float4(f[0], f[1], f[2], f[3]));
-        }
-      }
-    }
-  };
-  const bool whole = nt == block_size && units % (UNR * 256) == 0;
-  if constexpr (FMT == RKV_I8) {
-    if (whole) {
-      if (bs_log2 >= 0) run(std::true_type{}, std::false_type{});
-      else run(std::false_type{}, std::false_type{});
-      return;
+      store16<RKV_GATHER_Q_NTS>(dst + (int64_t)k * row_stride * D,
+                                make_float4(f[0], f[1], f[2], f[3]));
     }
   }
-  if (bs_log2 >= 0) run(std::true_type{}, std::true_type{});
-  else run(std::false_type{}, std::true_type{});
 }
 
 int check_common(int num_kv_heads, int head_dim, int block_size, int64_t num_blocks, int dtype) {
@@ -530,14 +491,36 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
     return fail(RKV_ERR_INVALID_ARG, "padded output needs max_ctx > 0");
   if (!aligned16(k_out) || !aligned16(v_out) || !aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
-  dim3 grid((unsigned)max_blocks_per_seq, (unsigned)num_seqs, 2);
+  const int epu = out_dtype == RKV_F32 ? 4 : 8;  // output elements per 16-byte unit
+  const int64_t pieces = ((int64_t)block_size * (head_dim / epu) + 255) / 256;
+  const int ppw = pieces % RKV_GATHER_PPW == 0 ? RKV_GATHER_PPW : 1;
+  const int64_t ppt = pieces / ppw;  // workgroups per tile
+  // heads per workgroup: the build's choice when it divides num_kv_heads
+  const int hpw = num_kv_heads % RKV_GATHER_HPW == 0 ? RKV_GATHER_HPW
+                  : num_kv_heads % 4 == 0 && RKV_GATHER_HPW > 4 ? 4
+                  : num_kv_heads % 2 == 0 && RKV_GATHER_HPW > 2 ? 2 : 1;
+  const int64_t gx = (int64_t)max_blocks_per_seq * (num_kv_heads / hpw) * ppt;
+  if (gx > INT32_MAX)
+    return fail(RKV_ERR_INVALID_ARG, "max_blocks_per_seq * num_kv_heads * tile pieces exceeds 2^31 - 1");
+  dim3 grid((unsigned)gx, (unsigned)num_seqs, 2);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int bs_log2 = (block_size & (block_size - 1)) ? -1 : __builtin_ctz((unsigned)block_size);
-#define RKV_GATHER_D(TI, TO, DT)                                                               \
-  gather_kernel<TI, TO, DT><<<grid, 256, 0, s>>>(                                              \
+#define RKV_GATHER_HP(TI, TO, DT, H, P)                                                        \
+  gather_kernel<TI, TO, DT, H, P><<<grid, 256, 0, s>>>(                                        \
       static_cast<TO*>(k_out), static_cast<TO*>(v_out), static_cast<const TI*>(k_pool),        \
       static_cast<const TI*>(v_pool), block_tables, max_blocks_per_seq, ctx_lens, out_offsets, \
-      num_kv_heads, head_dim, block_size, bs_log2, num_blocks, max_ctx)
+      num_kv_heads, head_dim, block_size, (int)ppt, num_blocks, max_ctx)
+#define RKV_GATHER_H(TI, TO, DT, H)                                    \
+  do {                                                                 \
+    if (ppw == RKV_GATHER_PPW) RKV_GATHER_HP(TI, TO, DT, H, RKV_GATHER_PPW); \
+    else RKV_GATHER_HP(TI, TO, DT, H, 1);                              \
+  } while (0)
+#define RKV_GATHER_D(TI, TO, DT)                                                     \
+  do {                                                                               \
+    if (hpw == RKV_GATHER_HPW) RKV_GATHER_H(TI, TO, DT, RKV_GATHER_HPW);             \
+    else if (hpw == 4) RKV_GATHER_H(TI, TO, DT, (RKV_GATHER_HPW > 4 ? 4 : 1));       \
+    else if (hpw == 2) RKV_GATHER_H(TI, TO, DT, (RKV_GATHER_HPW > 2 ? 2 : 1));       \
+    else RKV_GATHER_H(TI, TO, DT, 1);                                                \
+  } while (0)
 #define RKV_GATHER(TI, TO)                       \
   do {                                           \
     if (head_dim == 128) RKV_GATHER_D(TI, TO, 128); \
@@ -553,6 +536,8 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
     RKV_GATHER(uint16_t, uint16_t);
 #undef RKV_GATHER
 #undef RKV_GATHER_D
+#undef RKV_GATHER_H
+#undef RKV_GATHER_HP
   return check_launch("rkv_gather");
 }
 
@@ -633,14 +618,25 @@ extern "C" int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, cons
     return fail(RKV_ERR_INVALID_ARG, "padded output needs max_ctx > 0");
   if (!aligned16(k_out) || !aligned16(v_out) || !aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
-  const dim3 grid((unsigned)max_blocks_per_seq, (unsigned)num_seqs, 2);
+  const int64_t ppt = ((int64_t)block_size * (head_dim / 4) + 255) / 256;
+  const int hpw = num_kv_heads % RKV_GATHER_Q_HPW == 0 ? RKV_GATHER_Q_HPW
+                  : num_kv_heads % 2 == 0 && RKV_GATHER_Q_HPW > 2 ? 2 : 1;
+  const int64_t gx = (int64_t)max_blocks_per_seq * (num_kv_heads / hpw) * ppt;
+  if (gx > INT32_MAX)
+    return fail(RKV_ERR_INVALID_ARG, "max_blocks_per_seq * num_kv_heads * tile pieces exceeds 2^31 - 1");
+  const dim3 grid((unsigned)gx, (unsigned)num_seqs, 2);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int bs_log2 = (block_size & (block_size - 1)) ? -1 : __builtin_ctz((unsigned)block_size);
-#define RKV_GATHER_Q(D, F)                                                                      \
-  gather_q_kernel<D, F><<<grid, 256, 0, s>>>(                                                   \
+#define RKV_GATHER_QH(D, F, H)                                                                  \
+  gather_q_kernel<D, F, H><<<grid, 256, 0, s>>>(                                                \
       k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),   \
       k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,  \
-      block_size, bs_log2, num_blocks, max_ctx)
+      block_size, (int)ppt, num_blocks, max_ctx)
+#define RKV_GATHER_Q(D, F)                                                   \
+  do {                                                                       \
+    if (hpw == RKV_GATHER_Q_HPW) RKV_GATHER_QH(D, F, RKV_GATHER_Q_HPW);      \
+    else if (hpw == 2) RKV_GATHER_QH(D, F, (RKV_GATHER_Q_HPW > 2 ? 2 : 1));  \
+    else RKV_GATHER_QH(D, F, 1);                                             \
+  } while (0)
   if (dtype == RKV_I8) {
     if (head_dim == 32) RKV_GATHER_Q(32, RKV_I8);
     else if (head_dim == 64) RKV_GATHER_Q(64, RKV_I8);
@@ -651,6 +647,7 @@ extern "C" int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, cons
     else RKV_GATHER_Q(128, RKV_FP8);
   }
 #undef RKV_GATHER_Q
+#undef RKV_GATHER_QH
   return check_launch("rkv_gather_q");
 }
 
@@ -668,9 +665,12 @@ extern "C" int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_
     return fail(RKV_ERR_INVALID_ARG, "layer_stride_bytes must be a multiple of 16");
   if (!aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG, "pools must be 16-byte aligned");
-  dim3 grid((unsigned)n_pairs, (unsigned)n_layers, 2);
+  const int64_t pieces = (block_bytes + kCopyPiece - 1) / kCopyPiece;
+  if ((int64_t)n_pairs * pieces > INT32_MAX)
+    return fail(RKV_ERR_INVALID_ARG, "n_pairs * ceil(block_bytes / 4096) exceeds 2^31 - 1");
+  dim3 grid((unsigned)(n_pairs * pieces), (unsigned)n_layers, 2);
   copy_blocks_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<char*>(k_pool), static_cast<char*>(v_pool), layer_stride_bytes, pairs,
-      block_bytes, num_blocks);
+      block_bytes, (int)pieces, num_blocks);
   return check_launch("rkv_copy_blocks");
 }

@@ -24,8 +24,8 @@
 //     dims, then lanes of different rows are summed by shuffles).  The waves
 //     of a partition combine their states through LDS.
 //   * int8 pools (G <= 4) keep both products on the integer matrix cores:
-//     q and the PV weights are split into three int8 limbs (fixed point
-//     against the head's maximum, ~22 bits), the stored bytes enter
+//     q and the PV weights are split into four int8 limbs (fixed point
+//     against the head's maximum, ~31 bits), the stored bytes enter
 //     v_mfma_i32_16x16x64_i8 / _16x16x32_i8 unconverted and the int32 sums
 //     are exact; fp8 pools convert their bytes to bf16 (exact).
 // Pass 2 (decode_merge_kernel): per (query head, sequence) merge of the
@@ -201,9 +201,9 @@ __device__ __forceinline__ float lo_col(float x) {
 #ifndef RKV_DECODE_K_LDS
 #define RKV_DECODE_K_LDS 1
 #endif
-// int8 pools: QK^T on v_mfma_i32_16x16x64_i8 with q in three int8 limbs (1)
+// int8 pools: QK^T on v_mfma_i32_16x16x64_i8 with q in four int8 limbs (1)
 // or on the bf16 MFMA with the K bytes converted (0); PV on
-// v_mfma_i32_16x16x32_i8 with the weights in three int8 limbs (1) or on the
+// v_mfma_i32_16x16x32_i8 with the weights in four int8 limbs (1) or on the
 // bf16 MFMA with the V bytes converted (0).
 #ifndef RKV_DECODE_I8_QK
 #define RKV_DECODE_I8_QK 1
@@ -290,18 +290,21 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
   // which keeps the staging buffer at one tile.
   constexpr bool MPV = MFMA;
   // int8 pools (G <= 4): QK^T on the integer matrix cores, exact in int32.
-  // q of head h is written as (M_h / 127) (a0 + a1 / 254 + a2 / 254^2) with
-  // M_h = max |q| over the head's dims and int8 limbs a0, a1, a2 (round to
-  // nearest at each step; with the fp32 roundings of q * 127 / M_h and of
-  // the residuals, |q - that sum| < M_h 2^-22), the limbs are rows
-  // 4 h + j of A, and B is the stored K bytes as they are.  Row 4 h + j of
-  // the result lands in lane 16 h + token, register j: each lane combines
-  // the three limb dots of one (head, token) pair in its own registers.  No
+  // q of head h is written as (M_h / 127) (a0 + a1 / 254 + a2 / 254^2 +
+  // a3 / 254^3) with M_h = max |q| over the head's dims and int8 limbs a0 ..
+  // a3 (round to nearest at each step; with the fp32 roundings of
+  // q * 127 / M_h and of the residuals, |q - that sum| < |q| 2^-23 +
+  // M_h 2^-31, where three limbs left M_h 2^-22: a component far under the
+  // head's maximum keeps its own precision), the limbs are rows 4 h + j of
+  // A, and B is the stored K bytes as they are.  Row 4 h + j of the result
+  // lands in lane 16 h + token, register j: each lane combines the four
+  // limb dots of one (head, token) pair in its own registers.  No
   // K byte is converted, and a 64-dim K block is one MFMA instead of two.
   constexpr bool I8QK = MFMA && FMT == RKV_I8 && G <= 4 && RKV_DECODE_I8_QK;
   // PV likewise: the weights w = p * (V row scale) of head h over the
-  // wave's slice are written as (W_h / 127) (b0 + b1 / 254 + b2 / 254^2)
-  // with W_h = their maximum, the limbs are the A rows 4 h + j (bytes in
+  // wave's slice are written as (W_h / 127) (b0 + ... + b3 / 254^3) with
+  // W_h = their maximum (so a row whose scale dwarfs the slice's others
+  // leaves theirs ~2^-31 W_h of precision, not 2^-22), the limbs are the A rows 4 h + j (bytes in
   // LDS, written once per slice by the softmax pass), B is the staged V
   // bytes read transposed, and the int32 sums over the slice are exact.
   constexpr bool I8PV = MPV && FMT == RKV_I8 && G <= 4 && RKV_DECODE_I8_PV;
@@ -545,24 +548,27 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     const float inv = amax >= 0x1p-120f ? 127.0f / amax : 0.0f;  // finite
     // limb rows 4 h + j of D bytes each, after the K staging rows
     uint8_t* qbuf = s_vq[w] + BS * KROW;
-    uint32_t lw[3][QN / 4];
+    uint32_t lw[4][QN / 4];
 #pragma unroll
     for (int e4 = 0; e4 < QN / 4; ++e4) {
-      lw[0][e4] = lw[1][e4] = lw[2][e4] = 0u;
+      lw[0][e4] = lw[1][e4] = lw[2][e4] = lw[3][e4] = 0u;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float a = qv[4 * e4 + e] * inv;  // |a| <= 127
         const float a0 = rintf(a);
         const float r1 = (a - a0) * 254.0f;  // |r1| <= 127
         const float a1 = rintf(r1);
-        const float a2 = rintf((r1 - a1) * 254.0f);
+        const float r2 = (r1 - a1) * 254.0f;
+        const float a2 = rintf(r2);
+        const float a3 = rintf((r2 - a2) * 254.0f);
         lw[0][e4] |= ((uint32_t)(int32_t)a0 & 0xffu) << (8 * e);
         lw[1][e4] |= ((uint32_t)(int32_t)a1 & 0xffu) << (8 * e);
         lw[2][e4] |= ((uint32_t)(int32_t)a2 & 0xffu) << (8 * e);
+        lw[3][e4] |= ((uint32_t)(int32_t)a3 & 0xffu) << (8 * e);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < 4; ++j) {
       uint8_t* dst = qbuf + (4 * (lane >> 4) + j) * D + (lane & 15) * QN;
       if constexpr (QN == 8)
         *reinterpret_cast<uint2*>(dst) = make_uint2(lw[j][0], lw[j][1]);
@@ -572,8 +578,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the limb rows ...
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads
-    // A row kt: head kt / 4, limb kt % 4 (limb 3 and heads >= G are zero)
-    const bool live = kt / 4 < G && (kt & 3) < 3;
+    // A row kt: head kt / 4, limb kt % 4 (heads >= G are zero rows)
+    const bool live = kt / 4 < G;
 #pragma unroll
     for (int n = 0; n < NL; ++n) {
       const uint4 v = *reinterpret_cast<const uint4*>(
@@ -655,7 +661,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
                                                          __builtin_bit_cast(i32x4_t, kb[n]),
                                                          iacc, 0, 0, 0);
           sacc[0] = ((float)iacc[0] + (float)iacc[1] * (1.0f / 254.0f) +
-                     (float)iacc[2] * (1.0f / 64516.0f)) * qmul;
+                     (float)iacc[2] * (1.0f / 64516.0f) +
+                     (float)iacc[3] * (1.0f / 16387064.0f)) * qmul;
         } else if constexpr (QNT) {
 #pragma unroll
           for (int n = 0; n < NL; ++n) {
@@ -771,10 +778,13 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
                 const float b0 = rintf(a);
                 const float r1 = (a - b0) * 254.0f;
                 const float b1 = rintf(r1);
-                const float b2 = rintf((r1 - b1) * 254.0f);
+                const float r2 = (r1 - b1) * 254.0f;
+                const float b2 = rintf(r2);
+                const float b3 = rintf((r2 - b2) * 254.0f);
                 s_w8[(4 * g + 0) * NK + x] = (uint8_t)(int32_t)b0;
                 s_w8[(4 * g + 1) * NK + x] = (uint8_t)(int32_t)b1;
                 s_w8[(4 * g + 2) * NK + x] = (uint8_t)(int32_t)b2;
+                s_w8[(4 * g + 3) * NK + x] = (uint8_t)(int32_t)b3;
               }
             }
           }
@@ -869,10 +879,9 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");  // ... before the reads below
         // A = weight limbs: lane (kq, kt) holds row kt (head kt / 4, limb
-        // kt % 4; limb 3 and heads >= G are zero rows), keys 8 kq .. + 7 of
-        // the pair
+        // kt % 4; heads >= G are zero rows), keys 8 kq .. + 7 of the pair
         const uint8_t* s_w8 = reinterpret_cast<const uint8_t*>(s_pq[w]);
-        const bool arow = kt < 4 * G && (kt & 3) < 3;
+        const bool arow = kt < 4 * G;
         const uint2 wa = *reinterpret_cast<const uint2*>(
             s_w8 + (arow ? kt : 0) * NK + (i - 1) * BS + 8 * kq);
         const long pa = arow ? __builtin_bit_cast(long, wa) : 0l;
@@ -966,7 +975,8 @@ __attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stre
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
       iv[c] = ((float)iov[c][0] + (float)iov[c][1] * (1.0f / 254.0f) +
-               (float)iov[c][2] * (1.0f / 64516.0f)) * pmul;
+               (float)iov[c][2] * (1.0f / 64516.0f) +
+               (float)iov[c][3] * (1.0f / 16387064.0f)) * pmul;
   } else if constexpr (MPV) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)

@@ -137,6 +137,58 @@ class BlockManager {
     return moves;
   }
 
+  // The blocks plan_compaction(.., below_only = false) would move -- the
+  // min(max_moves, live, free) highest live ids -- go into the longest runs
+  // of consecutive free ids instead of the lowest free ids: runs by length,
+  // longest first (lower start on ties), each filled from its low end.  The
+  // i-th lowest source goes to the i-th lowest destination, so the pairs
+  // come out ascending on both sides and a copy writes whole runs of
+  // consecutive blocks.
+  int64_t plan_relocation(int64_t max_moves, std::vector<int32_t>* pairs) {
+    std::vector<int32_t> fr(free_.begin(), free_.end());
+    std::sort(fr.begin(), fr.end());
+    std::vector<int32_t> src;
+    for (int64_t b = num_blocks() - 1;
+         b >= 0 && (int64_t)src.size() < max_moves && src.size() < fr.size(); --b)
+      if (owner_[b] >= 0) src.push_back((int32_t)b);
+    const size_t n = src.size();
+    std::reverse(src.begin(), src.end());
+    struct Run { int32_t start, len; };
+    std::vector<Run> runs;
+    for (size_t i = 0; i < fr.size();) {
+      size_t k = i + 1;
+      while (k < fr.size() && fr[k] == fr[k - 1] + 1) ++k;
+      runs.push_back({fr[i], (int32_t)(k - i)});
+      i = k;
+    }
+    std::stable_sort(runs.begin(), runs.end(),
+                     [](const Run& a, const Run& b) { return a.len > b.len; });
+    std::vector<int32_t> dst;
+    for (const Run& r : runs)
+      for (int32_t x = 0; x < r.len && dst.size() < n; ++x) dst.push_back(r.start + x);
+    std::sort(dst.begin(), dst.end());
+    std::vector<char> taken((size_t)num_blocks(), 0);
+    for (size_t i = 0; i < n; ++i) {
+      const int32_t b = src[i], d = dst[i];
+      const int64_t seq = owner_[b], p = pos_[b];
+      tables_[seq][p] = d;
+      owner_[d] = seq;
+      pos_[d] = p;
+      owner_[b] = -1;
+      pos_[b] = -1;
+      taken[(size_t)d] = 1;
+      pairs->push_back(b);
+      pairs->push_back(d);
+    }
+    std::vector<int32_t> rest;
+    for (int32_t f : fr)
+      if (!taken[(size_t)f]) rest.push_back(f);
+    rest.insert(rest.end(), src.begin(), src.end());
+    std::sort(rest.begin(), rest.end());
+    free_.assign(rest.begin(), rest.end());
+    return (int64_t)n;
+  }
+
  private:
   int block_size_;
   std::deque<int32_t> free_;                                  // FIFO
@@ -444,6 +496,17 @@ extern "C" int64_t rkv_bm_plan_migration(rkv_block_manager* bm, int64_t max_move
     return fail(RKV_ERR_INVALID_ARG, "rkv_bm_plan_migration: bad argument");
   std::vector<int32_t> p;
   const int64_t n = bm->bm->plan_compaction(std::min(max_moves, cap_pairs), &p, false);
+  std::memcpy(pairs, p.data(), p.size() * sizeof(int32_t));
+  return n;
+}
+
+extern "C" int64_t rkv_bm_plan_relocation(rkv_block_manager* bm, int64_t max_moves,
+                                          int32_t* pairs, int64_t cap_pairs) {
+  rkv::clear_error();
+  if (!bm || max_moves < 0 || cap_pairs < 0 || (max_moves > 0 && !pairs))
+    return fail(RKV_ERR_INVALID_ARG, "rkv_bm_plan_relocation: bad argument");
+  std::vector<int32_t> p;
+  const int64_t n = bm->bm->plan_relocation(std::min(max_moves, cap_pairs), &p);
   std::memcpy(pairs, p.data(), p.size() * sizeof(int32_t));
   return n;
 }

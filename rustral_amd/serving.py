@@ -121,6 +121,15 @@ class PagedCache:
             raise _err(n)
         return buf[:n].copy()
 
+    def plan_relocation(self, max_moves: int) -> np.ndarray:
+        """The blocks plan_migration moves, into the longest runs of free ids
+        (longest first), pairs ascending on both sides."""
+        buf = np.empty((max(max_moves, 1), 2), np.int32)
+        n = lib().rkv_bm_plan_relocation(self._h, max_moves, _ptr(buf), max_moves)
+        if n < 0:
+            raise _err(n)
+        return buf[:n].copy()
+
 
 @dataclass
 class Batch:

@@ -209,7 +209,7 @@ def test_decode_q_int8_wide_dynamic_range(dev, hq, hkv):
     10^U(-2, 2) per (token, head), q heads by 10^U(-1.5, 1), one q head all
     zeros and one a single spike over 1e-3 values.  For G <= 4 the kernel
     runs QK^T and PV on the integer matrix cores with q and the PV weights in
-    three int8 limbs, fixed point against each head's maximum: these inputs
+    four int8 limbs, fixed point against each head's maximum: these inputs
     put the small terms many decades under that maximum, where a dropped or
     mis-scaled limb would show.  (G = 8 runs the bf16 path, q as bf16 hi +
     lo; the other cases cover it.)"""

@@ -171,10 +171,16 @@ def test_block_manager_matches_restatement(seed):
             want = r.plan_compaction(m)
             assert [tuple(p) for p in got.tolist()] == want
             assert len(set(got[:, 0].tolist()) & set(got[:, 1].tolist())) == 0
-        else:
+        elif op < 0.965:
             m = rng.randrange(0, 20)
             got = c.plan_migration(m)
             want = r.plan_migration(m)
+            assert [tuple(p) for p in got.tolist()] == want
+            assert len(set(got[:, 0].tolist()) & set(got[:, 1].tolist())) == 0
+        else:
+            m = rng.randrange(0, 20)
+            got = c.plan_relocation(m)
+            want = r.plan_relocation(m)
             assert [tuple(p) for p in got.tolist()] == want
             assert len(set(got[:, 0].tolist()) & set(got[:, 1].tolist())) == 0
         _check_tables(c, r)
@@ -304,3 +310,50 @@ def test_migration_moves_the_requested_share_even_without_lower_holes():
     for s in range(12):
         np.testing.assert_array_equal(pool[c.table(s)], before[s])
     assert c.num_free() == nb - live
+
+
+def test_relocation_fills_the_longest_free_runs_in_order():
+    """plan_relocation moves what plan_migration moves (the highest live
+    ids) into the longest runs of free ids, longest first, with both sides
+    ascending; the data gathered through the tables is unchanged and the
+    vacated sources join the free list."""
+    rng = np.random.default_rng(7)
+    nb, bs = 400, 16
+    c, m = PagedCache(bs, nb), PagedCache(bs, nb)
+    pending = {sid: int(rng.integers(3, 15)) for sid in range(20)}
+    while pending:                                       # round-robin: interleaved ids
+        for sid in list(pending):
+            assert c.allocate(sid, bs) is not None and m.allocate(sid, bs) is not None
+            pending[sid] -= 1
+            if not pending[sid]:
+                del pending[sid]
+    for sid in (3, 8, 11):                               # single-block holes
+        c.free(sid), m.free(sid)
+    keep = [s for s in range(20) if s not in (3, 8, 11)]
+    live = sum(len(c.table(s)) for s in keep)
+    free_before = sorted(c.free_list())
+    pool = rng.standard_normal((nb, 2, bs, 4)).astype(np.float32)
+    before = {s: pool[c.table(s)].copy() for s in keep}
+    want = live // 4
+    pairs = c.plan_relocation(want)
+    mig = m.plan_migration(want)
+    assert len(pairs) == len(mig) == want
+    src, dst = pairs[:, 0], pairs[:, 1]
+    assert sorted(src.tolist()) == sorted(mig[:, 0].tolist())   # the same blocks move
+    assert (np.diff(src) > 0).all() and (np.diff(dst) > 0).all()
+    assert not set(src.tolist()) & set(dst.tolist())
+    runs = []
+    for f in free_before:
+        if runs and runs[-1][0] + runs[-1][1] == f:
+            runs[-1][1] += 1
+        else:
+            runs.append([f, 1])
+    runs.sort(key=lambda r: (-r[1], r[0]))
+    assert runs[0][1] >= want                            # the pool's unused top is one run
+    assert dst.tolist() == list(range(runs[0][0], runs[0][0] + want))
+    pool[dst] = pool[src]
+    for s, v in before.items():
+        np.testing.assert_array_equal(pool[c.table(s)], v)
+    assert c.num_free() == nb - live
+    free_after = set(c.free_list())
+    assert set(src.tolist()) <= free_after and not set(dst.tolist()) & free_after
