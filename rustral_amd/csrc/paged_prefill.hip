@@ -96,8 +96,28 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   constexpr int PT = (KB * CH + NT - 1) / NT;  // chunks per thread and iteration
   constexpr int NC = D / 32;               // QK^T MFMAs per key block (per slice)
   constexpr int NO = D / 16;               // PV MFMAs per key block (per slice)
-  __shared__ __align__(16) uint16_t s_k[2][NS][KB * kBS * KP];
-  __shared__ __align__(16) uint16_t s_v[2][NS][KB * kBS * VKP];
+  // The output rows go out through LDS: each wave writes one head's 16 rows
+  // (MFMA layout) into wave-private rows of D floats padded by 16 bytes
+  // (the 16 rows of one write then fall on distinct banks) and stores them
+  // back whole, 512 contiguous bytes per half-wave, where the MFMA layout
+  // stored 16 rows x 64 bytes per instruction.  The rows sit after the K/V
+  // staging buffers, so no workgroup barrier separates them from the loop.
+  // configs[4] admissions (us per call, one box, one process): 30.5 with
+  // stores from the MFMA layout, 28.0 through the rows; q staged the same
+  // way as well 30.0 (its LDS round trip costs more than the contiguous
+  // loads save), both heads' rows at once behind a workgroup barrier 28.7.
+  // Builds of one head per wave hold two workgroups per CU, which the rows'
+  // LDS would halve: they store from the MFMA layout.
+  constexpr bool STAGE_OUT = HW > 1;
+  constexpr int NW = NT / 64;                         // waves
+  constexpr int RWO = D + 4;                          // padded output row (floats)
+  constexpr int KB_BYTES = 2 * NS * KB * kBS * KP * 2;
+  constexpr int KV_BYTES = KB_BYTES + 2 * NS * KB * kBS * VKP * 2;
+  constexpr int LDS_BYTES = KV_BYTES + (STAGE_OUT ? NW * 16 * RWO * 4 : 0);
+  static_assert(KB_BYTES % 16 == 0 && KV_BYTES % 16 == 0, "16-byte aligned regions");
+  __shared__ __align__(16) uint8_t s_raw[LDS_BYTES];
+  auto s_k = reinterpret_cast<uint16_t (*)[NS][KB * kBS * KP]>(s_raw);
+  auto s_v = reinterpret_cast<uint16_t (*)[NS][KB * kBS * VKP]>(s_raw + KB_BYTES);
 
   const T* __restrict__ k_pool = static_cast<const T*>(k_pool_);
   const T* __restrict__ v_pool = static_cast<const T*>(v_pool_);
@@ -224,6 +244,8 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
       qraw[hh][c][1] = reinterpret_cast<const float4*>(qp + 32 * c)[1];
     }
   }
+  // every q load is issued before the K/V fetches below
+  __builtin_amdgcn_sched_barrier(0);
 
   int32_t ids[KB];
   load_ids(0, ids);
@@ -234,6 +256,7 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   load_ids(1, ids);
   uint32_t ok1 = fetch(ids, kr1, vr1);
   load_ids(2, ids);  // for the first fetch inside the loop
+  __builtin_amdgcn_sched_barrier(0);
 
   // B operand of S^T = K Q^T: Q[row r16][32c + 8 grp .. + 8] * q_scale, hi
   // and lo (scores come out already scaled by scale * log2 e), converted
@@ -505,18 +528,62 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   // every lane of the wave still active for the swaps
 #pragma unroll
   for (int hh = 0; hh < HW; ++hh) l[hh] = xor48_sum(l[hh]);
-  if (!row_ok) return;
+  if constexpr (!STAGE_OUT) {
+    if (!row_ok) return;
 #pragma unroll
-  for (int hh = 0; hh < HW; ++hh) {
-    const float inv = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
-    float* op = out + ((int64_t)(s0 + qi) * num_q_heads + h0 + hh) * D + 4 * grp;
+    for (int hh = 0; hh < HW; ++hh) {
+      const float inv = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
+      float* op = out + ((int64_t)(s0 + qi) * num_q_heads + h0 + hh) * D + 4 * grp;
 #pragma unroll
-    for (int c = 0; c < NO; ++c)
-      // nontemporal: the rows are not read again by this kernel (the
-      // admissions, whose fp32 output is ~45% of their bytes, ran 4% faster)
-      __builtin_nontemporal_store(
-          f32x4_t{o[hh][c][0] * inv, o[hh][c][1] * inv, o[hh][c][2] * inv, o[hh][c][3] * inv},
-          reinterpret_cast<f32x4_t*>(op + 16 * c));
+      for (int c = 0; c < NO; ++c)
+        // nontemporal: the rows are not read again by this kernel
+        __builtin_nontemporal_store(
+            f32x4_t{o[hh][c][0] * inv, o[hh][c][1] * inv, o[hh][c][2] * inv, o[hh][c][3] * inv},
+            reinterpret_cast<f32x4_t*>(op + 16 * c));
+    }
+  } else {
+    // The output through the wave's own LDS rows (outside the staging
+    // buffers), head by head: lane (grp, r16) holds dims 16 c + 4 grp .. + 3
+    // of row r16; the rows go out whole, unit u on lane u % 64.
+    auto wave_sync = []() __attribute__((always_inline)) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    constexpr int UPO = D / 4;               // 16-byte units per output row
+    constexpr int OU = 16 * UPO / 64;        // units per lane and head
+    static_assert((16 * UPO) % 64 == 0, "whole units per lane");
+    float* orows = reinterpret_cast<float*>(s_raw + KV_BYTES) + w * 16 * RWO;
+#pragma unroll
+    for (int hh = 0; hh < HW; ++hh) {
+      const float inv = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
+#pragma unroll
+      for (int c = 0; c < NO; ++c)
+        *reinterpret_cast<float4*>(orows + r16 * RWO + 16 * c + 4 * grp) =
+            make_float4(o[hh][c][0] * inv, o[hh][c][1] * inv, o[hh][c][2] * inv, o[hh][c][3] * inv);
+      wave_sync();
+      // all of the head's rows read back first, then stored: a store's data
+      // registers are then never reused while stores are in flight (which
+      // would wait for the stores to complete)
+      f32x4_t orow[OU];
+#pragma unroll
+      for (int k = 0; k < OU; ++k) {
+        const int u = lane + 64 * k;
+        orow[k] = *reinterpret_cast<const f32x4_t*>(orows + (u / UPO) * RWO + (u % UPO) * 4);
+      }
+      wave_sync();  // read before the next head overwrites
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < OU; ++k) {
+        const int u = lane + 64 * k, row = u / UPO, col = (u % UPO) * 4;
+        // nontemporal: the rows are not read again by this kernel (the
+        // admissions, whose fp32 output is ~45% of their bytes, ran 4% faster)
+        if (qr0 + row < nr)
+          __builtin_nontemporal_store(
+              orow[k], reinterpret_cast<f32x4_t*>(
+                           out + ((int64_t)(s0 + qr0 + row) * num_q_heads + h0 + hh) * D + col));
+      }
+    }
   }
 }
 
