@@ -50,7 +50,8 @@ def parse():
                    help="only run the 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     p.add_argument("--workload", default="config2",
                    choices=["config0", "config1", "config2", "config3", "config4", "prefill",
-                            "decode_q", "device_step", "ceilings", "store_variants"],
+                            "decode_q", "device_step", "ceilings", "store_variants",
+                            "patterns_1byte"],
                    help="config2 (default): the headline decode line; the others print "
                         "their own line (benchmark configs[0], [1], [3], [4])")
     return p.parse_args()
@@ -1084,6 +1085,81 @@ def run_ceilings(torch, dev, args):
                  decode_int8_over_stream_1byte=round(d8["GBps"] / st8["GBps"], 4), results=res)
 
 
+def run_patterns_1byte(torch, dev, args):
+    """The int8 decode's load pattern and variants of it, loads only
+    (rustral_amd/ceiling `tile_stream_1b`), timed beside the int8 decode call
+    (partition kernel and merge) on configs[2]'s shape over 32 layers of
+    1-byte pools: the pattern as the decode kernel reads it (2 KiB (block,
+    head) tiles plus the fp32 row scales), without the scales, two or four KV
+    heads per wave, a partition-major grid, and the K and V row scales in a
+    128-byte line after each K tile."""
+    import numpy as np
+    from rustral_amd import ceiling as C
+    from rustral_amd import kv
+    reps = max(args.steps // 4, 5)
+    rng = np.random.default_rng(SEED)
+    ctx = rng.integers(CTX_LO, CTX_HI + 1, size=B).astype(np.int32)
+    need = (ctx.astype(np.int64) + BS - 1) // BS
+    nb = int(need.sum())
+    mbs = CTX_HI // BS
+    ctx_d = torch.from_numpy(ctx).to(dev)
+    g = torch.Generator(device=dev).manual_seed(SEED + 2)
+    layers = []
+    for _ in range(args.layers):
+        kp = torch.randint(0, 256, (nb, HKV, BS, D), generator=g, dtype=torch.uint8, device=dev)
+        vp = torch.randint(0, 256, (nb, HKV, BS, D), generator=g, dtype=torch.uint8, device=dev)
+        kc = torch.randint(0, 256, (nb, HKV, BS * D + 128), generator=g, dtype=torch.uint8,
+                           device=dev)
+        ks = torch.rand((nb, HKV, BS), generator=g, device=dev) * 0.02
+        vs = torch.rand((nb, HKV, BS), generator=g, device=dev) * 0.02
+        q = torch.randn((B, HQ, D), generator=g, device=dev)
+        perm = torch.randperm(nb, generator=g, device=dev).to(torch.int32)
+        t = torch.full((B, mbs), -1, dtype=torch.int32, device=dev)
+        o = 0
+        for b in range(B):
+            t[b, :int(need[b])] = perm[o:o + int(need[b])]
+            o += int(need[b])
+        layers.append((q, kp, vp, kc, ks, vs, t))
+    n_layers = len(layers)
+    parts = (CTX_HI + 639) // 640
+    tokens = int(ctx.astype(np.int64).sum())
+    with_scales = tokens * HKV * (D + 4) * 2
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+
+    def rate(fn, moved):
+        fn()
+        ms = _timed(torch, fn, reps)
+        return {"GBps": round(moved * n_layers / (ms * 1e-3) / 1e9, 1),
+                "us_per_layer": round(1e3 * ms / n_layers, 2), "bytes_per_layer": int(moved)}
+
+    res = {}
+    for name in C.TILE_STREAM_1B:
+        moved = tokens * HKV * D * 2 if name == "no_scales" else with_scales
+
+        def fn(name=name):
+            for q, kp, vp, kc, ks, vs, t in layers:
+                C.tile_stream_1b(torch, kc if name == "scales_after_k_tile" else kp, vp, t, ctx_d,
+                                 sink, parts, name, nb, HKV, k_scale=ks, v_scale=vs)
+        res[name] = rate(fn, moved)
+    out = torch.empty((B, HQ, D), device=dev)
+    ws = torch.empty(kv.workspace_bytes(B, HQ, D, CTX_HI), dtype=torch.uint8, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def decode_all():
+        for q, kp, vp, kc, ks, vs, t in layers:
+            kv.decode_attention_q(q, kp, vp, ks, vs, t, ctx_d, scale, "int8",
+                                  max_context=CTX_HI, out=out, workspace=ws)
+    res["decode_int8_call"] = rate(decode_all, with_scales)
+    base = res["row_scales"]
+    return _line("int8 decode load pattern and variants, loads only (configs[2] shape)",
+                 base["GBps"], "GB/s", base["us_per_layer"] / 1e3, args, "u8",
+                 {"workload": "tile_stream_1b of rustral_amd/ceiling over 32 layers of 1-byte "
+                              "pools, configs[2] contexts", "layers": n_layers,
+                  "partitions": parts, "tokens": tokens},
+                 decode_call_over_pattern=round(res["decode_int8_call"]["GBps"] / base["GBps"], 4),
+                 results=res)
+
+
 def run_store_variants(torch, dev, args):
     """Write and copy ceilings from writers other than the library's own
     stream kernels: hipMemsetD32Async (eager), torch's fill_ and zero_,
@@ -1205,7 +1281,8 @@ def main():
         line = {"config0": run_config0, "config1": run_config1, "config3": run_config3,
                 "prefill": run_prefill, "decode_q": run_decode_q,
                 "config4": run_config4, "device_step": run_device_step,
-                "ceilings": run_ceilings, "store_variants": run_store_variants}[args.workload](
+                "ceilings": run_ceilings, "store_variants": run_store_variants,
+                "patterns_1byte": run_patterns_1byte}[args.workload](
                     torch, dev, args)
         print(json.dumps(line), flush=True)
         return

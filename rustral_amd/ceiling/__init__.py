@@ -29,6 +29,9 @@ _SIG = {
     "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                          C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_void_p,
                          C.c_uint, C.c_void_p],
+    "rkvc_tile_stream_1b": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                            C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int,
+                            C.c_void_p, C.c_uint, C.c_void_p],
 }
 _lib = None
 
@@ -151,3 +154,24 @@ def tile_stream(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int,
                                tables.data_ptr(), tables.shape[1], ctx_lens.data_ptr(),
                                tables.shape[0], hkv, nb, partitions, sink.data_ptr(), 0x9E3779B9,
                                _stream(torch, k_pool.device)), "rkvc_tile_stream")
+
+
+TILE_STREAM_1B = {"row_scales": 0, "no_scales": 1, "two_heads_per_wave": 2,
+                  "four_heads_per_wave": 3, "partition_major": 4, "scales_after_k_tile": 5}
+
+
+def tile_stream_1b(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int,
+                   variant: str, num_blocks: int, num_kv_heads: int,
+                   k_scale=None, v_scale=None) -> None:
+    """Variants of the 1-byte decode load pattern (D 128, 16-token blocks):
+    k_pool / v_pool byte pools of num_blocks x num_kv_heads tiles (2,048
+    bytes; the K pool's tiles 2,176 bytes for "scales_after_k_tile"),
+    k_scale / v_scale fp32 [num_blocks, Hkv, 16] for the variants that read
+    row scales."""
+    ks = k_scale.data_ptr() if k_scale is not None else None
+    vs = v_scale.data_ptr() if v_scale is not None else None
+    _ok(lib().rkvc_tile_stream_1b(k_pool.data_ptr(), v_pool.data_ptr(), ks, vs,
+                                  tables.data_ptr(), tables.shape[1], ctx_lens.data_ptr(),
+                                  tables.shape[0], num_kv_heads, num_blocks, partitions,
+                                  TILE_STREAM_1B[variant], sink.data_ptr(), 0x9E3779B9,
+                                  _stream(torch, k_pool.device)), "rkvc_tile_stream_1b")

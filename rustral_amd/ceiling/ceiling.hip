@@ -19,6 +19,9 @@
 //                     ring of 4 tiles, 1 KiB of whole rows per wave-load,
 //                     tiles past the context re-reading the wave's first
 //                     tile
+//   rkvc_tile_stream_1b  variants of the 1-byte pattern: no scales, 2 or 4
+//                     KV heads per wave, a partition-major grid, the scales
+//                     in a 128-byte line after each K tile
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -181,6 +184,86 @@ __global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
     if constexpr (t + kR < kNT) {
 #pragma unroll
       for (int n = 0; n < NL; ++n) ring[t % kR][n] = tile_load(t + kR, n);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  acc += __float_as_uint(sc);
+  if (acc == magic) sink[0] = acc;
+}
+
+// Variants of the 1-byte tile stream (same grid, 4 waves, 10 + 10 tiles a
+// wave, ring of 4 wave-load pairs):
+//   HPW  KV heads per wave: a (block, HPW heads) tile is HPW x 2 KiB of
+//        contiguous rows, the grid has Hkv / HPW workgroups per (partition,
+//        sequence) and the ring holds 4 / HPW tiles;
+//   SC   0: no scales; 1: the row scales as the decode kernel reads them
+//        (k_scale / v_scale [num_blocks][Hkv][16] fp32); 2: the K and V row
+//        scales of a (block, head) in a 128-byte line right after its K tile
+//        (the K pool then holds 2,176-byte tiles);
+//   PM   partition-major grid (Hkv / HPW, sequences, partitions): every
+//        sequence's first partition is dispatched before any second one.
+template <int HPW, int SC, bool PM>
+__global__ __launch_bounds__(64 * kSplit) void tile_stream1_kernel(
+    const uint8_t* __restrict__ k_pool, const uint8_t* __restrict__ v_pool,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale,
+    const int32_t* __restrict__ tables, int max_blocks, const int32_t* __restrict__ ctx_lens,
+    int num_kv_heads, int64_t num_blocks, unsigned* sink, unsigned magic) {
+  constexpr int NL = 2 * HPW, R = kR / HPW;
+  constexpr int KT = SC == 2 ? kBS * kD + 128 : kBS * kD, VT = kBS * kD;  // tile strides
+  static_assert(R >= 1, "ring of at least one tile");
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int kh = blockIdx.x * HPW;
+  const int part = PM ? blockIdx.z : blockIdx.y, b = PM ? blockIdx.y : blockIdx.z;
+  const int L = ctx_lens[b];
+  if (part * kP >= L) return;
+  const int lb0 = part * (kP / kBS) + w * kNTW;
+  const int32_t* tab = tables + (int64_t)b * max_blocks;
+  int32_t pb[kNTW];
+#pragma unroll
+  for (int i = 0; i < kNTW; ++i) {
+    const int lb = lb0 + i;
+    pb[i] = tab[lb < max_blocks ? lb : max_blocks - 1];
+  }
+  const int32_t pb0 = pb[0] >= 0 && pb[0] < num_blocks ? pb[0] : 0;
+  int64_t tix[kNTW];  // (block, first head) tile index
+#pragma unroll
+  for (int i = 0; i < kNTW; ++i) {
+    const bool ok = (lb0 + i) * kBS < L && pb[i] >= 0 && pb[i] < num_blocks;
+    tix[i] = (int64_t)(ok ? pb[i] : pb0) * num_kv_heads + kh;
+  }
+  const uint32_t off = lane * 16;
+  auto tile_load = [&](int t, int n) __attribute__((always_inline)) {
+    // HPW > 1 only with SC != 2: the HPW tiles of a block are contiguous
+    const uint8_t* p = t < kNTW ? k_pool + tix[t] * KT : v_pool + tix[t - kNTW] * VT;
+    return ld<true>(reinterpret_cast<const u32x4*>(p + off + n * 1024));
+  };
+  unsigned acc = 0;
+  u32x4 ring[R][NL];
+#pragma unroll
+  for (int t = 0; t < R; ++t)
+#pragma unroll
+    for (int n = 0; n < NL; ++n) ring[t][n] = tile_load(t, n);
+  float sc = 0.0f;
+  if constexpr (SC == 1) {
+#pragma unroll
+    for (int i = 0; i < kNTW; ++i) sc += k_scale[tix[i] * kBS + (lane & (16 * HPW - 1))];
+#pragma unroll
+    for (int j = 0; j < (kNTW * kBS * HPW + 63) / 64; ++j) {
+      const int x = lane + 64 * j;
+      if (x < kNTW * kBS * HPW) sc += v_scale[tix[x / (kBS * HPW)] * kBS + x % (kBS * HPW)];
+    }
+  } else if constexpr (SC == 2) {
+#pragma unroll
+    for (int i = 0; i < kNTW; ++i)
+      sc += reinterpret_cast<const float*>(k_pool + tix[i] * KT + kBS * kD)[lane & 31];
+  }
+  static_for<0, 2 * kNTW>([&](auto tc) __attribute__((always_inline)) {
+    constexpr int t = decltype(tc)::value;
+#pragma unroll
+    for (int n = 0; n < NL; ++n) acc ^= fold(ring[t % R][n]) + t;
+    if constexpr (t + R < 2 * kNTW) {
+#pragma unroll
+      for (int n = 0; n < NL; ++n) ring[t % R][n] = tile_load(t + R, n);
     }
     __builtin_amdgcn_sched_barrier(0);
   });
@@ -558,6 +641,36 @@ int rkvc_tile_stream(const void* k_pool, const void* v_pool, const float* k_scal
   const dim3 grid((unsigned)num_kv_heads, (unsigned)partitions, (unsigned)num_seqs);
   clear_errors();
   auto kern = elem_bytes == 2 ? tile_stream_kernel<2> : tile_stream_kernel<1>;
+  kern<<<grid, 64 * kSplit, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool), k_scale, v_scale,
+      tables, max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
+  return launched();
+}
+
+// variant: 0 the decode pattern (row scales), 1 no scales, 2 two KV heads per
+// wave, 3 four, 4 partition-major grid, 5 scales after each K tile (k_pool
+// of num_blocks * Hkv tiles of 2,176 bytes; k_scale / v_scale unused).
+int rkvc_tile_stream_1b(const void* k_pool, const void* v_pool, const float* k_scale,
+                        const float* v_scale, const int32_t* tables, int max_blocks,
+                        const int32_t* ctx_lens, int num_seqs, int num_kv_heads,
+                        int64_t num_blocks, int partitions, int variant, unsigned* sink,
+                        unsigned magic, void* stream) {
+  const int hpw = variant == 2 ? 2 : variant == 3 ? 4 : 1;
+  const bool scales = variant == 0 || variant == 2 || variant == 3 || variant == 4;
+  if (!k_pool || !v_pool || !tables || !ctx_lens || !sink || max_blocks <= 0 || num_seqs <= 0 ||
+      num_kv_heads <= 0 || num_blocks <= 0 || partitions <= 0 || variant < 0 || variant > 5 ||
+      num_kv_heads % hpw || (scales && (!k_scale || !v_scale)))
+    return -1;
+  const unsigned hx = (unsigned)(num_kv_heads / hpw);
+  const dim3 grid = variant == 4 ? dim3(hx, (unsigned)num_seqs, (unsigned)partitions)
+                                 : dim3(hx, (unsigned)partitions, (unsigned)num_seqs);
+  auto kern = variant == 0 ? tile_stream1_kernel<1, 1, false>
+            : variant == 1 ? tile_stream1_kernel<1, 0, false>
+            : variant == 2 ? tile_stream1_kernel<2, 1, false>
+            : variant == 3 ? tile_stream1_kernel<4, 1, false>
+            : variant == 4 ? tile_stream1_kernel<1, 1, true>
+                           : tile_stream1_kernel<1, 2, false>;
+  clear_errors();
   kern<<<grid, 64 * kSplit, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool), k_scale, v_scale,
       tables, max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
