@@ -284,11 +284,14 @@ impl TensorOps<RocmBackend> for RocmOps {
         if dim != 0 || tensors.is_empty() {
             return Err(unsupported("concat (only along dimension 0)"));
         }
+        if let Some(t) = tensors.iter().find(|t| t.shape.is_empty()) {
+            return Err(CoreError::InvalidArgument(format!("concat: rank-0 tensor {:?}", t.shape)));
+        }
         let first = tensors[0];
         let tail = &first.shape[1..];
         let mut rows = 0usize;
         for t in tensors {
-            if t.dtype != first.dtype || &t.shape[1..] != tail || t.shape.is_empty() {
+            if t.dtype != first.dtype || &t.shape[1..] != tail {
                 return Err(CoreError::ShapeMismatch { expected: first.shape.clone(), actual: t.shape.clone() });
             }
             rows += t.shape[0];

@@ -180,6 +180,62 @@ def test_crate_calls_only_declared_functions_and_balances_delimiters():
     assert used and used <= declared, used - declared
 
 
+def _call_args(code: str, start: int):
+    """The top-level arguments of the call whose '(' is at code[start]."""
+    depth, args, cur = 0, [], []
+    for i in range(start, len(code)):
+        ch = code[i]
+        if ch in "([{":
+            depth += 1
+            if depth == 1:
+                continue
+        elif ch in ")]}":
+            depth -= 1
+            if depth == 0:
+                last = "".join(cur).strip()
+                if last:
+                    args.append(last)
+                return args
+        elif ch == "," and depth == 1:
+            args.append("".join(cur).strip())
+            cur = []
+            continue
+        cur.append(ch)
+    raise AssertionError("unterminated call")
+
+
+def _ffi_calls():
+    """(file, function, [argument texts]) of every ffi::rkv_* call outside ffi.rs."""
+    calls = []
+    for root, _, files in os.walk(CRATE):
+        for f in files:
+            if not f.endswith(".rs") or f == "ffi.rs":
+                continue
+            code = open(os.path.join(root, f)).read()
+            code = re.sub(r"//[^\n]*", "", code)
+            code = re.sub(r'"(\\.|[^"\\])*"', '""', code)
+            for m in re.finditer(r"ffi::(rkv_\w+)\s*\(", code):
+                calls.append((f, m.group(1), _call_args(code, m.end() - 1)))
+    return calls
+
+
+def test_ffi_call_sites_pass_the_declared_arity_and_cast_types():
+    """Every ffi::rkv_* call passes as many arguments as the declaration
+    takes, and an argument written as a cast (`... as *const f32`, `as i64`)
+    casts to the declared parameter type."""
+    decl = ffi_protos()
+    calls = _ffi_calls()
+    assert len(calls) >= 60
+    for f, name, args in calls:
+        params = decl[name][1]
+        assert len(args) == len(params), f"{f}: {name} called with {len(args)} arguments, takes {len(params)}"
+        for a, (pname, ptype) in zip(args, params):
+            m = re.search(r"\bas\s+((?:\*(?:const|mut)\s+)*[A-Za-z_][\w:]*)\s*$", a)
+            if m:
+                ty = m.group(1).replace("std::os::raw::", "").replace("ffi::", "")
+                assert rust_type(ty) == ptype, f"{f}: {name}({pname}) gets `{a}`"
+
+
 @pytest.mark.parametrize("trait_method", [
     "fn shape", "fn tensor_from_vec", "fn zeros", "fn matmul", "fn transpose", "fn add",
     "fn add_row_vector", "fn relu", "fn softmax", "fn log_softmax", "fn argmax", "fn gather_rows",
