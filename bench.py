@@ -1257,6 +1257,19 @@ def run_store_variants(torch, dev, args):
         for unr in (1, 2, 4):
             res["block_copy"][f"{name}_piece{4 * unr}k"] = rate(
                 lambda: C.block_copy_unr(torch, a, pd, blk, unr), moved)
+    # one 16-byte unit a thread, by workgroup size (16 * threads bytes a
+    # workgroup): flat write, flat copy, and the two block-copy patterns the
+    # relocation plan produces
+    res["by_threads"] = {}
+    half_a, half_b = a[: a.numel() // 2], b[: b.numel() // 2]
+    seq = {k: torch.from_numpy(np.ascontiguousarray(np.stack(patterns[k], 1), dtype=np.int32)).to(dev)
+           for k in ("seq_src_seq_dst", "rand_src_seq_dst")}
+    for nth in (64, 128, 256, 512):
+        r = {"write": rate(lambda: C.write_nth(torch, b, nth), nbytes),
+             "copy": rate(lambda: C.copy_nth(torch, half_a, half_b, nth), nbytes)}
+        for k, pd in seq.items():
+            r[k] = rate(lambda: C.block_copy_nth(torch, a, pd, blk, nth), 2 * pd.shape[0] * blk)
+        res["by_threads"][f"{nth}_threads_{16 * nth}B"] = r
     best_w = max(res["write"].items(), key=lambda kv: kv[1])
     best_c = max(res["copy"].items(), key=lambda kv: kv[1])
     return _line("HBM write and copy ceilings: independent writers and store variants (4 GiB)",

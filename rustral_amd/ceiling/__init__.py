@@ -29,6 +29,8 @@ _SIG = {
     "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                          C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_void_p,
                          C.c_uint, C.c_void_p],
+    "rkvc_nth": [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_int64,
+                 C.c_int64, C.c_int, C.c_void_p],
     "rkvc_tile_stream_1b": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
                             C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int,
                             C.c_void_p, C.c_uint, C.c_void_p],
@@ -175,3 +177,22 @@ def tile_stream_1b(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: in
                                   tables.shape[0], num_kv_heads, num_blocks, partitions,
                                   TILE_STREAM_1B[variant], sink.data_ptr(), 0x9E3779B9,
                                   _stream(torch, k_pool.device)), "rkvc_tile_stream_1b")
+
+
+def write_nth(torch, buf, nth: int) -> None:
+    """Flat write of buf, one 16-byte unit a thread, nth threads a workgroup."""
+    _ok(lib().rkvc_nth(0, None, buf.data_ptr(), buf.numel() * buf.element_size(), None, 0, 0, 0,
+                       nth, _stream(torch, buf.device)), "rkvc_nth write")
+
+
+def copy_nth(torch, src, dst, nth: int) -> None:
+    """Flat copy src -> dst (nontemporal), one unit a thread, nth threads a workgroup."""
+    _ok(lib().rkvc_nth(1, src.data_ptr(), dst.data_ptr(), src.numel() * src.element_size(), None,
+                       0, 0, 0, nth, _stream(torch, src.device)), "rkvc_nth copy")
+
+
+def block_copy_nth(torch, pool, pairs, block_bytes: int, nth: int) -> None:
+    """Block copies inside pool (pairs int32 [n, 2]), pieces of 16 nth bytes."""
+    nb = pool.numel() * pool.element_size() // block_bytes
+    _ok(lib().rkvc_nth(2, None, pool.data_ptr(), 0, pairs.data_ptr(), pairs.shape[0], block_bytes,
+                       nb, nth, _stream(torch, pool.device)), "rkvc_nth block copy")

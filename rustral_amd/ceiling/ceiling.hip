@@ -19,6 +19,8 @@
 //                     ring of 4 tiles, 1 KiB of whole rows per wave-load,
 //                     tiles past the context re-reading the wave's first
 //                     tile
+//   rkvc_nth          write, copy and block copy, one 16-byte unit a thread,
+//                     by workgroup size (64 to 512 threads)
 //   rkvc_tile_stream_1b  variants of the 1-byte pattern: no scales, 2 or 4
 //                     KV heads per wave, a partition-major grid, the scales
 //                     in a 128-byte line after each K tile
@@ -372,6 +374,33 @@ __global__ __launch_bounds__(256) void block_copy_unr_kernel(char* __restrict__ 
   for (int k = 0; k < UNR; ++k) st<true>(dp + k * 256 + threadIdx.x, x[k]);
 }
 
+// One 16-byte unit a thread and NTH threads a workgroup, one round (the
+// grid covers the buffer, or every piece of every pair, once): flat write,
+// flat copy (nontemporal loads and stores) and block copies in pieces of
+// 16 NTH bytes -- the work per workgroup by workgroup size.
+template <int NTH>
+__global__ __launch_bounds__(NTH) void write_nth_kernel(u32x4* __restrict__ d, int64_t n) {
+  const int64_t u = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (u < n) st<false>(d + u, u32x4{threadIdx.x, blockIdx.x, 0x3f800000u, 0u});
+}
+template <int NTH>
+__global__ __launch_bounds__(NTH) void copy_nth_kernel(const u32x4* __restrict__ s,
+                                                       u32x4* __restrict__ d, int64_t n) {
+  const int64_t u = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  if (u < n) st<true>(d + u, ld<true>(s + u));
+}
+template <int NTH>
+__global__ __launch_bounds__(NTH) void block_copy_nth_kernel(char* __restrict__ pool,
+                                                             const int32_t* __restrict__ pairs,
+                                                             int64_t block_bytes,
+                                                             int64_t num_blocks) {
+  const int32_t src = pairs[2 * blockIdx.y], dst = pairs[2 * blockIdx.y + 1];
+  if (src < 0 || src >= num_blocks || dst < 0 || dst >= num_blocks) return;
+  const int64_t u = (int64_t)blockIdx.x * NTH + threadIdx.x;
+  const u32x4 x = ld<true>(reinterpret_cast<const u32x4*>(pool + src * block_bytes) + u);
+  st<true>(reinterpret_cast<u32x4*>(pool + dst * block_bytes) + u, x);
+}
+
 // Store and copy variants (the write side of every copy):
 //   NT      nontemporal (streaming) stores instead of the default policy
 //   VPL     16-byte vectors per lane per step: 1, or 2 adjacent (32 bytes)
@@ -612,6 +641,45 @@ int rkvc_block_copy_unr(void* pool, const int32_t* pairs, int n_pairs, int64_t b
     case 4: block_copy_unr_kernel<4><<<grid, 256, 0, st>>>(p, pairs, block_bytes, num_blocks); break;
     default: block_copy_unr_kernel<8><<<grid, 256, 0, st>>>(p, pairs, block_bytes, num_blocks); break;
   }
+  return launched();
+}
+
+// kind 0: write `bytes` of dst; 1: copy `bytes` from src to dst; 2: block
+// copies of the n_pairs pairs of block_bytes-byte blocks inside dst (src
+// unused); nth threads (64, 128, 256 or 512) and 16 nth bytes a workgroup.
+int rkvc_nth(int kind, const void* src, void* dst, int64_t bytes, const int32_t* pairs,
+             int n_pairs, int64_t block_bytes, int64_t num_blocks, int nth, void* stream) {
+  if (!dst || (nth != 64 && nth != 128 && nth != 256 && nth != 512) || kind < 0 || kind > 2)
+    return -1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid;
+  int64_t n = 0;
+  if (kind < 2) {
+    if (bytes < 16 || (bytes & 15) || (kind == 1 && !src)) return -1;
+    n = bytes >> 4;
+    const int64_t g = (n + nth - 1) / nth;
+    if (g > INT32_MAX) return -1;
+    grid = dim3((unsigned)g);
+  } else {
+    if (!pairs || n_pairs <= 0 || n_pairs > 65535 || block_bytes <= 0 || num_blocks <= 0 ||
+        block_bytes % (16 * nth))
+      return -1;
+    grid = dim3((unsigned)(block_bytes / (16 * nth)), (unsigned)n_pairs);
+  }
+  clear_errors();
+  u32x4* d = static_cast<u32x4*>(dst);
+  const u32x4* s = static_cast<const u32x4*>(src);
+  char* p = static_cast<char*>(dst);
+#define RKVC_NTH(T)                                                                           \
+  case T:                                                                                     \
+    if (kind == 0) write_nth_kernel<T><<<grid, T, 0, st>>>(d, n);                             \
+    else if (kind == 1) copy_nth_kernel<T><<<grid, T, 0, st>>>(s, d, n);                      \
+    else block_copy_nth_kernel<T><<<grid, T, 0, st>>>(p, pairs, block_bytes, num_blocks);    \
+    break;
+  switch (nth) {
+    RKVC_NTH(64) RKVC_NTH(128) RKVC_NTH(256) RKVC_NTH(512)
+  }
+#undef RKVC_NTH
   return launched();
 }
 

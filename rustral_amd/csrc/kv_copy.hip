@@ -135,7 +135,8 @@ __global__ __launch_bounds__(256) void append_kernel(
 // grid = (max_blocks_per_seq * (Hkv / HPW) * ppt, num_seqs, 2 [K,V]).  A
 // unit is 16 bytes of output (8 elements of a 16-bit output, 4 of an fp32
 // one) and its source elements; a (block, head) tile of block_size rows is
-// ppt pieces of 256 units.  One workgroup moves piece `piece` of HPW
+// ppt pieces of NTH units (NTH threads a workgroup).  One workgroup moves
+// piece `piece` of HPW
 // consecutive heads' tiles of one block: HPW units a thread, every load
 // issued before the first store.  Consecutive lanes take consecutive units
 // of a tile, so loads and stores of a wave are contiguous runs: a tile's
@@ -145,17 +146,28 @@ __global__ __launch_bounds__(256) void append_kernel(
 // of 8.  configs[1]'s gather (us per call; bf16 -> bf16, bf16 -> fp32,
 // fp32 -> fp32) by heads per workgroup HPW and pieces PPW: HPW 1 212 /
 // 421 / 480, 2 194 / 299 / 404, 4 198 / 332 / 433, 8 207 / 314 / 426; PPW 2
-// (a whole fp32 tile) with HPW 1 303 / 401, with HPW 2 307 / 425.  So 8 KiB
-// of output per workgroup; the previous kernel, a whole block (8 heads, 8-16
-// units a thread), ran 195 / 301 / 430.
+// (a whole fp32 tile) with HPW 1 303 / 401, with HPW 2 307 / 425 (all at
+// 256 threads).  So 8 KiB of output per workgroup for 16-bit pools, 4 KiB
+// (128 threads, below) for fp32 pools; the previous kernel, a whole block
+// (8 heads, 8-16 units a thread), ran 195 / 301 / 430.
 #ifndef RKV_GATHER_HPW
 #define RKV_GATHER_HPW 2  // heads (tiles) per workgroup, up to num_kv_heads
 #endif
 #ifndef RKV_GATHER_PPW
 #define RKV_GATHER_PPW 1  // pieces of each tile per workgroup
 #endif
-template <typename TIn, typename TOut, int DT, int HPW, int PPW>
-__global__ __launch_bounds__(256) void gather_kernel(
+// Threads per workgroup (= units per piece): 16-bit pools, and fp32 pools.
+// configs[1] (us per call; bf16 -> bf16, bf16 -> fp32, fp32 -> fp32) at
+// HPW 2: 256 threads 194 / 300 / 405, 128 threads 193 / 301 / 395, 64
+// threads 194 / 313 / 396.
+#ifndef RKV_GATHER_THREADS
+#define RKV_GATHER_THREADS 256
+#endif
+#ifndef RKV_GATHER_THREADS_F32
+#define RKV_GATHER_THREADS_F32 128
+#endif
+template <typename TIn, typename TOut, int DT, int HPW, int PPW, int NTH>
+__global__ __launch_bounds__(NTH) void gather_kernel(
     TOut* __restrict__ k_out, TOut* __restrict__ v_out, const TIn* __restrict__ k_pool,
     const TIn* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ ctx_lens,
@@ -202,7 +214,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
   uint4 y[PPW][HPW];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
-    const int u = (piece * PPW + q) * 256 + threadIdx.x;
+    const int u = (piece * PPW + q) * NTH + threadIdx.x;
     // loads are unconditional (a unit past the tile re-reads its last
     // unit) so each store waits for its own load only
     const int uc = u < tu ? u : tu - 1;
@@ -225,7 +237,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
   TOut* out = (is_v ? v_out : k_out) + seq_base + ((int64_t)h0 * row_stride + p0) * D;
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
-    const int u = (piece * PPW + q) * 256 + threadIdx.x;
+    const int u = (piece * PPW + q) * NTH + threadIdx.x;
     const int rr = u / upr, c = u - rr * upr;
     if (u < tu && rr < nt) {
 #pragma unroll
@@ -236,20 +248,25 @@ __global__ __launch_bounds__(256) void gather_kernel(
 }
 
 // ---- copy_blocks --------------------------------------------------------------
-// grid = (n_pairs * pieces, n_layers, 2 [K,V]); a piece is 4 KiB of a block
-// (pieces = ceil(block_bytes / 4096): a bf16 block of 8 heads x 16 rows x
-// 128 dims is 8 pieces, one per (block, head) tile) and each workgroup moves
-// one piece: one 16-byte load and one 16-byte store per thread, one round.
-// Measured on this part (32 KiB blocks in a 4 GiB pool, GB/s moved): the
-// same pairs copied 32 KiB per workgroup (8 loads then 8 stores a thread)
-// ran 5.97-6.06 with contiguous destinations and 5.28 with sparse sorted
-// ones; in 4 KiB pieces 6.37-6.41 and 5.67 (flat 4 GiB copies: 8 units a
-// thread 5.29, one 6.43).  The smaller the work per workgroup, the fewer
-// bytes the resident workgroups have in flight at once, and the fewer DRAM
-// rows the writes keep open.
-constexpr int kCopyPiece = 4096;  // bytes per workgroup
+// grid = (n_pairs * pieces, n_layers, 2 [K,V]); a piece is kCopyPiece bytes
+// of a block (a bf16 block of 8 heads x 16 rows x 128 dims is 32 pieces of
+// 1 KiB) and each workgroup -- one wave -- moves one piece: one 16-byte load
+// and one 16-byte store per lane, one round.  Measured on this part (32 KiB
+// blocks in a 4 GiB pool, GB/s moved, consecutive / random sources into
+// consecutive destinations): 32 KiB per workgroup (8 loads then 8 stores a
+// thread) 5.97-6.06; 4 KiB per 256-thread workgroup 6.37-6.44 / 6.41-6.44;
+// 2 KiB per 128 threads 6.37-6.38 / 6.43-6.48; 1 KiB per 64 threads
+// 6.66-6.69 / 6.68-6.71, as fast as a flat copy in the same shape (6.71-
+// 6.75; 4 KiB per workgroup 6.51-6.53).  The smaller the work per
+// workgroup, the fewer bytes the resident workgroups have in flight at once
+// and the fewer DRAM rows the writes keep open.
+#ifndef RKV_COPY_THREADS
+#define RKV_COPY_THREADS 64
+#endif
+constexpr int kCopyThreads = RKV_COPY_THREADS;
+constexpr int kCopyPiece = 16 * kCopyThreads;  // bytes per workgroup
 
-__global__ __launch_bounds__(256) void copy_blocks_kernel(
+__global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t layer_stride_bytes,
     const int32_t* __restrict__ pairs, int64_t block_bytes, int pieces, int64_t num_blocks) {
   const int64_t g = blockIdx.x;
@@ -346,16 +363,23 @@ __global__ __launch_bounds__(256) void append_q_kernel(
 #define RKV_GATHER_Q_NTS 1
 #endif
 // grid = (max_blocks_per_seq * (Hkv / HPW) * ppt, num_seqs, 2 [K,V]): one
-// piece of 256 words of HPW consecutive heads' (block, head) tiles per
+// piece of NTH words (NTH threads) of HPW consecutive heads' (block, head) tiles per
 // workgroup, HPW words (4 bytes in, 16 bytes of fp32 out each) per thread,
-// one round (a 16 x 128 tile is two pieces).  configs[1]'s gather over
-// 1-byte pools (us per call, int8 / fp8): HPW 1 493 / 505, 2 288 / 293,
-// 4 262 / 257, 8 271 / 276.
+// one round.  configs[1]'s gather over 1-byte pools (us per call, int8 /
+// fp8), 256 threads: HPW 1 493 / 505, 2 288 / 293, 4 262 / 257, 8 271 /
+// 276.  One configs[2] layer of 1-byte pools into the packed layout (int8,
+// us per call, one process, rotating over 32 layers) by threads x HPW:
+// 128 x 4 280, 256 x 4 288-291, 256 x 8 294, 64 x 4 292, 64 x 8 299,
+// 128 x 8 299-300.
 #ifndef RKV_GATHER_Q_HPW
 #define RKV_GATHER_Q_HPW 4
 #endif
+#ifndef RKV_GATHER_Q_THREADS
+#define RKV_GATHER_Q_THREADS 128  // threads per workgroup = words per piece
+#endif
+constexpr int kGatherQThreads = RKV_GATHER_Q_THREADS;
 template <int D, int FMT, int HPW>
-__global__ __launch_bounds__(256) void gather_q_kernel(
+__global__ __launch_bounds__(kGatherQThreads) void gather_q_kernel(
     float* __restrict__ k_out, float* __restrict__ v_out, const uint8_t* __restrict__ k_pool,
     const uint8_t* __restrict__ v_pool, const float* __restrict__ k_scale,
     const float* __restrict__ v_scale, const int32_t* __restrict__ block_tables,
@@ -390,7 +414,7 @@ __global__ __launch_bounds__(256) void gather_q_kernel(
   constexpr int U = D / 4;  // words per row
   const int tu = block_size * U;  // words per tile
   const int64_t row0 = ((int64_t)blk * num_kv_heads + h0) * block_size;  // first row of head h0
-  const int u = piece * 256 + threadIdx.x;
+  const int u = piece * kGatherQThreads + threadIdx.x;
   const int uc = u < tu ? u : tu - 1;  // loads are unconditional (the tile's last word)
   const uint32_t* src = reinterpret_cast<const uint32_t*>((is_v ? v_pool : k_pool) + row0 * D);
   const float* sc = (is_v ? v_scale : k_scale) + row0;
@@ -492,7 +516,8 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
   if (!aligned16(k_out) || !aligned16(v_out) || !aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
   const int epu = out_dtype == RKV_F32 ? 4 : 8;  // output elements per 16-byte unit
-  const int64_t pieces = ((int64_t)block_size * (head_dim / epu) + 255) / 256;
+  const int nth = dtype == RKV_F32 ? RKV_GATHER_THREADS_F32 : RKV_GATHER_THREADS;
+  const int64_t pieces = ((int64_t)block_size * (head_dim / epu) + nth - 1) / nth;
   const int ppw = pieces % RKV_GATHER_PPW == 0 ? RKV_GATHER_PPW : 1;
   const int64_t ppt = pieces / ppw;  // workgroups per tile
   // heads per workgroup: the build's choice when it divides num_kv_heads
@@ -505,7 +530,8 @@ extern "C" int rkv_gather(void* k_out, void* v_out, const void* k_pool, const vo
   dim3 grid((unsigned)gx, (unsigned)num_seqs, 2);
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define RKV_GATHER_HP(TI, TO, DT, H, P)                                                        \
-  gather_kernel<TI, TO, DT, H, P><<<grid, 256, 0, s>>>(                                        \
+  gather_kernel<TI, TO, DT, H, P,                                                              \
+                (sizeof(TI) == 4 ? RKV_GATHER_THREADS_F32 : RKV_GATHER_THREADS)><<<grid, nth, 0, s>>>(\
       static_cast<TO*>(k_out), static_cast<TO*>(v_out), static_cast<const TI*>(k_pool),        \
       static_cast<const TI*>(v_pool), block_tables, max_blocks_per_seq, ctx_lens, out_offsets, \
       num_kv_heads, head_dim, block_size, (int)ppt, num_blocks, max_ctx)
@@ -618,8 +644,10 @@ extern "C" int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, cons
     return fail(RKV_ERR_INVALID_ARG, "padded output needs max_ctx > 0");
   if (!aligned16(k_out) || !aligned16(v_out) || !aligned16(k_pool) || !aligned16(v_pool))
     return fail(RKV_ERR_INVALID_ARG, "pointers must be 16-byte aligned");
-  const int64_t ppt = ((int64_t)block_size * (head_dim / 4) + 255) / 256;
+  const int64_t ppt =
+      ((int64_t)block_size * (head_dim / 4) + kGatherQThreads - 1) / kGatherQThreads;
   const int hpw = num_kv_heads % RKV_GATHER_Q_HPW == 0 ? RKV_GATHER_Q_HPW
+                  : num_kv_heads % 4 == 0 && RKV_GATHER_Q_HPW > 4 ? 4
                   : num_kv_heads % 2 == 0 && RKV_GATHER_Q_HPW > 2 ? 2 : 1;
   const int64_t gx = (int64_t)max_blocks_per_seq * (num_kv_heads / hpw) * ppt;
   if (gx > INT32_MAX)
@@ -627,13 +655,14 @@ extern "C" int rkv_gather_q(float* k_out, float* v_out, const void* k_pool, cons
   const dim3 grid((unsigned)gx, (unsigned)num_seqs, 2);
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define RKV_GATHER_QH(D, F, H)                                                                  \
-  gather_q_kernel<D, F, H><<<grid, 256, 0, s>>>(                                                \
+  gather_q_kernel<D, F, H><<<grid, kGatherQThreads, 0, s>>>(                                    \
       k_out, v_out, static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool),   \
       k_scale, v_scale, block_tables, max_blocks_per_seq, ctx_lens, out_offsets, num_kv_heads,  \
       block_size, (int)ppt, num_blocks, max_ctx)
 #define RKV_GATHER_Q(D, F)                                                   \
   do {                                                                       \
     if (hpw == RKV_GATHER_Q_HPW) RKV_GATHER_QH(D, F, RKV_GATHER_Q_HPW);      \
+    else if (hpw == 4) RKV_GATHER_QH(D, F, (RKV_GATHER_Q_HPW > 4 ? 4 : 1));  \
     else if (hpw == 2) RKV_GATHER_QH(D, F, (RKV_GATHER_Q_HPW > 2 ? 2 : 1));  \
     else RKV_GATHER_QH(D, F, 1);                                             \
   } while (0)
@@ -667,9 +696,10 @@ extern "C" int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_
     return fail(RKV_ERR_INVALID_ARG, "pools must be 16-byte aligned");
   const int64_t pieces = (block_bytes + kCopyPiece - 1) / kCopyPiece;
   if ((int64_t)n_pairs * pieces > INT32_MAX)
-    return fail(RKV_ERR_INVALID_ARG, "n_pairs * ceil(block_bytes / 4096) exceeds 2^31 - 1");
+    return fail(RKV_ERR_INVALID_ARG, "n_pairs * ceil(block_bytes / " + std::to_string(kCopyPiece) +
+                                         ") exceeds 2^31 - 1");
   dim3 grid((unsigned)(n_pairs * pieces), (unsigned)n_layers, 2);
-  copy_blocks_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+  copy_blocks_kernel<<<grid, kCopyThreads, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<char*>(k_pool), static_cast<char*>(v_pool), layer_stride_bytes, pairs,
       block_bytes, (int)pieces, num_blocks);
   return check_launch("rkv_copy_blocks");
