@@ -82,17 +82,8 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) int i32x4_t;
 typedef __attribute__((ext_vector_type(4))) short bf16x4_t;
 
-// Converts one 16-byte load into E floats.
-__device__ __forceinline__ void to_float(const uint4& w, float (&f)[8]) {
-  f[0] = bf16_lo(w.x);
-  f[1] = bf16_hi(w.x);
-  f[2] = bf16_lo(w.y);
-  f[3] = bf16_hi(w.y);
-  f[4] = bf16_lo(w.z);
-  f[5] = bf16_hi(w.z);
-  f[6] = bf16_lo(w.w);
-  f[7] = bf16_hi(w.w);
-}
+// Converts one 16-byte load of an fp32 pool into 4 floats (16-bit pools
+// reach the matrix cores as they are stored).
 __device__ __forceinline__ void to_float(const uint4& w, float (&f)[4]) {
   f[0] = __uint_as_float(w.x);
   f[1] = __uint_as_float(w.y);
@@ -220,7 +211,7 @@ __device__ __forceinline__ float lo_col(float x) {
 template <typename T, int D, int G, int BS, int NTILE, int R, int SPLIT, int FMT,
           bool APPEND = false>
 __global__ __launch_bounds__(64 * SPLIT)
-__attribute__((amdgpu_waves_per_eu(RKV_DECODE_WAVES_PER_SIMD))) void decode_stream_kernel(
+__attribute__((amdgpu_waves_per_eu(G >= 8 ? 2 : RKV_DECODE_WAVES_PER_SIMD))) void decode_stream_kernel(
     float* __restrict__ out, float* __restrict__ part_acc, float* __restrict__ part_ml,
     const float* __restrict__ q, const void* __restrict__ k_pool_,
     const void* __restrict__ v_pool_, const float* __restrict__ k_scale,
