@@ -1032,6 +1032,21 @@ def run_ceilings(torch, dev, args):
     st = rate(stream_all, kv_bytes * n_layers)
     res["decode_tile_stream"] = {"GBps": st["GBps"], "us_per_layer": round(st["us"] / n_layers, 2),
                                  "kv_bytes_per_layer": kv_bytes}
+    # the same pattern at the partition shape the decode call picks for this
+    # workload (768 tokens: 8 waves of 6 tiles), which the decode kernel below
+    # runs
+    pick = kv.partition_size_for(B, HQ, HKV, D, kv._lib.RKV_BF16, max_ctx)
+    shape = {640: (10, 4), 768: (6, 8), 1280: (10, 8)}.get(pick)
+    if shape:
+        parts_p = (max_ctx + pick - 1) // pick
+
+        def stream_pick():
+            for q, k, v, t in layers:
+                C.tile_stream_shape(torch, k, v, t, ctx_d, sink, parts_p, *shape)
+        sp = rate(stream_pick, kv_bytes * n_layers)
+        res["decode_tile_stream_picked_shape"] = {
+            "partition_tokens": pick, "tiles_per_wave": shape[0], "waves": shape[1],
+            "GBps": sp["GBps"], "us_per_layer": round(sp["us"] / n_layers, 2)}
     ws = torch.empty(kv.workspace_bytes(B, HQ, D, max_ctx), dtype=torch.uint8, device=dev)
     out = torch.empty((B, HQ, D), device=dev)
     scale = 1.0 / math.sqrt(D)
@@ -1044,6 +1059,8 @@ def run_ceilings(torch, dev, args):
     res["decode_partition_kernel"] = {"GBps_kv": dp["GBps"],
                                       "us_per_layer": round(dp["us"] / n_layers, 2)}
     ratio = round(dp["GBps"] / st["GBps"], 4)
+    ratio_pick = (round(dp["GBps"] / res["decode_tile_stream_picked_shape"]["GBps"], 4)
+                  if "decode_tile_stream_picked_shape" in res else None)
     # the same shape, tables and q over 1-byte pools (int8 bytes, fp32 row scales)
     g8 = torch.Generator(device=dev).manual_seed(SEED + 1)
     layers8 = []
@@ -1082,6 +1099,7 @@ def run_ceilings(torch, dev, args):
                               "decode pattern", "flat_bytes": nbytes, "block_bytes": blk,
                   "block_pairs": npairs, "layers": n_layers},
                  decode_partition_over_stream=ratio,
+                 decode_partition_over_stream_same_shape=ratio_pick,
                  decode_int8_over_stream_1byte=round(d8["GBps"] / st8["GBps"], 4), results=res)
 
 

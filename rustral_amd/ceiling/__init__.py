@@ -29,6 +29,9 @@ _SIG = {
     "rkvc_tile_stream": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                          C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_int64, C.c_int, C.c_void_p,
                          C.c_uint, C.c_void_p],
+    "rkvc_tile_stream_shape": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int,
+                               C.c_int, C.c_int64, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_uint,
+                               C.c_void_p],
     "rkvc_nth": [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int, C.c_int64,
                  C.c_int64, C.c_int, C.c_void_p],
     "rkvc_tile_stream_1b": [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
@@ -196,3 +199,15 @@ def block_copy_nth(torch, pool, pairs, block_bytes: int, nth: int) -> None:
     nb = pool.numel() * pool.element_size() // block_bytes
     _ok(lib().rkvc_nth(2, None, pool.data_ptr(), 0, pairs.data_ptr(), pairs.shape[0], block_bytes,
                        nb, nth, _stream(torch, pool.device)), "rkvc_nth block copy")
+
+
+def tile_stream_shape(torch, k_pool, v_pool, tables, ctx_lens, sink, partitions: int,
+                      tiles_per_wave: int, waves: int) -> None:
+    """The bf16 decode pattern at (tiles a wave, waves a workgroup) = (10, 4),
+    (6, 8) or (10, 8): the 640-, 768- and 1280-token partition builds."""
+    nb, hkv = k_pool.shape[0], k_pool.shape[1]
+    _ok(lib().rkvc_tile_stream_shape(k_pool.data_ptr(), v_pool.data_ptr(), tables.data_ptr(),
+                                     tables.shape[1], ctx_lens.data_ptr(), tables.shape[0], hkv,
+                                     nb, partitions, tiles_per_wave, waves, sink.data_ptr(),
+                                     0x9E3779B9, _stream(torch, k_pool.device)),
+        "rkvc_tile_stream_shape")

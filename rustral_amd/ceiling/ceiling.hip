@@ -19,6 +19,8 @@
 //                     ring of 4 tiles, 1 KiB of whole rows per wave-load,
 //                     tiles past the context re-reading the wave's first
 //                     tile
+//   rkvc_tile_stream_shape  the bf16 decode pattern at the 768- and 1280-token
+//                     8-wave partition shapes
 //   rkvc_nth          write, copy and block copy, one 16-byte unit a thread,
 //                     by workgroup size (64 to 512 threads)
 //   rkvc_tile_stream_1b  variants of the 1-byte pattern: no scales, 2 or 4
@@ -127,11 +129,14 @@ __global__ __launch_bounds__(256) void block_copy_kernel(char* __restrict__ pool
 // eight 128-byte rows per wave-load, plus the fp32 row scales the decode
 // kernel reads (one K scale per lane and K tile, the V scales of the wave's
 // slice up front).
-constexpr int kD = 128, kBS = 16, kNTW = 10, kNT = 2 * kNTW, kR = 4, kSplit = 4;
-constexpr int kP = kNTW * kSplit * kBS;  // tokens per partition (640)
+// NTW tiles a wave and SPLIT waves a workgroup (partitions of 16 NTW SPLIT
+// tokens): 10 x 4 (640) is the decode kernel's 4-wave build, 6 x 8 (768) and
+// 10 x 8 (1280) its 8-wave builds.
+constexpr int kD = 128, kBS = 16, kNTW = 10, kR = 4, kSplit = 4;
+constexpr int kP = kNTW * kSplit * kBS;  // tokens per partition of the 1-byte variants (640)
 
-template <int EB>
-__global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
+template <int EB, int NTW = kNTW, int SPLIT = kSplit>
+__global__ __launch_bounds__(64 * SPLIT) void tile_stream_kernel(
     const uint8_t* __restrict__ k_pool, const uint8_t* __restrict__ v_pool,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale,
     const int32_t* __restrict__ tables, int max_blocks, const int32_t* __restrict__ ctx_lens,
@@ -141,26 +146,27 @@ __global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
   constexpr int NL = kBS / RPL;         // wave-loads per tile
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kh = blockIdx.x, part = blockIdx.y, b = blockIdx.z;
+  constexpr int P = NTW * SPLIT * kBS;
   const int L = ctx_lens[b];
-  if (part * kP >= L) return;
-  const int lb0 = part * (kP / kBS) + w * kNTW;
+  if (part * P >= L) return;
+  const int lb0 = part * (P / kBS) + w * NTW;
   const int32_t* tab = tables + (int64_t)b * max_blocks;
-  int32_t pb[kNTW];
+  int32_t pb[NTW];
 #pragma unroll
-  for (int i = 0; i < kNTW; ++i) {
+  for (int i = 0; i < NTW; ++i) {
     const int lb = lb0 + i;
     pb[i] = tab[lb < max_blocks ? lb : max_blocks - 1];
   }
   const int32_t pb0 = pb[0] >= 0 && pb[0] < num_blocks ? pb[0] : 0;
-  int64_t row0[kNTW];  // first token row of each (block, head) tile
+  int64_t row0[NTW];  // first token row of each (block, head) tile
 #pragma unroll
-  for (int i = 0; i < kNTW; ++i) {
+  for (int i = 0; i < NTW; ++i) {
     const bool ok = (lb0 + i) * kBS < L && pb[i] >= 0 && pb[i] < num_blocks;
     row0[i] = ((int64_t)(ok ? pb[i] : pb0) * num_kv_heads + kh) * kBS;
   }
   const uint32_t off = (lane / (64 / RPL)) * ROW + (lane % (64 / RPL)) * 16;
   auto tile_load = [&](int t, int n) __attribute__((always_inline)) {
-    const uint8_t* p = (t < kNTW ? k_pool : v_pool) + row0[t % kNTW] * ROW;
+    const uint8_t* p = (t < NTW ? k_pool : v_pool) + row0[t % NTW] * ROW;
     return ld<true>(reinterpret_cast<const u32x4*>(p + off + n * 1024));
   };
   unsigned acc = 0;
@@ -172,18 +178,18 @@ __global__ __launch_bounds__(64 * kSplit) void tile_stream_kernel(
   float sc = 0.0f;
   if constexpr (EB == 1) {
 #pragma unroll
-    for (int i = 0; i < kNTW; ++i) sc += k_scale[row0[i] + (lane & 15)];
+    for (int i = 0; i < NTW; ++i) sc += k_scale[row0[i] + (lane & 15)];
 #pragma unroll
-    for (int j = 0; j < (kNTW * kBS + 63) / 64; ++j) {
+    for (int j = 0; j < (NTW * kBS + 63) / 64; ++j) {
       const int x = lane + 64 * j;
-      if (x < kNTW * kBS) sc += v_scale[row0[x / kBS] + x % kBS];
+      if (x < NTW * kBS) sc += v_scale[row0[x / kBS] + x % kBS];
     }
   }
-  static_for<0, kNT>([&](auto tc) __attribute__((always_inline)) {
+  static_for<0, 2 * NTW>([&](auto tc) __attribute__((always_inline)) {
     constexpr int t = decltype(tc)::value;
 #pragma unroll
     for (int n = 0; n < NL; ++n) acc ^= fold(ring[t % kR][n]) + t;
-    if constexpr (t + kR < kNT) {
+    if constexpr (t + kR < 2 * NTW) {
 #pragma unroll
       for (int n = 0; n < NL; ++n) ring[t % kR][n] = tile_load(t + kR, n);
     }
@@ -711,6 +717,29 @@ int rkvc_tile_stream(const void* k_pool, const void* v_pool, const float* k_scal
   auto kern = elem_bytes == 2 ? tile_stream_kernel<2> : tile_stream_kernel<1>;
   kern<<<grid, 64 * kSplit, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool), k_scale, v_scale,
+      tables, max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
+  return launched();
+}
+
+// The bf16 decode pattern at the partition shapes of the decode kernel's
+// builds: (tiles a wave, waves a workgroup) = (10, 4) 640 tokens, (6, 8)
+// 768, (10, 8) 1280; grid (Hkv, partitions, sequences) as rkvc_tile_stream.
+int rkvc_tile_stream_shape(const void* k_pool, const void* v_pool, const int32_t* tables,
+                           int max_blocks, const int32_t* ctx_lens, int num_seqs,
+                           int num_kv_heads, int64_t num_blocks, int partitions, int ntw,
+                           int split, unsigned* sink, unsigned magic, void* stream) {
+  if (!k_pool || !v_pool || !tables || !ctx_lens || !sink || max_blocks <= 0 || num_seqs <= 0 ||
+      num_kv_heads <= 0 || num_blocks <= 0 || partitions <= 0)
+    return -1;
+  auto kern = ntw == 10 && split == 4   ? tile_stream_kernel<2, 10, 4>
+              : ntw == 6 && split == 8  ? tile_stream_kernel<2, 6, 8>
+              : ntw == 10 && split == 8 ? tile_stream_kernel<2, 10, 8>
+                                        : nullptr;
+  if (!kern) return -1;
+  const dim3 grid((unsigned)num_kv_heads, (unsigned)partitions, (unsigned)num_seqs);
+  clear_errors();
+  kern<<<grid, 64 * split, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint8_t*>(k_pool), static_cast<const uint8_t*>(v_pool), nullptr, nullptr,
       tables, max_blocks, ctx_lens, num_kv_heads, num_blocks, sink, magic);
   return launched();
 }

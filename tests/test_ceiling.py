@@ -10,7 +10,7 @@ import torch
 from rustral_amd import ceiling as C
 
 NAMES = ("rkvc_read", "rkvc_write", "rkvc_copy", "rkvc_block_copy", "rkvc_tile_stream",
-         "rkvc_tile_stream_1b", "rkvc_nth")
+         "rkvc_tile_stream_1b", "rkvc_nth", "rkvc_tile_stream_shape")
 
 
 def test_library_loads_and_exports_the_stream_kernels():
@@ -34,6 +34,8 @@ def test_arguments_are_checked_before_any_launch():
     assert L.rkvc_nth(0, None, 16, 1 << 20, None, 0, 0, 0, 96, None) != 0
     assert L.rkvc_nth(1, 16, 16, 100, None, 0, 0, 0, 64, None) != 0
     assert L.rkvc_nth(2, None, 16, 0, 16, 1, 1000, 4, 64, None) != 0
+    # a partition shape the decode kernel has no build for
+    assert L.rkvc_tile_stream_shape(16, 16, 16, 4, 16, 1, 8, 64, 1, 7, 8, 16, 0, None) != 0
     # the 1-byte pattern variants: an unknown variant, heads not divisible by
     # the heads per wave, scales missing where the variant reads them
     assert L.rkvc_tile_stream_1b(16, 16, 16, 16, 16, 4, 16, 1, 8, 64, 1, 6, 16, 0, None) != 0
@@ -73,6 +75,8 @@ def test_copies_are_bit_exact_and_streams_leave_the_sink(dev):
     tab = torch.tensor([[3, 9, -1, 70], [5, 6, 7, 8]], dtype=torch.int32, device=dev)
     ctx = torch.tensor([40, 64], dtype=torch.int32, device=dev)
     C.tile_stream(torch, k, v, tab, ctx, sink, partitions=1)
+    for tpw, waves in ((10, 4), (6, 8), (10, 8)):
+        C.tile_stream_shape(torch, k, v, tab, ctx, sink, 1, tpw, waves)
     k8 = torch.randint(0, 255, (nb, hkv, 16, 128), generator=g, dtype=torch.uint8, device=dev)
     v8 = torch.randint(0, 255, (nb, hkv, 16, 128), generator=g, dtype=torch.uint8, device=dev)
     ks = torch.rand((nb, hkv, 16), generator=g, device=dev)
