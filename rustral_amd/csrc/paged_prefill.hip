@@ -34,6 +34,7 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 namespace rkv {
@@ -75,13 +76,13 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t& hi, uint32_t&
   lo = cvt_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
 }
 
-template <typename T, int D, int G, int HW, int QS, int KB>
-__global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
+template <typename T, int D, int G, int HW, int QS, int KB, bool PFN>
+__global__ __launch_bounds__(64 * (G / HW) * QS) __attribute__((amdgpu_waves_per_eu(2))) void prefill_kernel(
     float* __restrict__ out, const float* __restrict__ q, const void* __restrict__ k_pool_,
     const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ q_start,
     const int32_t* __restrict__ ctx_lens, int num_kv_heads, int64_t num_blocks, int max_q_len,
-    float q_scale, int heavy_first) {
+    float q_scale, int heavy_first, int pf_stride) {
   constexpr bool F32 = sizeof(T) == 4;
   static_assert(G % HW == 0, "heads per wave must divide the group");
   constexpr int NT = 64 * (G / HW) * QS;
@@ -168,10 +169,10 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
   // Two register sets: the loads of iteration it + 2 are issued while
   // iteration it is computed (one workgroup fills a CU, so its own loads
   // have to be in flight early).
-  uint4 kr0[PT], vr0[PT], kr1[PT], vr1[PT];
+  u32x4_t kr0[PT], vr0[PT], kr1[PT], vr1[PT];
   // Issues the K/V loads of the KB blocks with ids id into registers;
   // returns a bit per block whose id is valid.
-  auto fetch = [&](const int32_t (&id)[KB], uint4 (&kr)[PT], uint4 (&vr)[PT])
+  auto fetch = [&](const int32_t (&id)[KB], u32x4_t (&kr)[PT], u32x4_t (&vr)[PT])
                    __attribute__((always_inline)) {
     uint32_t okm = 0;
     int64_t base[KB];
@@ -190,14 +191,14 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
         int64_t bb = base[0];  // base[kb] by selects (kb is not a compile-time index)
 #pragma unroll
         for (int x = 1; x < KB; ++x) bb = kb == x ? base[x] : bb;
-        kr[i] = *reinterpret_cast<const uint4*>(k_pool + bb + cc * CE);
-        vr[i] = *reinterpret_cast<const uint4*>(v_pool + bb + cc * CE);
+        kr[i] = *reinterpret_cast<const u32x4_t*>(k_pool + bb + cc * CE);
+        vr[i] = *reinterpret_cast<const u32x4_t*>(v_pool + bb + cc * CE);
       }
     }
     return okm;
   };
   // Writes the registers into LDS buffer buf (K and V row-major).
-  auto stage = [&](int buf, const uint4 (&kr)[PT], const uint4 (&vr)[PT])
+  auto stage = [&](int buf, const u32x4_t (&kr)[PT], const u32x4_t (&vr)[PT])
                    __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < PT; ++i) {
@@ -208,8 +209,8 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
         uint16_t* kd = &s_k[buf][0][(kb * kBS + key) * KP + col];
         uint16_t* vd = &s_v[buf][0][(kb * kBS + key) * VKP + col];
         if constexpr (!F32) {
-          *reinterpret_cast<uint4*>(kd) = kr[i];
-          *reinterpret_cast<uint4*>(vd) = vr[i];
+          *reinterpret_cast<u32x4_t*>(kd) = kr[i];
+          *reinterpret_cast<u32x4_t*>(vd) = vr[i];
         } else {
           constexpr int KS = KB * kBS * KP, VS = KB * kBS * VKP;  // slice strides
           const float kf[4] = {__uint_as_float(kr[i].x), __uint_as_float(kr[i].y),
@@ -284,6 +285,38 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
     for (int c = 0; c < NO; ++c) o[hh][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     m[hh] = -INFINITY;
     l[hh] = 0.0f;
+  }
+
+  // PFN: the q rows of the workgroup pf_stride places later in dispatch
+  // order (the one that takes a slot of this round when one frees up, on the
+  // same XCD when pf_stride is a multiple of 8) are touched now, one 4-byte
+  // load per 64-byte line, while this workgroup computes and HBM has little
+  // else to do: that workgroup then finds them in the caches instead of
+  // queueing behind this round's output stores.  Issued after this wave's q
+  // and first K/V loads, so waits for those are not held up; the values are
+  // consumed (by an empty asm) only at the end of the kernel.
+  constexpr int LPR = G * D * 4 / 64;  // 64-byte lines of one (token, KV head) q row
+  constexpr int PF = PFN ? (QT * LPR + NT - 1) / NT : 1;
+  float pfv[PF];
+  if constexpr (PFN) {
+    const int j = (int)(blockIdx.x + gridDim.x * blockIdx.y) + pf_stride;
+    const bool pf_on = heavy_first && pf_stride > 0 && j < (int)(gridDim.x * gridDim.y);
+    const int jx = pf_on ? j % (int)gridDim.x : 0, jy = pf_on ? j / (int)gridDim.x : 0;
+    const int jqt = (int)gridDim.y - 1 - jy, jkh = jx % num_kv_heads, jb = jx / num_kv_heads;
+    const int js0 = pf_on ? q_start[jb] : 0;
+    const int jn = pf_on ? q_start[jb + 1] - js0 : 0;
+    const int jnr = jn < max_q_len ? jn : max_q_len;
+    const int jq0 = jqt * QT;
+    const int jrows = jnr - jq0 < QT ? jnr - jq0 : QT;  // <= 0: nothing to touch
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int u = tid + i * NT, row = u / LPR, line = u % LPR;
+      const bool on = pf_on && u < QT * LPR && row < jrows;
+      // off: this wave's own first q line (already loaded) is read again
+      const int64_t off = on ? ((int64_t)(js0 + jq0 + row) * num_q_heads + jkh * G) * D + 16 * line
+                             : ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h0) * D;
+      pfv[i] = q[off];
+    }
   }
 
   // Iteration it on LDS buffer buf (okm: valid blocks of the iteration).
@@ -585,10 +618,14 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) void prefill_kernel(
       }
     }
   }
+  if constexpr (PFN) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) asm volatile("" ::"v"(pfv[i]));
+  }
 }
 
 using PrefillFn = void (*)(float*, const float*, const void*, const void*, const int32_t*, int,
-                           const int32_t*, const int32_t*, int, int64_t, int, float, int);
+                           const int32_t*, const int32_t*, int, int64_t, int, float, int, int);
 
 // Waves per workgroup, query heads per wave (for groups of at least 4 heads)
 // and key blocks per staged iteration.  With 8 waves a workgroup may hold up
@@ -607,7 +644,24 @@ using PrefillFn = void (*)(float*, const float*, const void*, const void*, const
 #ifndef RKV_PREFILL_HEAVY_FIRST
 #define RKV_PREFILL_HEAVY_FIRST 1
 #endif
+// The build for calls whose sequences hold at most as many cached keys as
+// new tokens (bf16 pools, 4 query heads per KV head, D = 128): workgroups of
+// RKV_PREFILL_SHORT_WAVES waves (32-row tiles, two workgroups per CU at 235
+// VGPRs and 68 KB of LDS) that touch the q rows of the next round's
+// workgroups (RKV_PREFILL_PREFETCH).  Longer cached prefixes keep the 8-wave
+// 64-row tiles, which stage each K/V tile for twice the rows.  us per call
+// (one box, events): 25 x 128 new tokens 28.7 against 30.3; 8 x 512 square
+// 51.5 / 52.6; 4 x 2048 square 238 / 253; 8 x 512 after 512 cached 104 /
+// 104; 25 x 128 after 384 cached 65.7 / 66.2; after 896 cached 117 / 114;
+// 8 x 512 after 1536 cached 210 / 204; after 3584 cached 430 / 413.
+#ifndef RKV_PREFILL_SHORT_WAVES
+#define RKV_PREFILL_SHORT_WAVES 4
+#endif
+#ifndef RKV_PREFILL_PREFETCH
+#define RKV_PREFILL_PREFETCH 1
+#endif
 constexpr int kWaves = RKV_PREFILL_WAVES;
+constexpr int kShortWaves = RKV_PREFILL_SHORT_WAVES;
 constexpr int kHW = RKV_PREFILL_HW;
 constexpr int kKB = RKV_PREFILL_KB;
 
@@ -615,33 +669,65 @@ struct PrefillCfg {
   PrefillFn fn;
   int waves;   // per workgroup
   int tile;    // query tokens per workgroup
+  bool next;   // touches the next round's q rows (wants pf_stride)
 };
 
-template <typename T, int D, int G>
+// Workgroups of fn (threads each) resident on the current device at once:
+// compute units x workgroups per compute unit, asked of the runtime once per
+// (device, kernel) and kept; 0 if the runtime cannot say.
+int resident_workgroups(PrefillFn fn, int threads) {
+  struct Entry {
+    PrefillFn fn;
+    int device, resident;
+  };
+  static std::mutex mu;
+  static Entry table[256];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (table[i].fn == fn && table[i].device == dev) return table[i].resident;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
+                                                   threads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int resident = cus * per_cu;
+  if (used < 256) table[used++] = {fn, dev, resident};
+  return resident;
+}
+
+template <typename T, int D, int G, int W, bool PFN>
 PrefillCfg cfg_g() {
   constexpr int HW = G >= 4 && G % kHW == 0 ? kHW : 1;
-  constexpr int QS = kWaves / (G / HW) > 0 ? kWaves / (G / HW) : 1;  // row sub-tiles
-  return {&prefill_kernel<T, D, G, HW, QS, kKB>, (G / HW) * QS, 16 * QS};
+  constexpr int QS = W / (G / HW) > 0 ? W / (G / HW) : 1;  // row sub-tiles
+  return {&prefill_kernel<T, D, G, HW, QS, kKB, PFN>, (G / HW) * QS, 16 * QS, PFN};
 }
 
 template <typename T, int D>
-PrefillCfg pick_g(int G) {
+PrefillCfg pick_g(int G, bool short_prefix) {
   switch (G) {
-    case 1: return cfg_g<T, D, 1>();
-    case 2: return cfg_g<T, D, 2>();
-    case 4: return cfg_g<T, D, 4>();
-    case 8: return cfg_g<T, D, 8>();
-    default: return {nullptr, 0, 0};
+    case 1: return cfg_g<T, D, 1, kWaves, false>();
+    case 2: return cfg_g<T, D, 2, kWaves, false>();
+    case 4:
+      if constexpr (std::is_same<T, uint16_t>::value && D == 128)
+        if (short_prefix) return cfg_g<T, D, 4, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
+      return cfg_g<T, D, 4, kWaves, false>();
+    case 8: return cfg_g<T, D, 8, kWaves, false>();
+    default: return {nullptr, 0, 0, false};
   }
 }
 
 template <typename T>
-PrefillCfg pick_d(int D, int G) {
+PrefillCfg pick_d(int D, int G, bool short_prefix) {
   switch (D) {
-    case 32: return pick_g<T, 32>(G);
-    case 64: return pick_g<T, 64>(G);
-    case 128: return pick_g<T, 128>(G);
-    default: return {nullptr, 0, 0};
+    case 32: return pick_g<T, 32>(G, short_prefix);
+    case 64: return pick_g<T, 64>(G, short_prefix);
+    case 128: return pick_g<T, 128>(G, short_prefix);
+    default: return {nullptr, 0, 0, false};
   }
 }
 
@@ -668,8 +754,11 @@ extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_p
   if (block_size != kBS)
     return fail(RKV_ERR_UNSUPPORTED, "rkv_prefill_attention: block_size must be 16");
   const int G = num_q_heads / num_kv_heads;
-  const PrefillCfg cfg =
-      dtype == RKV_BF16 ? pick_d<uint16_t>(head_dim, G) : pick_d<float>(head_dim, G);
+  // at most as many cached keys as new tokens, judged by the table width
+  // (the keys a sequence can hold) against the longest new-token run
+  const bool short_prefix = (int64_t)max_blocks_per_seq * kBS <= 2 * (int64_t)max_q_len;
+  const PrefillCfg cfg = dtype == RKV_BF16 ? pick_d<uint16_t>(head_dim, G, short_prefix)
+                                           : pick_d<float>(head_dim, G, short_prefix);
   if (!cfg.fn)
     return fail(RKV_ERR_UNSUPPORTED,
                 "rkv_prefill_attention: head_dim must be 32, 64 or 128 and num_q_heads / "
@@ -691,8 +780,11 @@ extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_p
   const int heavy = RKV_PREFILL_HEAVY_FIRST && n_tiles <= 65535 && n_heads <= 0x7fffffff;
   const dim3 grid = heavy ? dim3((unsigned)n_heads, (unsigned)n_tiles, 1)
                           : dim3((unsigned)n_tiles, (unsigned)num_kv_heads, (unsigned)num_seqs);
+  // the workgroup that takes this one's slot in the next round is
+  // `resident` places later in dispatch order
+  const int pf_stride = cfg.next && heavy ? resident_workgroups(cfg.fn, 64 * cfg.waves) : 0;
   hipLaunchKernelGGL(cfg.fn, grid, dim3(64 * cfg.waves), 0, static_cast<hipStream_t>(stream), out, q, k_pool,
                      v_pool, block_tables, max_blocks_per_seq, q_start, ctx_lens, num_kv_heads,
-                     num_blocks, max_q_len, scale * kLog2e, heavy);
+                     num_blocks, max_q_len, scale * kLog2e, heavy, pf_stride);
   return check_launch("rkv_prefill_attention");
 }

@@ -70,6 +70,53 @@ def test_prefill_config4_admission_shape(dev):
     assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle")
 
 
+def short_prefix_case(seed, n_seq, n_max, with_edges):
+    """Ragged sequences of 1 .. n_max new tokens with at most as many cached
+    keys as new ones (contexts up to 1.5 n_max); with_edges adds a sequence without new tokens and one
+    with more new tokens than context (zero rows before position 0)."""
+    rng = np.random.default_rng(seed)
+    n_new = rng.integers(1, n_max + 1, size=n_seq).astype(np.int32)
+    n_new[0] = n_max
+    ctx = (n_new + rng.integers(0, n_new + 1)).astype(np.int32)
+    ctx = np.minimum(ctx, n_max + n_max // 2).astype(np.int32)
+    if with_edges:
+        n_new[1], ctx[1] = 0, 30
+        n_new[2], ctx[2] = 50, 20
+    return n_new, ctx
+
+
+@pytest.mark.parametrize("seed,n_seq,n_max,with_edges",
+                         [(60, 40, 128, False), (61, 33, 96, True), (62, 7, 256, True)])
+def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges):
+    """Calls whose tables hold at most twice the longest new-token run take
+    the 4-wave build that touches the next round's q rows (bf16, Hq 32, Hkv 8,
+    D 128); grids of 448 to 1,280 workgroups (one round of 512 resident
+    workgroups to two and a half), so the touched rows include tiles past a
+    sequence's end.  Against the oracle, and bit-equal to the
+    8-wave build, which a wider table (extra -1 entries) selects."""
+    n_new, ctx = short_prefix_case(seed, n_seq, n_max, with_edges)
+    say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max}")
+    q, kp, vp, _, _, tables, qs = case(seed, 32, 8, 128, n_new, ctx, "bf16")
+    assert tables.shape[1] * 16 <= 2 * int(n_new.max())
+    got = run_gpu(dev, q, kp, vp, tables, qs, ctx, 0.088)
+    want = oracle.prefill_attention(q, kp, vp, tables, qs, ctx, 0.088)
+    assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle")
+    if with_edges:
+        assert np.all(got[qs[2]:qs[2] + 30] == 0.0)
+    wide = np.full((tables.shape[0], 2 * tables.shape[1] + 1), -1, np.int32)
+    wide[:, :tables.shape[1]] = tables
+    long_build = run_gpu(dev, q, kp, vp, wide, qs, ctx, 0.088)
+    assert np.array_equal(got, long_build)
+    # the rows past a max_q_len cap stay unwritten in the short build too
+    # (the cap still at least half the table's keys)
+    cap = (tables.shape[1] * 16 + 1) // 2
+    assert cap < n_max
+    capped = run_gpu(dev, q, kp, vp, tables, qs, ctx, 0.088, max_q_len=cap)
+    rows = np.concatenate([np.arange(qs[b], qs[b] + min(cap, n_new[b])) for b in range(n_seq)])
+    assert np.array_equal(capped[rows], got[rows])
+    assert np.all(capped[np.setdiff1d(np.arange(qs[-1]), rows)] == 0.0)
+
+
 def test_prefill_long_chunk_after_long_context(dev):
     n_new = np.array([200, 64], np.int32)
     ctx = np.array([3000, 1100], np.int32)
