@@ -299,9 +299,9 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) __attribute__((amdgpu_waves_per
   constexpr int PF = PFN ? (QT * LPR + NT - 1) / NT : 1;
   float pfv[PF];
   if constexpr (PFN) {
-    const int j = (int)(blockIdx.x + gridDim.x * blockIdx.y) + pf_stride;
-    const bool pf_on = heavy_first && pf_stride > 0 && j < (int)(gridDim.x * gridDim.y);
-    const int jx = pf_on ? j % (int)gridDim.x : 0, jy = pf_on ? j / (int)gridDim.x : 0;
+    const int64_t j = (int64_t)blockIdx.x + (int64_t)gridDim.x * blockIdx.y + pf_stride;
+    const bool pf_on = heavy_first && pf_stride > 0 && j < (int64_t)gridDim.x * gridDim.y;
+    const int jx = pf_on ? (int)(j % gridDim.x) : 0, jy = pf_on ? (int)(j / gridDim.x) : 0;
     const int jqt = (int)gridDim.y - 1 - jy, jkh = jx % num_kv_heads, jb = jx / num_kv_heads;
     const int js0 = pf_on ? q_start[jb] : 0;
     const int jn = pf_on ? q_start[jb + 1] - js0 : 0;
