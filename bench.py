@@ -485,7 +485,10 @@ def run_prefill(torch, dev, args):
     sequences x 128 new prompt tokens (ctx == 128), Hq 32, Hkv 8, D 128, bf16
     pool, 32 layers (distinct q and pools per layer), one call per layer.  A
     second figure: a chunked prefill of 512 new tokens after 3584 cached ones
-    for 8 sequences (the compute-heavy end)."""
+    for 8 sequences (the compute-heavy end).  us_per_call times the layers'
+    calls back to back (events around each burst of 32, as a forward pass
+    keeps the GPU busy); us_per_call_events_each times each call between
+    events of its own (the GPU idles between calls)."""
     import numpy as np
     from rustral_amd import kv
     g = torch.Generator(device=dev).manual_seed(7)
@@ -516,8 +519,26 @@ def run_prefill(torch, dev, args):
         def call():
             q, k, v, t, o = layers[next(it) % n_layers]
             kv.prefill_attention(q, k, v, t, qs, cl, 1.0 / math.sqrt(D), max_q_len=mq, out=o)
-        for _ in range(n_layers):
-            call()
+        # untimed passes over the layers for at least 50 ms: the clock
+        # takes ~15 ms of this load to settle (admissions: 27-33 us per call
+        # over the first ~15 bursts of 32, 26.0 after)
+        t_warm = time.perf_counter()
+        while True:
+            for _ in range(n_layers):
+                call()
+            torch.cuda.synchronize()
+            if time.perf_counter() - t_warm > 0.05:
+                break
+        # the layers' calls back to back, events around each burst (the GPU
+        # stays busy, as in a forward pass), then with events around each call
+        bursts = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(reps_per_layer)]
+        torch.cuda.synchronize()
+        for a, e in bursts:
+            a.record()
+            for _ in range(n_layers):
+                call()
+            e.record()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(n_layers * reps_per_layer)]
         torch.cuda.synchronize()
@@ -526,17 +547,18 @@ def run_prefill(torch, dev, args):
             call()
             e.record()
         torch.cuda.synchronize()
-        us = 1e3 * sum(a.elapsed_time(e) for a, e in ev) / len(ev)
+        us_burst = 1e3 * sum(a.elapsed_time(e) for a, e in bursts) / (len(bursts) * n_layers)
+        us_each = 1e3 * sum(a.elapsed_time(e) for a, e in ev) / len(ev)
         del layers
         torch.cuda.empty_cache()
-        return us
+        return us_burst, us_each
 
     n_adm = np.full(25, 128, np.int32)
-    us_adm = measure(n_adm, n_adm, 32, max(args.steps // 4, 3))
+    us_adm, us_adm_each = measure(n_adm, n_adm, 32, max(args.steps // 4, 3))
     b_adm, f_adm = prefill_bytes_flops(n_adm, n_adm)
     n_chk = np.full(8, 512, np.int32)
     c_chk = np.full(8, 4096, np.int32)
-    us_chk = measure(n_chk, c_chk, 8, max(args.steps // 4, 3))
+    us_chk, us_chk_each = measure(n_chk, c_chk, 8, max(args.steps // 4, 3))
     b_chk, f_chk = prefill_bytes_flops(n_chk, c_chk)
     gbps = b_adm / (us_adm * 1e-6) / 1e9
     return _line("causal prefill over paged KV GB/s (configs[4] admissions: 25 x 128 tokens)", gbps,
@@ -544,9 +566,11 @@ def run_prefill(torch, dev, args):
                  {"workload": "paged causal prefill, configs[4] admission shape", "sequences": 25,
                   "new_tokens": 128, "context": 128, "num_q_heads": HQ, "num_kv_heads": HKV,
                   "head_dim": D, "block_size": BS, "layers": 32},
-                 us_per_call=round(us_adm, 2), algorithmic_bytes_per_call=b_adm,
+                 us_per_call=round(us_adm, 2), us_per_call_events_each=round(us_adm_each, 2),
+                 algorithmic_bytes_per_call=b_adm,
                  flops_per_call=f_adm, tflops=round(f_adm / (us_adm * 1e-6) / 1e12, 2),
                  chunked_512_after_3584={"sequences": 8, "us_per_call": round(us_chk, 2),
+                                         "us_per_call_events_each": round(us_chk_each, 2),
                                          "bytes": b_chk, "flops": f_chk,
                                          "GBps": round(b_chk / (us_chk * 1e-6) / 1e9, 1),
                                          "tflops": round(f_chk / (us_chk * 1e-6) / 1e12, 2)})
@@ -1352,6 +1376,14 @@ def main():
         for i in range(n_layers):
             call(i, "both")
     graph.replay()
+    # untimed replays for at least 100 ms more: the clock takes ~15 ms of
+    # sustained load to settle
+    warm_replays, t_warm = 1, time.perf_counter()
+    while time.perf_counter() - t_warm < 0.1:
+        for _ in range(4):
+            graph.replay()
+        torch.cuda.synchronize()
+        warm_replays += 4
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     start, stop = ev(), ev()
     marks_step = [ev() for _ in range(args.steps + 1)]   # per-replay boundaries
@@ -1450,6 +1482,7 @@ def main():
         "decode_tokens_per_s_b64": round(tokens_per_s, 1),
         "us_per_call": round(call_us, 2),
         "step_ms_stats": step_stats,
+        "untimed_replays_before_timing": warm_replays,
         "value_at_p50_step": round(bytes_call * n_layers / (step_stats["p50"] * 1e-3) / 1e9, 2),
         "step_ms_eager_with_events": round(ms_step_eager, 4),
         "partition_kernel_us": round(avg_burst_part_us, 2),

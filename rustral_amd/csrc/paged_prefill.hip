@@ -82,7 +82,7 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) __attribute__((amdgpu_waves_per
     const void* __restrict__ v_pool_, const int32_t* __restrict__ block_tables,
     int max_blocks_per_seq, const int32_t* __restrict__ q_start,
     const int32_t* __restrict__ ctx_lens, int num_kv_heads, int64_t num_blocks, int max_q_len,
-    float q_scale, int heavy_first, int pf_stride) {
+    float q_scale, int heavy_first, int pf_stride, int pf_first) {
   constexpr bool F32 = sizeof(T) == 4;
   static_assert(G % HW == 0, "heads per wave must divide the group");
   constexpr int NT = 64 * (G / HW) * QS;
@@ -287,20 +287,22 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) __attribute__((amdgpu_waves_per
     l[hh] = 0.0f;
   }
 
-  // PFN: the q rows of the workgroup pf_stride places later in dispatch
-  // order (the one that takes a slot of this round when one frees up, on the
-  // same XCD when pf_stride is a multiple of 8) are touched now, one 4-byte
-  // load per 64-byte line, while this workgroup computes and HBM has little
-  // else to do: that workgroup then finds them in the caches instead of
-  // queueing behind this round's output stores.  Issued after this wave's q
-  // and first K/V loads, so waits for those are not held up; the values are
-  // consumed (by an empty asm) only at the end of the kernel.
+  // PFN: workgroups from pf_first on touch the q rows of the workgroup
+  // pf_stride places later in dispatch order (one that starts when a slot of
+  // the first round frees up, on the same XCD when pf_stride is a multiple
+  // of 8), one 4-byte load per 64-byte line, while they compute and HBM has
+  // little else to do: that workgroup then finds them in the caches instead
+  // of queueing behind the first round's output stores.  Issued after this
+  // wave's q and first K/V loads, so waits for those are not held up; the
+  // values are consumed (by an empty asm) only at the end of the kernel.
   constexpr int LPR = G * D * 4 / 64;  // 64-byte lines of one (token, KV head) q row
   constexpr int PF = PFN ? (QT * LPR + NT - 1) / NT : 1;
   float pfv[PF];
   if constexpr (PFN) {
-    const int64_t j = (int64_t)blockIdx.x + (int64_t)gridDim.x * blockIdx.y + pf_stride;
-    const bool pf_on = heavy_first && pf_stride > 0 && j < (int64_t)gridDim.x * gridDim.y;
+    const int64_t self = (int64_t)blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
+    const int64_t j = self + pf_stride;
+    const bool pf_on =
+        heavy_first && pf_stride > 0 && self >= pf_first && j < (int64_t)gridDim.x * gridDim.y;
     const int jx = pf_on ? (int)(j % gridDim.x) : 0, jy = pf_on ? (int)(j / gridDim.x) : 0;
     const int jqt = (int)gridDim.y - 1 - jy, jkh = jx % num_kv_heads, jb = jx / num_kv_heads;
     const int js0 = pf_on ? q_start[jb] : 0;
@@ -309,13 +311,18 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) __attribute__((amdgpu_waves_per
     const int jq0 = jqt * QT;
     const int jrows = jnr - jq0 < QT ? jnr - jq0 : QT;  // <= 0: nothing to touch
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const int u = tid + i * NT, row = u / LPR, line = u % LPR;
-      const bool on = pf_on && u < QT * LPR && row < jrows;
-      // off: this wave's own first q line (already loaded) is read again
-      const int64_t off = on ? ((int64_t)(js0 + jq0 + row) * num_q_heads + jkh * G) * D + 16 * line
-                             : ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h0) * D;
-      pfv[i] = q[off];
+    for (int i = 0; i < PF; ++i) pfv[i] = 0.0f;
+    if (pf_on && jrows > 0) {  // workgroup-uniform
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int u = tid + i * NT, row = u / LPR, line = u % LPR;
+        const bool on = u < QT * LPR && row < jrows;
+        // off: this wave's own first q line (already loaded) is read again
+        const int64_t off =
+            on ? ((int64_t)(js0 + jq0 + row) * num_q_heads + jkh * G) * D + 16 * line
+               : ((int64_t)(s0 + (row_ok ? qi : q0)) * num_q_heads + h0) * D;
+        pfv[i] = q[off];
+      }
     }
   }
 
@@ -625,7 +632,7 @@ __global__ __launch_bounds__(64 * (G / HW) * QS) __attribute__((amdgpu_waves_per
 }
 
 using PrefillFn = void (*)(float*, const float*, const void*, const void*, const int32_t*, int,
-                           const int32_t*, const int32_t*, int, int64_t, int, float, int, int);
+                           const int32_t*, const int32_t*, int, int64_t, int, float, int, int, int);
 
 // Waves per workgroup, query heads per wave (for groups of at least 4 heads)
 // and key blocks per staged iteration.  With 8 waves a workgroup may hold up
@@ -780,11 +787,24 @@ extern "C" int rkv_prefill_attention(float* out, const float* q, const void* k_p
   const int heavy = RKV_PREFILL_HEAVY_FIRST && n_tiles <= 65535 && n_heads <= 0x7fffffff;
   const dim3 grid = heavy ? dim3((unsigned)n_heads, (unsigned)n_tiles, 1)
                           : dim3((unsigned)n_tiles, (unsigned)num_kv_heads, (unsigned)num_seqs);
-  // the workgroup that takes this one's slot in the next round is
-  // `resident` places later in dispatch order
-  const int pf_stride = cfg.next && heavy ? resident_workgroups(cfg.fn, 64 * cfg.waves) : 0;
+  // Of R resident workgroups and T in all, the later ones (from R on) start
+  // as slots free up.  The touches go to the last min(R, T - R) workgroups
+  // of the first round (its lightest: the grid runs heaviest first), each
+  // for the workgroup that many places later; the heaviest, which end the
+  // first round, touch nothing.  configs[4] admissions (us per call, one
+  // box, interleaved): 26.7 against 28.6 when the first T - R workgroups
+  // touch and 27.4 when the first R - (T - R) touch workgroups of the first
+  // round (8 x 512 square: the same workgroups either way, 52.6).
+  int pf_stride = 0, pf_first = 0;
+  if (cfg.next && heavy) {
+    const int64_t R = resident_workgroups(cfg.fn, 64 * cfg.waves), T = n_heads * n_tiles;
+    if (R > 0 && T > R) {
+      pf_stride = (int)(T - R < R ? T - R : R);
+      pf_first = (int)(R - pf_stride);
+    }
+  }
   hipLaunchKernelGGL(cfg.fn, grid, dim3(64 * cfg.waves), 0, static_cast<hipStream_t>(stream), out, q, k_pool,
                      v_pool, block_tables, max_blocks_per_seq, q_start, ctx_lens, num_kv_heads,
-                     num_blocks, max_q_len, scale * kLog2e, heavy, pf_stride);
+                     num_blocks, max_q_len, scale * kLog2e, heavy, pf_stride, pf_first);
   return check_launch("rkv_prefill_attention");
 }
