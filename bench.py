@@ -209,8 +209,17 @@ def traffic_from_profiles():
 
 # ---- the other benchmark configs (one JSON line each; not the headline) -----------
 
-def _timed(torch, fn, reps):
-    """Average ms of fn() over reps calls, HIP events on the current stream."""
+def _timed(torch, fn, reps, settle_s=0.05):
+    """Average ms of fn() over reps calls, HIP events on the current stream,
+    after untimed rounds of reps calls for at least settle_s seconds (the
+    clock takes ~15 ms of sustained load to settle)."""
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= settle_s:
+            break
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
