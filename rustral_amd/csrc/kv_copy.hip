@@ -159,7 +159,10 @@ __global__ __launch_bounds__(256) void append_kernel(
 // Threads per workgroup (= units per piece): 16-bit pools, and fp32 pools.
 // configs[1] (us per call; bf16 -> bf16, bf16 -> fp32, fp32 -> fp32) at
 // HPW 2: 256 threads 194 / 300 / 405, 128 threads 193 / 301 / 395, 64
-// threads 194 / 313 / 396.  The workgroups of one block's head groups are
+// threads 194 / 313 / 396; HPW 1 (one tile per workgroup): 128 threads
+// 214 / 426 / 489, 64 threads (1 KiB per workgroup, the shape copy_blocks
+// streams fastest in) 238 / 487 / 531 -- each workgroup waits on its table
+// and length reads before its first load, which small workgroups repeat.  The workgroups of one block's head groups are
 // consecutive in the grid; one head group's blocks consecutive instead (so
 // that consecutive workgroups write consecutive rows) ran 197 / 313 / 416
 // against 194 / 300 / 396 (HPW 1: 241 / 478 / 491, HPW 4: 203 / 335 / 440).
