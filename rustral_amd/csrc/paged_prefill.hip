@@ -651,16 +651,22 @@ using PrefillFn = void (*)(float*, const float*, const void*, const void*, const
 #ifndef RKV_PREFILL_HEAVY_FIRST
 #define RKV_PREFILL_HEAVY_FIRST 1
 #endif
-// The build for calls whose sequences hold at most as many cached keys as
-// new tokens (bf16 pools, 4 query heads per KV head, D = 128): workgroups of
-// RKV_PREFILL_SHORT_WAVES waves (32-row tiles, two workgroups per CU at 235
-// VGPRs and 68 KB of LDS) that touch the q rows of the next round's
-// workgroups (RKV_PREFILL_PREFETCH).  Longer cached prefixes keep the 8-wave
-// 64-row tiles, which stage each K/V tile for twice the rows.  us per call
-// (one box, events): 25 x 128 new tokens 28.7 against 30.3; 8 x 512 square
-// 51.5 / 52.6; 4 x 2048 square 238 / 253; 8 x 512 after 512 cached 104 /
-// 104; 25 x 128 after 384 cached 65.7 / 66.2; after 896 cached 117 / 114;
-// 8 x 512 after 1536 cached 210 / 204; after 3584 cached 430 / 413.
+// The build for bf16 pools with 4 or 8 query heads per KV head on calls
+// whose sequences hold at most as many cached keys as new tokens (at D = 64
+// on every call): workgroups of RKV_PREFILL_SHORT_WAVES waves (32-row tiles
+// at G = 4, 16-row at G = 8; two workgroups per CU at D = 128 with 235
+// VGPRs and 68 KB of LDS, three at D = 64) that touch the q rows of the
+// next round's workgroups (RKV_PREFILL_PREFETCH).  Elsewhere the 8-wave
+// tiles stay ahead: they stage each K/V tile for twice the rows.  us per
+// call (one box, interleaved; 8-wave -> this build), G = 4, D = 128: 25 x
+// 128 new tokens 29.8 -> 26.0, 8 x 512 square 52.6 -> 51.5, 4 x 2048
+// square 253 -> 241, 8 x 512 after 512 cached 104 / 104, 25 x 128 after 896
+// cached 114 / 117, 8 x 512 after 3584 cached 413 / 430; G = 8, D = 128:
+// 64.3 -> 61.4, 109.3 -> 100.1, after 512 cached 215 / 215, after 3584
+// cached 827 / 849; G = 4, D = 64: 19.5 -> 16.6, 34.8 -> 30.2, after 512
+// cached 69.9 -> 62.5, after 3584 cached 270 -> 265; G = 8, D = 64: 35.1 ->
+// 26.4, 67.9 -> 52.7, after 3584 cached 535 -> 486; G = 4, D = 32: 10.9 /
+// 11.0, 22.0 -> 20.4, after 3584 cached 166 / 173.
 #ifndef RKV_PREFILL_SHORT_WAVES
 #define RKV_PREFILL_SHORT_WAVES 4
 #endif
@@ -720,10 +726,13 @@ PrefillCfg pick_g(int G, bool short_prefix) {
     case 1: return cfg_g<T, D, 1, kWaves, false>();
     case 2: return cfg_g<T, D, 2, kWaves, false>();
     case 4:
-      if constexpr (std::is_same<T, uint16_t>::value && D == 128)
-        if (short_prefix) return cfg_g<T, D, 4, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
+      if constexpr (std::is_same<T, uint16_t>::value)
+        if (short_prefix || D == 64) return cfg_g<T, D, 4, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
       return cfg_g<T, D, 4, kWaves, false>();
-    case 8: return cfg_g<T, D, 8, kWaves, false>();
+    case 8:
+      if constexpr (std::is_same<T, uint16_t>::value)
+        if (short_prefix || D == 64) return cfg_g<T, D, 8, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
+      return cfg_g<T, D, 8, kWaves, false>();
     default: return {nullptr, 0, 0, false};
   }
 }

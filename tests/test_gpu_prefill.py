@@ -85,33 +85,41 @@ def short_prefix_case(seed, n_seq, n_max, with_edges):
     return n_new, ctx
 
 
-@pytest.mark.parametrize("seed,n_seq,n_max,with_edges",
-                         [(60, 40, 128, False), (61, 33, 96, True), (62, 7, 256, True)])
-def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges):
+@pytest.mark.parametrize("seed,n_seq,n_max,with_edges,hq,hkv,d",
+                         [(60, 40, 128, False, 32, 8, 128), (61, 33, 96, True, 32, 8, 128),
+                          (62, 7, 256, True, 32, 8, 128), (63, 20, 128, True, 64, 8, 128),
+                          (64, 30, 128, True, 32, 8, 64), (65, 12, 160, True, 64, 8, 64),
+                          (66, 40, 128, True, 32, 8, 32)])
+def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv, d):
     """Calls whose tables hold at most twice the longest new-token run take
-    the 4-wave build that touches the next round's q rows (bf16, Hq 32, Hkv 8,
-    D 128); grids of 448 to 1,280 workgroups (one round of 512 resident
-    workgroups to two and a half), so the touched rows include tiles past a
-    sequence's end.  Against the oracle, and bit-equal to the
-    8-wave build, which a wider table (extra -1 entries) selects."""
+    the 4-wave build that touches the next round's q rows (bf16 pools, 4 or 8
+    query heads per KV head; at head_dim 64 every call takes it).  Grids of
+    448 to 1,280 workgroups (up to 2.5 rounds of the resident ones), so the
+    touched rows include tiles past a sequence's end.  Against the oracle;
+    at head_dim 128 and 32 also bit-equal to the 8-wave build, which a wider
+    table (extra -1 entries) selects there."""
     n_new, ctx = short_prefix_case(seed, n_seq, n_max, with_edges)
-    say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max}")
-    q, kp, vp, _, _, tables, qs = case(seed, 32, 8, 128, n_new, ctx, "bf16")
+    say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max} hq={hq} d={d}")
+    q, kp, vp, _, _, tables, qs = case(seed, hq, hkv, d, n_new, ctx, "bf16")
     assert tables.shape[1] * 16 <= 2 * int(n_new.max())
-    got = run_gpu(dev, q, kp, vp, tables, qs, ctx, 0.088)
-    want = oracle.prefill_attention(q, kp, vp, tables, qs, ctx, 0.088)
+    scale = float(np.float32(1.0 / math.sqrt(d)))
+    got = run_gpu(dev, q, kp, vp, tables, qs, ctx, scale)
+    want = oracle.prefill_attention(q, kp, vp, tables, qs, ctx, scale)
     assert_allclose_ref(got, want, RTOL, ATOL, "gpu vs oracle")
     if with_edges:
         assert np.all(got[qs[2]:qs[2] + 30] == 0.0)
     wide = np.full((tables.shape[0], 2 * tables.shape[1] + 1), -1, np.int32)
     wide[:, :tables.shape[1]] = tables
-    long_build = run_gpu(dev, q, kp, vp, wide, qs, ctx, 0.088)
-    assert np.array_equal(got, long_build)
+    other = run_gpu(dev, q, kp, vp, wide, qs, ctx, scale)
+    if d != 64:
+        assert np.array_equal(got, other)
+    else:
+        assert_allclose_ref(other, want, RTOL, ATOL, "gpu (wide table) vs oracle")
     # the rows past a max_q_len cap stay unwritten in the short build too
     # (the cap still at least half the table's keys)
     cap = (tables.shape[1] * 16 + 1) // 2
     assert cap < n_max
-    capped = run_gpu(dev, q, kp, vp, tables, qs, ctx, 0.088, max_q_len=cap)
+    capped = run_gpu(dev, q, kp, vp, tables, qs, ctx, scale, max_q_len=cap)
     rows = np.concatenate([np.arange(qs[b], qs[b] + min(cap, n_new[b])) for b in range(n_seq)])
     assert np.array_equal(capped[rows], got[rows])
     assert np.all(capped[np.setdiff1d(np.arange(qs[-1]), rows)] == 0.0)
