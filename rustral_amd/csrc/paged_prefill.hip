@@ -651,22 +651,25 @@ using PrefillFn = void (*)(float*, const float*, const void*, const void*, const
 #ifndef RKV_PREFILL_HEAVY_FIRST
 #define RKV_PREFILL_HEAVY_FIRST 1
 #endif
-// The build for bf16 pools with 4 or 8 query heads per KV head on calls
-// whose sequences hold at most as many cached keys as new tokens (at D = 64
-// on every call): workgroups of RKV_PREFILL_SHORT_WAVES waves (32-row tiles
-// at G = 4, 16-row at G = 8; two workgroups per CU at D = 128 with 235
-// VGPRs and 68 KB of LDS, three at D = 64) that touch the q rows of the
-// next round's workgroups (RKV_PREFILL_PREFETCH).  Elsewhere the 8-wave
-// tiles stay ahead: they stage each K/V tile for twice the rows.  us per
-// call (one box, interleaved; 8-wave -> this build), G = 4, D = 128: 25 x
-// 128 new tokens 29.8 -> 26.0, 8 x 512 square 52.6 -> 51.5, 4 x 2048
-// square 253 -> 241, 8 x 512 after 512 cached 104 / 104, 25 x 128 after 896
-// cached 114 / 117, 8 x 512 after 3584 cached 413 / 430; G = 8, D = 128:
-// 64.3 -> 61.4, 109.3 -> 100.1, after 512 cached 215 / 215, after 3584
-// cached 827 / 849; G = 4, D = 64: 19.5 -> 16.6, 34.8 -> 30.2, after 512
-// cached 69.9 -> 62.5, after 3584 cached 270 -> 265; G = 8, D = 64: 35.1 ->
-// 26.4, 67.9 -> 52.7, after 3584 cached 535 -> 486; G = 4, D = 32: 10.9 /
-// 11.0, 22.0 -> 20.4, after 3584 cached 166 / 173.
+// A build of RKV_PREFILL_SHORT_WAVES waves per workgroup that touches the
+// q rows of the next round's workgroups (RKV_PREFILL_PREFETCH), for bf16
+// pools on the calls short_build_use (below) gives it: G = 4 -> 32-row
+// tiles, G = 8 -> 16-row, G = 2 -> 32-row, G = 1 -> 64-row; at D = 128 and
+// G >= 4 two workgroups per CU (235 VGPRs, 68 KB of LDS), at D = 64 three.
+// Where it loses, the 8-wave tiles, which stage each K/V tile for twice the
+// rows, stay.  us per call (one box, interleaved; 8-wave -> 4-wave) for 25 x
+// 128 new tokens / 8 x 512 square / 8 x 512 after 512 cached / after 3584
+// cached: G = 4, D = 128: 29.8 -> 26.0 / 52.6 -> 51.5 / 104 = 104 / 413 ->
+// 430; G = 8, D = 128: 64.3 -> 61.4 / 109 -> 100 / 215 = 215 / 827 -> 849;
+// G = 2, D = 128: 17.4 -> 19.7 / 31.5 -> 33.3 / 57.8 -> 66.0 / 224 -> 261;
+// G = 1, D = 128: 13.2 -> 11.6 / 25.8 -> 21.9 / 42.6 -> 38.6 / 144 = 143;
+// D = 64, G = 8, 4, 2, 1: 35.1 -> 26.4, 19.5 -> 16.6, 10.9 = 10.8, 8.1 ->
+// 7.2 / 67.9 -> 52.7, 34.8 -> 30.2, 22.2 -> 19.3, 18.4 -> 14.4 / -, 69.9 ->
+// 62.5, 38.7 -> 35.3, 30.9 -> 25.4 / 535 -> 486, 270 -> 265, 144 = 145,
+// 103 -> 93; D = 32, G = 8, 4, 2, 1: 16.5 = 16.3, 10.9 = 11.0, 7.5 = 7.6,
+// 6.0 -> 5.8 / 34.9 = 34.6, 22.0 -> 20.4, 15.4 -> 14.9, 13.4 -> 12.6 /
+// 75.7 = 75.5, -, 28.4 -> 27.1, 23.3 -> 22.1 / 307 -> 314, 166 -> 173, 104
+// -> 107, 85.5 -> 83.3.
 #ifndef RKV_PREFILL_SHORT_WAVES
 #define RKV_PREFILL_SHORT_WAVES 4
 #endif
@@ -720,19 +723,29 @@ PrefillCfg cfg_g() {
   return {&prefill_kernel<T, D, G, HW, QS, kKB, PFN>, (G / HW) * QS, 16 * QS, PFN};
 }
 
+// When bf16 pools take the 4-wave build: 2 on every call, 1 when the
+// sequences hold at most as many cached keys as new tokens, 0 never (fp32
+// pools always keep the 8-wave build: at D = 128 its 4-wave form spills
+// into AGPRs at one wave per SIMD).
+constexpr int short_build_use(int G, int D) {
+  return D == 64 ? 2 : G == 1 ? 2 : (D == 128 && G == 2) ? 0 : 1;
+}
+
+template <typename T, int D, int G>
+PrefillCfg cfg_pick(bool short_prefix) {
+  constexpr int use = std::is_same<T, uint16_t>::value ? short_build_use(G, D) : 0;
+  if constexpr (use > 0)
+    if (use == 2 || short_prefix) return cfg_g<T, D, G, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
+  return cfg_g<T, D, G, kWaves, false>();
+}
+
 template <typename T, int D>
 PrefillCfg pick_g(int G, bool short_prefix) {
   switch (G) {
-    case 1: return cfg_g<T, D, 1, kWaves, false>();
-    case 2: return cfg_g<T, D, 2, kWaves, false>();
-    case 4:
-      if constexpr (std::is_same<T, uint16_t>::value)
-        if (short_prefix || D == 64) return cfg_g<T, D, 4, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
-      return cfg_g<T, D, 4, kWaves, false>();
-    case 8:
-      if constexpr (std::is_same<T, uint16_t>::value)
-        if (short_prefix || D == 64) return cfg_g<T, D, 8, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
-      return cfg_g<T, D, 8, kWaves, false>();
+    case 1: return cfg_pick<T, D, 1>(short_prefix);
+    case 2: return cfg_pick<T, D, 2>(short_prefix);
+    case 4: return cfg_pick<T, D, 4>(short_prefix);
+    case 8: return cfg_pick<T, D, 8>(short_prefix);
     default: return {nullptr, 0, 0, false};
   }
 }

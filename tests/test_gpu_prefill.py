@@ -85,19 +85,27 @@ def short_prefix_case(seed, n_seq, n_max, with_edges):
     return n_new, ctx
 
 
-@pytest.mark.parametrize("seed,n_seq,n_max,with_edges,hq,hkv,d",
-                         [(60, 40, 128, False, 32, 8, 128), (61, 33, 96, True, 32, 8, 128),
-                          (62, 7, 256, True, 32, 8, 128), (63, 20, 128, True, 64, 8, 128),
-                          (64, 30, 128, True, 32, 8, 64), (65, 12, 160, True, 64, 8, 64),
-                          (66, 40, 128, True, 32, 8, 32)])
-def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv, d):
-    """Calls whose tables hold at most twice the longest new-token run take
-    the 4-wave build that touches the next round's q rows (bf16 pools, 4 or 8
-    query heads per KV head; at head_dim 64 every call takes it).  Grids of
-    448 to 1,280 workgroups (up to 2.5 rounds of the resident ones), so the
-    touched rows include tiles past a sequence's end.  Against the oracle;
-    at head_dim 128 and 32 also bit-equal to the 8-wave build, which a wider
-    table (extra -1 entries) selects there."""
+# (seed, sequences, longest new-token run, edge sequences, Hq, Hkv, D, whether a
+# wider table selects the 8-wave build: the 4-wave one is taken on every call
+# at D = 64 and at G = 1, on no call at G = 2 with D = 128)
+SHORT_CASES = [(60, 40, 128, False, 32, 8, 128, True), (61, 33, 96, True, 32, 8, 128, True),
+               (62, 7, 256, True, 32, 8, 128, True), (63, 20, 128, True, 64, 8, 128, True),
+               (64, 30, 128, True, 32, 8, 64, False), (65, 12, 160, True, 64, 8, 64, False),
+               (66, 40, 128, True, 32, 8, 32, True), (67, 40, 128, True, 8, 8, 128, False),
+               (68, 40, 128, True, 16, 8, 64, False), (69, 40, 128, True, 16, 8, 32, True),
+               (70, 25, 128, True, 16, 8, 128, False)]
+
+
+@pytest.mark.parametrize("seed,n_seq,n_max,with_edges,hq,hkv,d,two_builds", SHORT_CASES)
+def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv, d, two_builds):
+    """bf16 pools take the 4-wave build that touches the next round's q rows
+    on the calls it was measured faster for: every call at head_dim 64 and
+    at one query head per KV head, else calls whose tables hold at most
+    twice the longest new-token run (never at two heads per KV head with
+    head_dim 128).  Grids of several hundred to a few thousand workgroups,
+    over one to several rounds of the resident ones, so the touched rows
+    include tiles past a sequence's end.  Against the oracle; where a wider
+    table (extra -1 entries) selects the 8-wave build, bit-equal to it."""
     n_new, ctx = short_prefix_case(seed, n_seq, n_max, with_edges)
     say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max} hq={hq} d={d}")
     q, kp, vp, _, _, tables, qs = case(seed, hq, hkv, d, n_new, ctx, "bf16")
@@ -111,7 +119,7 @@ def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv
     wide = np.full((tables.shape[0], 2 * tables.shape[1] + 1), -1, np.int32)
     wide[:, :tables.shape[1]] = tables
     other = run_gpu(dev, q, kp, vp, wide, qs, ctx, scale)
-    if d != 64:
+    if two_builds:
         assert np.array_equal(got, other)
     else:
         assert_allclose_ref(other, want, RTOL, ATOL, "gpu (wide table) vs oracle")
