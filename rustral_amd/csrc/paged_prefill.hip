@@ -723,17 +723,22 @@ PrefillCfg cfg_g() {
   return {&prefill_kernel<T, D, G, HW, QS, kKB, PFN>, (G / HW) * QS, 16 * QS, PFN};
 }
 
-// When bf16 pools take the 4-wave build: 2 on every call, 1 when the
-// sequences hold at most as many cached keys as new tokens, 0 never (fp32
-// pools always keep the 8-wave build: at D = 128 its 4-wave form spills
-// into AGPRs at one wave per SIMD).
-constexpr int short_build_use(int G, int D) {
+// When the 4-wave build is taken: 2 on every call, 1 when the sequences
+// hold at most as many cached keys as new tokens, 0 never.  fp32 pools (us
+// per call, same four shapes as above; 8-wave -> 4-wave): G = 1, D = 32
+// 6.2 -> 5.8 / 14.5 -> 13.2 / 25.2 -> 23.2 / 95 -> 83; G = 1, D = 128 15.4
+// -> 14.8 / 32.4 -> 30.7 / 57.2 = 58.4 / 219 -> 242; elsewhere slower or
+// even (G = 4, D = 32: 11.6 = 11.6 / 25.0 -> 23.3 / 50.9 -> 52.2 / 209 ->
+// 226; at D = 64 slower on all four; at D = 128 and G >= 4 the 4-wave form
+// spills into AGPRs at one wave per SIMD).
+constexpr int short_build_use(bool f32, int G, int D) {
+  if (f32) return G == 1 && D == 32 ? 2 : G == 1 && D == 128 ? 1 : 0;
   return D == 64 ? 2 : G == 1 ? 2 : (D == 128 && G == 2) ? 0 : 1;
 }
 
 template <typename T, int D, int G>
 PrefillCfg cfg_pick(bool short_prefix) {
-  constexpr int use = std::is_same<T, uint16_t>::value ? short_build_use(G, D) : 0;
+  constexpr int use = short_build_use(sizeof(T) == 4, G, D);
   if constexpr (use > 0)
     if (use == 2 || short_prefix) return cfg_g<T, D, G, kShortWaves, RKV_PREFILL_PREFETCH != 0>();
   return cfg_g<T, D, G, kWaves, false>();

@@ -85,30 +85,40 @@ def short_prefix_case(seed, n_seq, n_max, with_edges):
     return n_new, ctx
 
 
-# (seed, sequences, longest new-token run, edge sequences, Hq, Hkv, D, whether a
-# wider table selects the 8-wave build: the 4-wave one is taken on every call
-# at D = 64 and at G = 1, on no call at G = 2 with D = 128)
-SHORT_CASES = [(60, 40, 128, False, 32, 8, 128, True), (61, 33, 96, True, 32, 8, 128, True),
-               (62, 7, 256, True, 32, 8, 128, True), (63, 20, 128, True, 64, 8, 128, True),
-               (64, 30, 128, True, 32, 8, 64, False), (65, 12, 160, True, 64, 8, 64, False),
-               (66, 40, 128, True, 32, 8, 32, True), (67, 40, 128, True, 8, 8, 128, False),
-               (68, 40, 128, True, 16, 8, 64, False), (69, 40, 128, True, 16, 8, 32, True),
-               (70, 25, 128, True, 16, 8, 128, False)]
+# (seed, sequences, longest new-token run, edge sequences, Hq, Hkv, D, pool
+# dtype, whether a wider table selects the 8-wave build).  bf16 pools: the
+# 4-wave build on every call at D = 64 and at G = 1, on no call at G = 2 with
+# D = 128, else for short cached prefixes; fp32 pools: every call at G = 1
+# with D = 32, short cached prefixes at G = 1 with D = 128, else never.
+SHORT_CASES = [(60, 40, 128, False, 32, 8, 128, "bf16", True),
+               (61, 33, 96, True, 32, 8, 128, "bf16", True),
+               (62, 7, 256, True, 32, 8, 128, "bf16", True),
+               (63, 20, 128, True, 64, 8, 128, "bf16", True),
+               (64, 30, 128, True, 32, 8, 64, "bf16", False),
+               (65, 12, 160, True, 64, 8, 64, "bf16", False),
+               (66, 40, 128, True, 32, 8, 32, "bf16", True),
+               (67, 40, 128, True, 8, 8, 128, "bf16", False),
+               (68, 40, 128, True, 16, 8, 64, "bf16", False),
+               (69, 40, 128, True, 16, 8, 32, "bf16", True),
+               (70, 25, 128, True, 16, 8, 128, "bf16", False),
+               (71, 40, 128, True, 8, 8, 32, "f32", False),
+               (72, 30, 128, True, 8, 8, 128, "f32", True)]
 
 
-@pytest.mark.parametrize("seed,n_seq,n_max,with_edges,hq,hkv,d,two_builds", SHORT_CASES)
-def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv, d, two_builds):
-    """bf16 pools take the 4-wave build that touches the next round's q rows
-    on the calls it was measured faster for: every call at head_dim 64 and
-    at one query head per KV head, else calls whose tables hold at most
-    twice the longest new-token run (never at two heads per KV head with
-    head_dim 128).  Grids of several hundred to a few thousand workgroups,
-    over one to several rounds of the resident ones, so the touched rows
-    include tiles past a sequence's end.  Against the oracle; where a wider
-    table (extra -1 entries) selects the 8-wave build, bit-equal to it."""
+@pytest.mark.parametrize("seed,n_seq,n_max,with_edges,hq,hkv,d,dtype,two_builds", SHORT_CASES)
+def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv, d, dtype,
+                                    two_builds):
+    """The 4-wave build that touches the next round's q rows is taken on the
+    calls it was measured faster for (per pool dtype, query heads per KV
+    head and head_dim; for short cached prefixes the table width against the
+    longest new-token run decides).  Grids of several hundred to a few
+    thousand workgroups, over one to several rounds of the resident ones, so
+    the touched rows include tiles past a sequence's end.  Against the
+    oracle; where a wider table (extra -1 entries) selects the 8-wave build,
+    bit-equal to it."""
     n_new, ctx = short_prefix_case(seed, n_seq, n_max, with_edges)
-    say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max} hq={hq} d={d}")
-    q, kp, vp, _, _, tables, qs = case(seed, hq, hkv, d, n_new, ctx, "bf16")
+    say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max} hq={hq} d={d} {dtype}")
+    q, kp, vp, _, _, tables, qs = case(seed, hq, hkv, d, n_new, ctx, dtype)
     assert tables.shape[1] * 16 <= 2 * int(n_new.max())
     scale = float(np.float32(1.0 / math.sqrt(d)))
     got = run_gpu(dev, q, kp, vp, tables, qs, ctx, scale)
