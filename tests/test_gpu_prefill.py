@@ -102,7 +102,9 @@ SHORT_CASES = [(60, 40, 128, False, 32, 8, 128, "bf16", True),
                (69, 40, 128, True, 16, 8, 32, "bf16", True),
                (70, 25, 128, True, 16, 8, 128, "bf16", False),
                (71, 40, 128, True, 8, 8, 32, "f32", False),
-               (72, 30, 128, True, 8, 8, 128, "f32", True)]
+               (72, 30, 128, True, 8, 8, 128, "f32", True),
+               (73, 30, 128, True, 8, 8, 64, "bf16", False),
+               (74, 30, 128, True, 8, 8, 64, "f32", False)]
 
 
 @pytest.mark.parametrize("seed,n_seq,n_max,with_edges,hq,hkv,d,dtype,two_builds", SHORT_CASES)
