@@ -119,7 +119,7 @@ def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv
     oracle; where a wider table (extra -1 entries) selects the 8-wave build,
     bit-equal to it."""
     n_new, ctx = short_prefix_case(seed, n_seq, n_max, with_edges)
-    say(f"prefill short-prefix build seed={seed} seqs={n_seq} n_max={n_max} hq={hq} d={d} {dtype}")
+    say(f"prefill 4-wave build seed={seed} seqs={n_seq} n_max={n_max} hq={hq} d={d} {dtype}")
     q, kp, vp, _, _, tables, qs = case(seed, hq, hkv, d, n_new, ctx, dtype)
     assert tables.shape[1] * 16 <= 2 * int(n_new.max())
     scale = float(np.float32(1.0 / math.sqrt(d)))
@@ -135,7 +135,7 @@ def test_prefill_short_prefix_build(dev, seed, n_seq, n_max, with_edges, hq, hkv
         assert np.array_equal(got, other)
     else:
         assert_allclose_ref(other, want, RTOL, ATOL, "gpu (wide table) vs oracle")
-    # the rows past a max_q_len cap stay unwritten in the short build too
+    # the rows past a max_q_len cap stay unwritten in the 4-wave build too
     # (the cap still at least half the table's keys)
     cap = (tables.shape[1] * 16 + 1) // 2
     assert cap < n_max
