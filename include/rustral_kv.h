@@ -109,7 +109,7 @@ int rkv_copy_blocks(void* k_pool, void* v_pool, int64_t layer_stride_bytes, int 
  * max_context: host-side upper bound on every ctx_lens[b] (for example
  * max_blocks_per_seq*block_size).  partition_size: the size the call will
  * use (rkv_decode_partition_size_for), or <= 0 for the smallest size any
- * call picks by itself (640), which is enough for every pool dtype and
+ * call picks by itself (512), which is enough for every pool dtype and
  * shape. */
 size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_context,
                                   int partition_size);
@@ -128,7 +128,8 @@ int rkv_decode_partition_size(int partition_size, int head_dim, int dtype, int m
  * rkv_decode_partition_size), else its own pick: for RKV_BF16 pools with
  * head_dim 128 and at most 4 query heads per KV head, 1280 when
  * num_kv_heads * num_seqs * max_context / 2 >= 1200 * 1280 tokens, else 768
- * when that is >= 1000 * 768, else 640; 640 for every other shape and
+ * when that is >= 1000 * 768, else 640 when that is >= 800 * 512, else
+ * 512; 640 for every other shape and
  * dtype.  The split entry points take this value as their partition_size to
  * match the one-call entry point. */
 int rkv_decode_partition_size_for(int partition_size, int num_seqs, int num_q_heads,

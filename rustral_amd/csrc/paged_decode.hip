@@ -1413,9 +1413,14 @@ int default_part(int dtype, int /*max_context*/) { return one_byte(dtype) ? kPQ 
 // the library: for bf16 pools with head_dim 128 and at most 4 query heads
 // per KV head, 1280 when the call holds work for at least 1,200 such
 // partitions over all KV heads (contexts taken as uniform up to cap), else
-// 768 when it holds work for 1,000 of those, else 640 (the measurements
-// above: configs[2] 768, configs[3] and 256 x U[1, 8192] 1280, small
-// batches 640).
+// 768 when it holds work for 1,000 of those, else 640 when it holds work for
+// 800 partitions of 512, else 512 (the measurements above: configs[2] 768,
+// configs[3] and 256 x U[1, 8192] 1280; and, us per call at 512 / 640 /
+// 768 over U[512, 4096] contexts, 32 layers back to back: 8 sequences x 8
+// KV heads 19.5 / 22.4 / 24.3, 64 x 1 (configs[2]'s share of one GPU of 8
+// by KV heads) 23.8 / 24.5 / 25.9, 16 x 8 33.4 / 38.9 / 35.9, 64 x 2 36.9 /
+// 41.4 / 40.7, 24 x 8 42.4 / 43.5 / 43.8, 32 x 8 56.4 / 56.5 / 55.7, 64 x 4
+// 60.8 / 58.9 / 64.6, 48 x 8 82.8 / 81.7 / 81.3).
 int shape_part(int dtype, int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                int cap) {
   if (dtype != RKV_BF16 || head_dim != 128 || num_kv_heads <= 0 || num_seqs <= 0 ||
@@ -1424,7 +1429,8 @@ int shape_part(int dtype, int num_seqs, int num_q_heads, int num_kv_heads, int h
   const double work = (double)num_kv_heads * num_seqs * (0.5 * cap);  // KV-head tokens
   if (work >= 1200.0 * kWideP2) return kWideP2;
   if (work >= 1000.0 * kWideP1) return kWideP1;
-  return kP;
+  if (work >= 800.0 * kSmallP) return kP;
+  return kSmallP;
 }
 
 // The partition size a call uses: the request when it is > 0 (a multiple of
@@ -1685,9 +1691,11 @@ using namespace rkv;
 extern "C" size_t rkv_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim,
                                              int max_context, int partition_size) {
   if (num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_context <= 0) return 0;
-  // a given partition size, else the smaller of the 16-bit and 1-byte
-  // defaults for this max_context: enough for every pool dtype
-  const int dflt = std::min(default_part(RKV_BF16, max_context), default_part(RKV_I8, max_context));
+  // a given partition size, else the smallest size a call picks by itself
+  // (the 512-token build's, for small bf16 calls): enough for every pool
+  // dtype and shape
+  const int dflt = std::min({kSmallP, default_part(RKV_BF16, max_context),
+                             default_part(RKV_I8, max_context)});
   const int P = partition_size > 0 ? partition_size : dflt;
   const int max_parts = (max_context + P - 1) / P;
   return ws_bytes(num_seqs, num_q_heads, head_dim, max_parts);

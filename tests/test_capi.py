@@ -70,9 +70,12 @@ def test_workspace_size():
     L = _lib.lib()
     P = L.rkv_decode_partition_size(0, 128, RKV_BF16, 4096)
     assert P == 640
-    assert L.rkv_decode_workspace_bytes(64, 32, 128, P, 0) == 0  # one partition
+    # the default workspace (partition size 0) is sized for the smallest size
+    # a call picks by itself, 512
+    assert L.rkv_decode_workspace_bytes(64, 32, 128, 512, 0) == 0  # one partition
+    assert L.rkv_decode_workspace_bytes(64, 32, 128, 640, 0) > 0
     ws = L.rkv_decode_workspace_bytes(64, 32, 128, 4096, 0)
-    rows = 64 * 32 * -(-4096 // P)
+    rows = 64 * 32 * -(-4096 // 512)
     assert ws >= rows * (128 + 2) * 4
     # each pool dtype has its default partition size at a max_context; the
     # default workspace (partition size 0) covers every one of them
@@ -88,14 +91,16 @@ def test_workspace_size():
             assert L.rkv_decode_partition_size(0, 128, dt, maxc) == 640
     # the one-call pick by shape: bf16, head_dim 128, <= 4 query heads per KV
     # head; 1280 with work for >= 1200 such partitions, 768 with work for >=
-    # 1000 of those, else 640 (configs[2]: 768; configs[3] and 256 x 8192:
-    # 1280; small batches, 8 heads per KV head, head_dim 64, fp32 and 1-byte
+    # 1000 of those, 640 with work for >= 800 partitions of 512, else 512
+    # (configs[2]: 768; configs[3] and 256 x 8192: 1280; configs[2]'s share
+    # of one GPU of 8: 512; 8 heads per KV head, head_dim 64, fp32 and 1-byte
     # pools: 640)
     F = L.rkv_decode_partition_size_for
     assert F(0, 64, 32, 8, 128, RKV_BF16, 4096) == 768
     assert F(0, 8, 32, 8, 128, RKV_BF16, 65536) == 1280
     assert F(0, 256, 32, 8, 128, RKV_BF16, 8192) == 1280
-    assert F(0, 8, 32, 8, 128, RKV_BF16, 4096) == 640
+    assert F(0, 8, 32, 8, 128, RKV_BF16, 4096) == 512     # 8 sequences (a DP share)
+    assert F(0, 64, 4, 1, 128, RKV_BF16, 4096) == 512     # one KV head (a TP share)
     assert F(0, 4, 32, 8, 128, RKV_BF16, 32768) == 640
     assert F(0, 64, 64, 8, 128, RKV_BF16, 4096) == 640    # G = 8
     assert F(0, 64, 32, 8, 64, RKV_BF16, 4096) == 640     # head_dim 64
@@ -112,6 +117,12 @@ def test_workspace_size():
     assert F(0, 1, 32, 8, 128, RKV_BF16, 383999) == 768
     assert F(0, 1, 32, 8, 128, RKV_BF16, 192000) == 768   # 8 * 96000 = 768k
     assert F(0, 1, 32, 8, 128, RKV_BF16, 191999) == 640
+    assert F(0, 1, 32, 8, 128, RKV_BF16, 102400) == 640   # 8 * 51200 = 800 x 512
+    assert F(0, 1, 32, 8, 128, RKV_BF16, 102399) == 512
+    # the default workspace covers the smallest pick
+    for maxc in (4096, 65536):
+        assert (L.rkv_decode_workspace_bytes(8, 32, 128, maxc, 0)
+                >= L.rkv_decode_workspace_bytes(8, 32, 128, maxc, 512))
     # bf16 pools also take multiples of 128 up to 1280; the others do not
     for req in (768, 896, 1024, 1280):
         assert L.rkv_decode_partition_size(req, 128, RKV_BF16, 4096) == req
