@@ -1421,16 +1421,24 @@ int default_part(int dtype, int /*max_context*/) { return one_byte(dtype) ? kPQ 
 // by KV heads) 23.8 / 24.5 / 25.9, 16 x 8 33.4 / 38.9 / 35.9, 64 x 2 36.9 /
 // 41.4 / 40.7, 24 x 8 42.4 / 43.5 / 43.8, 32 x 8 56.4 / 56.5 / 55.7, 64 x 4
 // 60.8 / 58.9 / 64.6, 48 x 8 82.8 / 81.7 / 81.3).
+// The 512-token tier holds for 16-bit and fp32 pools of every shape (the
+// 512-token build exists for all of them; 1-byte pools have one build):
+// 512 / 640 us at 8 and 16 sequences x 8 KV heads, G = 8: 21.9 / 23.7,
+// 32.0 / 37.1; head_dim 64: 13.5 / 15.1, 20.6 / 23.6; fp32 pools: 31.8 /
+// 37.3, 58.9 / 69.0; at 32 and 64 sequences even or 640 ahead (G = 8 at 64:
+// 121.6 / 116.3).
 int shape_part(int dtype, int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                int cap) {
-  if (dtype != RKV_BF16 || head_dim != 128 || num_kv_heads <= 0 || num_seqs <= 0 ||
-      num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > 4 || cap <= 0)
+  if (one_byte(dtype) || num_kv_heads <= 0 || num_seqs <= 0 || cap <= 0)
     return default_part(dtype, cap);
   const double work = (double)num_kv_heads * num_seqs * (0.5 * cap);  // KV-head tokens
+  if (work < 800.0 * kSmallP) return kSmallP;
+  if (dtype != RKV_BF16 || head_dim != 128 || num_q_heads % num_kv_heads != 0 ||
+      num_q_heads / num_kv_heads > 4)
+    return default_part(dtype, cap);
   if (work >= 1200.0 * kWideP2) return kWideP2;
   if (work >= 1000.0 * kWideP1) return kWideP1;
-  if (work >= 800.0 * kSmallP) return kP;
-  return kSmallP;
+  return kP;
 }
 
 // The partition size a call uses: the request when it is > 0 (a multiple of

@@ -93,14 +93,19 @@ def test_workspace_size():
     # head; 1280 with work for >= 1200 such partitions, 768 with work for >=
     # 1000 of those, 640 with work for >= 800 partitions of 512, else 512
     # (configs[2]: 768; configs[3] and 256 x 8192: 1280; configs[2]'s share
-    # of one GPU of 8: 512; 8 heads per KV head, head_dim 64, fp32 and 1-byte
-    # pools: 640)
+    # of one GPU of 8: 512; above the 512 tier, 8 heads per KV head, head_dim
+    # 64 and fp32 pools: 640; 1-byte pools: 640 always)
     F = L.rkv_decode_partition_size_for
     assert F(0, 64, 32, 8, 128, RKV_BF16, 4096) == 768
     assert F(0, 8, 32, 8, 128, RKV_BF16, 65536) == 1280
     assert F(0, 256, 32, 8, 128, RKV_BF16, 8192) == 1280
     assert F(0, 8, 32, 8, 128, RKV_BF16, 4096) == 512     # 8 sequences (a DP share)
     assert F(0, 64, 4, 1, 128, RKV_BF16, 4096) == 512     # one KV head (a TP share)
+    assert F(0, 8, 64, 8, 128, RKV_BF16, 4096) == 512     # small calls: every shape
+    assert F(0, 8, 32, 8, 64, RKV_BF16, 4096) == 512
+    assert F(0, 8, 32, 8, 128, RKV_F32, 4096) == 512
+    for dt in (RKV_I8, RKV_FP8):                          # 1-byte pools: one build
+        assert F(0, 8, 32, 8, 128, dt, 4096) == 640
     assert F(0, 4, 32, 8, 128, RKV_BF16, 32768) == 640
     assert F(0, 64, 64, 8, 128, RKV_BF16, 4096) == 640    # G = 8
     assert F(0, 64, 32, 8, 64, RKV_BF16, 4096) == 640     # head_dim 64
