@@ -127,10 +127,10 @@ int rkv_decode_partition_size(int partition_size, int head_dim, int dtype, int m
  * shape: the request when partition_size > 0 (rules of
  * rkv_decode_partition_size), else its own pick.  With W = num_kv_heads *
  * num_seqs * max_context / 2 tokens: RKV_F32 and RKV_BF16 pools take 512
- * when W < 800 * 512; above that, RKV_BF16 pools with head_dim 128 and at
- * most 4 query heads per KV head take 1280 when W >= 1200 * 1280, else 768
- * when W >= 1000 * 768, else 640; every other shape, and 1-byte pools
- * always, 640.  The split entry points take this value as their
+ * when W < 800 * 512, 1-byte pools when W < 1600 * 512; above that, RKV_BF16
+ * pools with head_dim 128 and at most 4 query heads per KV head take 1280
+ * when W >= 1200 * 1280, else 768 when W >= 1000 * 768, else 640; every
+ * other shape and dtype 640.  The split entry points take this value as their
  * partition_size to match the one-call entry point. */
 int rkv_decode_partition_size_for(int partition_size, int num_seqs, int num_q_heads,
                                   int num_kv_heads, int head_dim, int dtype, int max_context);

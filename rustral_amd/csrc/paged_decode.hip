@@ -1399,6 +1399,8 @@ constexpr int split_of() { return sizeof(T) == 1 ? RKV_DECODE_SPLIT_Q : RKV_DECO
 // rkv_decode_attention picks by the call's shape (shape_part).
 constexpr int kSmallP = 512;
 static_assert(kSmallP <= kP && kSmallP % (16 * RKV_DECODE_SPLIT) == 0, "small partition build");
+static_assert(kSmallP <= kPQ && kSmallP % (16 * RKV_DECODE_SPLIT_Q) == 0,
+              "small partition build of the 1-byte pools");
 constexpr int kWideSplit = 8;
 constexpr int kWideP1 = 768, kWideP2 = 1280;
 static_assert(kWideP1 % (16 * kWideSplit) == 0 && kWideP2 % (16 * kWideSplit) == 0 &&
@@ -1421,18 +1423,20 @@ int default_part(int dtype, int /*max_context*/) { return one_byte(dtype) ? kPQ 
 // by KV heads) 23.8 / 24.5 / 25.9, 16 x 8 33.4 / 38.9 / 35.9, 64 x 2 36.9 /
 // 41.4 / 40.7, 24 x 8 42.4 / 43.5 / 43.8, 32 x 8 56.4 / 56.5 / 55.7, 64 x 4
 // 60.8 / 58.9 / 64.6, 48 x 8 82.8 / 81.7 / 81.3).
-// The 512-token tier holds for 16-bit and fp32 pools of every shape (the
-// 512-token build exists for all of them; 1-byte pools have one build):
-// 512 / 640 us at 8 and 16 sequences x 8 KV heads, G = 8: 21.9 / 23.7,
-// 32.0 / 37.1; head_dim 64: 13.5 / 15.1, 20.6 / 23.6; fp32 pools: 31.8 /
-// 37.3, 58.9 / 69.0; at 32 and 64 sequences even or 640 ahead (G = 8 at 64:
-// 121.6 / 116.3).
+// The 512-token tier holds for fp32 pools and every head shape: 512 / 640
+// us at 8 and 16 sequences x 8 KV heads, G = 8: 21.9 / 23.7, 32.0 / 37.1;
+// head_dim 64: 13.5 / 15.1, 20.6 / 23.6; fp32 pools: 31.8 / 37.3, 58.9 /
+// 69.0; at 32 and 64 sequences even or 640 ahead (G = 8 at 64: 121.6 /
+// 116.3).  1-byte pools take it up to twice the work (int8, contexts U[512,
+// 4096], 512 / 640: 8 sequences 13.4 / 15.2, 16 sequences 21.0 / 24.2, 32
+// sequences 33.0 / 33.8, 64 sequences 66.5 / 64.2; 64 x 1 KV head 16.0 /
+// 16.4).
 int shape_part(int dtype, int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                int cap) {
-  if (one_byte(dtype) || num_kv_heads <= 0 || num_seqs <= 0 || cap <= 0)
-    return default_part(dtype, cap);
+  if (num_kv_heads <= 0 || num_seqs <= 0 || cap <= 0) return default_part(dtype, cap);
   const double work = (double)num_kv_heads * num_seqs * (0.5 * cap);  // KV-head tokens
-  if (work < 800.0 * kSmallP) return kSmallP;
+  if (work < (one_byte(dtype) ? 1600.0 : 800.0) * kSmallP) return kSmallP;
+  if (one_byte(dtype)) return default_part(dtype, cap);
   if (dtype != RKV_BF16 || head_dim != 128 || num_q_heads % num_kv_heads != 0 ||
       num_q_heads / num_kv_heads > 4)
     return default_part(dtype, cap);
@@ -1493,7 +1497,7 @@ Launch make_launch(bool append) {
 
 // The build for partitions of P tokens: above the largest 4-wave build (bf16
 // pools), the smallest 8-wave build that holds them; else the 512-token
-// build when it holds them (16-bit and fp32 pools), else the largest.
+// build when it holds them, else the largest.
 template <typename T, int D, int G, int FMT>
 Launch pick_p(int P, bool append) {
   if constexpr (FMT == RKV_BF16) {
@@ -1502,7 +1506,7 @@ Launch pick_p(int P, bool append) {
       return make_launch<T, D, G, FMT, kWideP2 / kBS, kWideSplit>(append);
     }
   }
-  if constexpr (sizeof(T) != 1 && kSmallP < kP) {
+  if constexpr (kSmallP < part_of<T>()) {
     if (P <= kSmallP) return make_launch<T, D, G, FMT, kSmallP / kBS>(append);
   }
   return make_launch<T, D, G, FMT, part_of<T>() / kBS>(append);

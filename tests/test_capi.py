@@ -94,7 +94,7 @@ def test_workspace_size():
     # 1000 of those, 640 with work for >= 800 partitions of 512, else 512
     # (configs[2]: 768; configs[3] and 256 x 8192: 1280; configs[2]'s share
     # of one GPU of 8: 512; above the 512 tier, 8 heads per KV head, head_dim
-    # 64 and fp32 pools: 640; 1-byte pools: 640 always)
+    # 64, fp32 and 1-byte pools: 640)
     F = L.rkv_decode_partition_size_for
     assert F(0, 64, 32, 8, 128, RKV_BF16, 4096) == 768
     assert F(0, 8, 32, 8, 128, RKV_BF16, 65536) == 1280
@@ -104,8 +104,12 @@ def test_workspace_size():
     assert F(0, 8, 64, 8, 128, RKV_BF16, 4096) == 512     # small calls: every shape
     assert F(0, 8, 32, 8, 64, RKV_BF16, 4096) == 512
     assert F(0, 8, 32, 8, 128, RKV_F32, 4096) == 512
-    for dt in (RKV_I8, RKV_FP8):                          # 1-byte pools: one build
-        assert F(0, 8, 32, 8, 128, dt, 4096) == 640
+    for dt in (RKV_I8, RKV_FP8):  # 1-byte pools: 512 up to twice the work
+        assert F(0, 8, 32, 8, 128, dt, 4096) == 512
+        assert F(0, 32, 32, 8, 128, dt, 4096) == 512
+        assert F(0, 64, 32, 8, 128, dt, 4096) == 640
+        assert F(0, 1, 32, 8, 128, dt, 204800) == 640     # 8 * 102400 = 1600 x 512
+        assert F(0, 1, 32, 8, 128, dt, 204799) == 512
     assert F(0, 4, 32, 8, 128, RKV_BF16, 32768) == 640
     assert F(0, 64, 64, 8, 128, RKV_BF16, 4096) == 640    # G = 8
     assert F(0, 64, 32, 8, 64, RKV_BF16, 4096) == 640     # head_dim 64

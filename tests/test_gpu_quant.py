@@ -300,10 +300,11 @@ def test_decode_q_quantization_error_is_small(dev):
 
 
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
-@pytest.mark.parametrize("P", [128, 384])
+@pytest.mark.parametrize("P", [128, 384, 512, 576])
 def test_decode_q_caller_partition_sizes(dev, fmt, P):
-    """1-byte pools at requested partition sizes (the 640-token build with the
-    slots past the size masked), against the oracle on the dequantized pool."""
+    """1-byte pools at requested partition sizes (the smallest of the 512- and
+    640-token builds that holds the size, the slots past it masked), against
+    the oracle on the dequantized pool."""
     say(f"decode_q partition_size={P} fmt={fmt}")
     rng = np.random.default_rng(P)
     ctx = np.array([1, 100, 128, 129, 384, 385, 1000, 2500], np.int32)
